@@ -1,0 +1,94 @@
+/*
+ * mpserve_amd — MI355X (gfx950) FP8 + Huffman-sidecar weight path, C ABI.
+ *
+ * Plain pointers and sizes only. Every pointer named "device" is HIP device
+ * memory on the current device; host pointers are named so. All entry points
+ * return MPS_OK (0) or a negative MPS_ERR_* code; mps_last_error() gives the
+ * message of the last failure on the calling thread.
+ *
+ * Sidecar format: the one MPServe's builder writes
+ * (reference kernel/build_huffman.cu:292-969, scripts/compress_llm_fp8_huffman.py:284-306).
+ */
+#ifndef MPSERVE_AMD_H
+#define MPSERVE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MPS_OK 0
+#define MPS_ERR_INVALID_ARGUMENT (-1) /* maps to Python ValueError (std::invalid_argument in the reference) */
+#define MPS_ERR_RUNTIME (-2)          /* maps to Python RuntimeError */
+#define MPS_ERR_HIP (-3)              /* a HIP runtime call failed */
+#define MPS_ERR_NO_MEMORY (-4)
+
+/* Device-side integrity flags a decode records (see mps_fp8_read_status). */
+#define MPS_STATUS_BAD_BUCKET 0x1u   /* row range / column range outside the tensor */
+#define MPS_STATUS_BAD_ROW 0x2u      /* a row index outside [0, n) */
+#define MPS_STATUS_BAD_TABLE 0x4u    /* a bucket_table gid outside [-1, G) */
+#define MPS_STATUS_DESYNC 0x8u       /* a lane ended at a bit other than the next lane's start */
+
+/* One FP8 tensor and its sidecar, all device pointers, as stored by the
+ * reference's compress script (huff_* tensors) with the decode call's dtype
+ * views (reference scripts/mpserve_vllm_fp8_huffman.py:457-472). */
+typedef struct mps_fp8_tensor {
+  const uint8_t *fp8;                    /* [n*m]            huff_fp8_u8 */
+  const uint64_t *bitstream;             /* [bitstream_words] huff_bitstream_u64 */
+  int64_t bitstream_words;
+  const uint16_t *decode_syms;           /* [num_tables,128] huff_decode_syms_u16 */
+  const uint8_t *decode_lens;            /* [num_tables,64]  huff_decode_lens_u8 (packed 4-bit) */
+  int64_t num_tables;
+  const int32_t *bucket_table;           /* [num_buckets,256] fp8 byte -> table id or -1 */
+  const int32_t *bucket_col_start;       /* [num_buckets] */
+  const int32_t *bucket_col_len;         /* [num_buckets] */
+  const int32_t *bucket_row_offsets;     /* [num_buckets+1] into row_indices */
+  const int32_t *row_indices;            /* [num_row_indices] */
+  int64_t num_row_indices;
+  const uint32_t *bucket_thread_startbit;/* [num_buckets, k+1] lane start bits, relative */
+  const int64_t *bucket_bit_base;        /* [num_buckets+1] bucket base bits (64-aligned) */
+  int64_t num_buckets;
+  int64_t k;                             /* substreams (lanes) per bucket, 1..1024 */
+  int64_t n, m;                          /* output shape [n, m] */
+  uint16_t *out;                         /* [n*m] BF16 bit patterns (device) */
+} mps_fp8_tensor;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *mps_last_error(void);
+
+/* HIP clock rate (kHz) of `device`.
+ * Replaces MPServe_cuda.cuda_clock_rate_khz (reference kernel/wrapper.cpp:133-141). */
+int mps_clock_rate_khz(int device, int64_t *khz_out);
+
+/* Decode one tensor: out[n,m] = BF16 rebuilt from FP8 bytes + sidecar, on `stream`
+ * (a hipStream_t; NULL = the legacy default stream). Lossless: reads the raw
+ * 16 bits after ESC codes, and walks columns as e % col_len.
+ * Replaces huffman_cpp::huffman_decode_fp8_entry (reference kernel/decode_huffman.cu:591-758,
+ * bound as MPServe_cuda.huffman_decode_fp8 at kernel/wrapper.cpp:456-503); the
+ * shape/dtype checks of that entry are done by the caller, which knows dtypes.
+ * max_len must be 7. Asynchronous: returns after the launch. */
+int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
+
+/* Batched decode plan: one launch decodes many tensors (a layer, a model).
+ * The plan copies the descriptors to device memory it owns (synchronously, at
+ * create time); the pointed-to sidecars must stay alive while the plan is used.
+ * No counterpart in the reference, which launches once per tensor
+ * (kernel/decode_huffman.cu:739); it serves its apply() and model loading paths
+ * (scripts/mpserve_vllm_fp8_huffman.py:491-557). */
+typedef struct mps_fp8_plan mps_fp8_plan;
+int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_plan **plan_out);
+int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream);
+/* Launches of the plan's work list (for profiling tools): work items, bytes of LDS per workgroup. */
+int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes);
+int mps_fp8_plan_destroy(mps_fp8_plan *plan);
+
+/* Read and clear the MPS_STATUS_* flags the decodes on `device` recorded
+ * since the last call. Synchronises `stream` first. */
+int mps_fp8_read_status(int device, void *stream, uint32_t *status_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MPSERVE_AMD_H */

@@ -1,0 +1,235 @@
+"""The ``MPServe_cuda`` op surface, served by HIP kernels on MI355X.
+
+Same op names, argument names, defaults, dict keys and error types as the
+reference's pybind11 module (kernel/wrapper.cpp:132-504); the repository root
+module ``MPServe_cuda`` re-exports this one so ``import MPServe_cuda`` keeps
+working. Tensors cross into libmpserve_amd.so as raw device pointers.
+
+Every op runs on the GPU. There is no CPU fallback: without the native
+library the ops raise ImportError, and without a GPU they raise RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Dict
+
+import torch
+
+from . import _native
+
+__all__ = [
+    "huffman_build_fp8_decode_tables",
+    "huffman_decode_fp8",
+    "cuda_clock_rate_khz",
+    "SIDECAR_KEYS",
+]
+
+# Output keys of the build op, in the reference's tuple order (wrapper.cpp:429-446).
+SIDECAR_KEYS = (
+    "decode_syms_u16", "decode_lens_u8", "table_scale_u16", "table_fp8_u16",
+    "bucket_scale_u16", "bucket_row_offsets_i32", "row_indices_i32", "bucket_table_i32",
+    "bucket_col_start_i32", "bucket_col_len_i32", "bucket_thread_startbit_u32",
+    "bucket_bit_base_i64", "bitstream_u64", "shape_nmk_i64", "bucket_U_i32",
+    "bucket_unique_gid_i32", "bucket_fp8_uidx_i16",
+)
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_cuda_contig(t: torch.Tensor, name: str, device: torch.device | None) -> None:
+    # decode_huffman.cu:59-63
+    if t is None:
+        raise ValueError(f"{name} must be defined")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+
+
+def cuda_clock_rate_khz() -> int:
+    """Clock rate (kHz) of the current device (wrapper.cpp:133-141)."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("cudaGetDevice failed: no GPU device is visible")
+    v = ctypes.c_int64(0)
+    _native.check(_native.lib().mps_clock_rate_khz(torch.cuda.current_device(), ctypes.byref(v)))
+    return int(v.value)
+
+
+def _descriptor(fp8_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32,
+                bucket_col_start_i32, bucket_col_len_i32, bucket_row_offsets_i32, row_indices_i32,
+                bucket_thread_startbit_u32, bucket_bit_base_i64, n: int, m: int,
+                out: torch.Tensor) -> _native.MpsFp8Tensor:
+    d = _native.MpsFp8Tensor()
+    d.fp8 = fp8_u8.data_ptr()
+    d.bitstream = bitstream_u64.data_ptr()
+    d.bitstream_words = bitstream_u64.numel()
+    d.decode_syms = decode_syms_u16.data_ptr()
+    d.decode_lens = decode_lens_u8.data_ptr()
+    d.num_tables = decode_syms_u16.size(0)
+    d.bucket_table = bucket_table_i32.data_ptr()
+    d.bucket_col_start = bucket_col_start_i32.data_ptr()
+    d.bucket_col_len = bucket_col_len_i32.data_ptr()
+    d.bucket_row_offsets = bucket_row_offsets_i32.data_ptr()
+    d.row_indices = row_indices_i32.data_ptr()
+    d.num_row_indices = row_indices_i32.numel()
+    d.bucket_thread_startbit = bucket_thread_startbit_u32.data_ptr()
+    d.bucket_bit_base = bucket_bit_base_i64.data_ptr()
+    d.num_buckets = bucket_table_i32.size(0)
+    d.k = bucket_thread_startbit_u32.size(1) - 1
+    d.n = int(n)
+    d.m = int(m)
+    d.out = out.data_ptr()
+    return d
+
+
+def validate_decode_args(fp8_params_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32,
+                         bucket_col_start_i32, bucket_col_len_i32, bucket_row_offsets_i32, row_indices_i32,
+                         bucket_thread_startbit_u32, bucket_bit_base_i64, n, m, max_len) -> None:
+    """The argument checks of huffman_decode_fp8_entry (decode_huffman.cu:606-697), same messages."""
+    dev = fp8_params_u8.device if isinstance(fp8_params_u8, torch.Tensor) else None
+    named = (
+        (fp8_params_u8, "fp8_params_u8"), (bitstream_u64, "bitstream_u64"), (decode_syms_u16, "decode_syms_u16"),
+        (decode_lens_u8, "decode_lens_u8"), (bucket_table_i32, "bucket_table_i32"),
+        (bucket_col_start_i32, "bucket_col_start_i32"), (bucket_col_len_i32, "bucket_col_len_i32"),
+        (bucket_row_offsets_i32, "bucket_row_offsets_i32"), (row_indices_i32, "row_indices_i32"),
+        (bucket_thread_startbit_u32, "bucket_thread_startbit_u32"), (bucket_bit_base_i64, "bucket_bit_base_i64"),
+    )
+    for t, name in named:
+        _check_cuda_contig(t, name, dev)
+    if fp8_params_u8.dtype != torch.uint8:
+        raise ValueError("fp8_params_u8 must be uint8 CUDA")
+    if bitstream_u64.dtype != torch.uint64 or bitstream_u64.dim() != 1:
+        raise ValueError("bitstream_u64 must be uint64 1D CUDA")
+    if decode_syms_u16.dtype != torch.uint16 or decode_syms_u16.dim() != 2:
+        raise ValueError("decode_syms_u16 must be uint16 2D CUDA [G, 2^L]")
+    if decode_lens_u8.dtype != torch.uint8 or decode_lens_u8.dim() != 2:
+        raise ValueError("decode_lens_u8 must be uint8 2D CUDA [G, 2^(L-1)]")
+    if bucket_table_i32.dtype != torch.int32 or bucket_table_i32.dim() != 2 or bucket_table_i32.size(1) != 256:
+        raise ValueError("bucket_table_i32 must be int32 CUDA [B,256]")
+    if bucket_col_start_i32.dtype != torch.int32 or bucket_col_start_i32.dim() != 1:
+        raise ValueError("bucket_col_start_i32 must be int32 1D CUDA [B]")
+    if bucket_col_len_i32.dtype != torch.int32 or bucket_col_len_i32.dim() != 1:
+        raise ValueError("bucket_col_len_i32 must be int32 1D CUDA [B]")
+    if bucket_row_offsets_i32.dtype != torch.int32 or bucket_row_offsets_i32.dim() != 1:
+        raise ValueError("bucket_row_offsets_i32 must be int32 1D CUDA [B+1]")
+    if row_indices_i32.dtype != torch.int32 or row_indices_i32.dim() != 1:
+        raise ValueError("row_indices_i32 must be int32 1D CUDA")
+    if bucket_thread_startbit_u32.dtype != torch.uint32 or bucket_thread_startbit_u32.dim() != 2:
+        raise ValueError("bucket_thread_startbit_u32 must be uint32 2D CUDA [B,k+1]")
+    if bucket_bit_base_i64.dtype != torch.int64 or bucket_bit_base_i64.dim() != 1:
+        raise ValueError("bucket_bit_base_i64 must be int64 1D CUDA [B+1]")
+    if max_len <= 0 or max_len > 15:
+        raise ValueError("max_len must be in [1,15]")
+    if max_len != 7:
+        raise ValueError("decode kernel is specialized: max_len must be 7")
+    if n <= 0 or m <= 0:
+        raise ValueError("n,m must be > 0")
+    if fp8_params_u8.numel() != n * m:
+        raise ValueError("fp8_params_u8 numel must equal n*m")
+    B = bucket_table_i32.size(0)
+    if bucket_col_start_i32.numel() != B:
+        raise ValueError("bucket_col_start_i32 length must be B")
+    if bucket_col_len_i32.numel() != B:
+        raise ValueError("bucket_col_len_i32 length must be B")
+    if bucket_row_offsets_i32.numel() != B + 1:
+        raise ValueError("bucket_row_offsets_i32 length must be B+1")
+    if bucket_thread_startbit_u32.size(0) != B:
+        raise ValueError("bucket_thread_startbit_u32 first dim must be B")
+    if bucket_bit_base_i64.numel() != B + 1:
+        raise ValueError("bucket_bit_base_i64 length must be B+1")
+    if decode_syms_u16.size(1) != 128:
+        raise ValueError("decode_syms_u16 second dim must be 2^max_len")
+    if decode_lens_u8.size(1) != 64:
+        raise ValueError("decode_lens_u8 second dim must be 2^(max_len-1)")
+    if decode_syms_u16.size(0) != decode_lens_u8.size(0):
+        raise ValueError("decode_syms_u16 and decode_lens_u8 first dim must match")
+    k = bucket_thread_startbit_u32.size(1) - 1
+    if k <= 0 or k > 1024:
+        raise ValueError("bucket_thread_startbit_u32 has invalid k (must be 1..1024)")
+
+
+def read_status(device: torch.device | None = None) -> int:
+    """MPS_STATUS_* flags recorded by decodes on ``device`` since the last read (synchronises)."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    v = ctypes.c_uint32(0)
+    _native.check(_native.lib().mps_fp8_read_status(device.index or 0, ctypes.c_void_p(_stream_handle(device)),
+                                                    ctypes.byref(v)))
+    return int(v.value)
+
+
+def _maybe_check_status(device: torch.device) -> None:
+    if os.environ.get("MPSERVE_DECODE_CHECK", "0") == "1":
+        st = read_status(device)
+        if st:
+            raise RuntimeError(f"huffman_decode_fp8: sidecar integrity flags 0x{st:x} "
+                               "(1=bucket range, 2=row index, 4=table id, 8=lane bit desync)")
+
+
+def huffman_decode_fp8(fp8_params_u8: torch.Tensor, bitstream_u64: torch.Tensor, decode_syms_u16: torch.Tensor,
+                       decode_lens_u8: torch.Tensor, bucket_table_i32: torch.Tensor,
+                       bucket_col_start_i32: torch.Tensor, bucket_col_len_i32: torch.Tensor,
+                       bucket_row_offsets_i32: torch.Tensor, row_indices_i32: torch.Tensor,
+                       bucket_thread_startbit_u32: torch.Tensor, bucket_bit_base_i64: torch.Tensor,
+                       n: int, m: int, max_len: int = 12, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """BF16 ``[n, m]`` rebuilt from FP8 bytes + Huffman sidecar (wrapper.cpp:456-503).
+
+    Runs on the current stream of the FP8 tensor's device. ``out`` (keyword
+    only, not in the reference) decodes into a caller-owned contiguous BF16
+    buffer of n*m elements, e.g. a preallocated scratch weight.
+    """
+    n = int(n)
+    m = int(m)
+    max_len = int(max_len)
+    validate_decode_args(fp8_params_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32,
+                         bucket_col_start_i32, bucket_col_len_i32, bucket_row_offsets_i32, row_indices_i32,
+                         bucket_thread_startbit_u32, bucket_bit_base_i64, n, m, max_len)
+    dev = fp8_params_u8.device
+    if out is None:
+        out = torch.empty((n, m), dtype=torch.bfloat16, device=dev)
+    else:
+        if out.dtype != torch.bfloat16 or out.device != dev or not out.is_contiguous() or out.numel() != n * m:
+            raise ValueError("out must be a contiguous bfloat16 tensor of n*m elements on the fp8 device")
+    d = _descriptor(fp8_params_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32,
+                    bucket_col_start_i32, bucket_col_len_i32, bucket_row_offsets_i32, row_indices_i32,
+                    bucket_thread_startbit_u32, bucket_bit_base_i64, n, m, out)
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().mps_fp8_decode(ctypes.byref(d), max_len, ctypes.c_void_p(_stream_handle(dev))))
+    _maybe_check_status(dev)
+    return out
+
+
+def huffman_build_fp8_decode_tables(bf16_params: torch.Tensor, fp8_params: torch.Tensor, scales: torch.Tensor,
+                                    max_len: int = 12, threads_per_block: int = 256) -> Dict[str, torch.Tensor]:
+    """Build the Huffman sidecar on the GPU (build_huffman.cu:292-969, bound at wrapper.cpp:418-454).
+
+    Returns the reference's 17-key dict, byte-identical to its builder. CPU
+    inputs (the reference's contract) are copied to the current GPU and the
+    outputs come back as CPU tensors; CUDA inputs give CUDA outputs.
+    """
+    from .encode import build_fp8_sidecar
+
+    return build_fp8_sidecar(bf16_params, fp8_params, scales, int(max_len), int(threads_per_block))
+
+
+def _not_in_scope(name: str):
+    def f(*args, **kwargs):
+        raise NotImplementedError(f"MPServe_cuda.{name} is not provided by the MI355X build "
+                                  "(only the FP8 Huffman path is)")
+    f.__name__ = name
+    return f
+
+
+# Names the reference module binds (wrapper.cpp:142-179, :180-416) outside the FP8 path.
+for _name in ("init_cuda", "cleanup_cuda", "build_trie_AWQ", "build_trie", "query_trie", "free_trie",
+              "get_trie_count", "get_tot_path_length", "save_trie_collection", "load_trie_collection",
+              "save_trie_collection_awq", "load_trie_collection_awq", "load_bf16_from_int8", "dequantize_awq",
+              "build_trie_AWQ_to_FP8", "save_trie_collection_awq_to_fp8", "load_trie_collection_awq_to_fp8",
+              "huffman_build_awq_decode_tables", "huffman_decode_awq_shared_table",
+              "huffman_build_awq_int4_bucket_decode_tables", "huffman_build_awq_int4_bucket_decode_tables_by_scale",
+              "huffman_decode_awq_int4_bucket", "huffman_decode_awq_int4_bucket_by_scale"):
+    globals()[_name] = _not_in_scope(_name)

@@ -1,0 +1,211 @@
+"""HIP decode parity: MPServe_cuda.huffman_decode_fp8 vs the CPU oracle and the input weights.
+
+Integer path, so the bar is bit-exact equality of the BF16 bit patterns.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import decode_args, synth, to_torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _gpu_decode(sc, q):
+    import MPServe_cuda
+
+    sc_t = to_torch(sc, DEV)
+    q_t = torch.from_numpy(np.ascontiguousarray(q)).to(DEV)
+    out = MPServe_cuda.huffman_decode_fp8(*decode_args(sc_t, q_t))
+    torch.cuda.synchronize()
+    return out.view(torch.uint16).cpu().numpy()
+
+
+def _status():
+    from mpserve_amd.mpserve_cuda import read_status
+
+    return read_status(torch.device(DEV))
+
+
+@pytest.mark.parametrize("n,m,k,seed", [
+    (4096, 4096, 1024, 0),   # config 1 shape, compress default k
+    (1, 1, 1, 1),
+    (3, 5, 7, 2),
+    (7, 100, 1024, 3),       # col_len < k_eff: lanes wrap several rows per step
+    (64, 256, 64, 4),
+    (300, 513, 1024, 5),
+    (129, 1000, 256, 6),
+    (40, 3000, 1000, 7),
+    (1024, 4096, 1024, 8),   # k_proj / v_proj shape of the 8B layer
+    (256, 14336, 1024, 9),   # down_proj row length
+])
+def test_decode_roundtrip_per_row(n, m, k, seed):
+    bf, q, sc_u16 = synth(n, m, seed=seed)
+    sc = oracle.encode(bf, q, sc_u16, 7, k)
+    _status()
+    got = _gpu_decode(sc, q)
+    ref = oracle.decode(sc, q, n, m, 7, nthreads=8)
+    assert np.array_equal(ref, bf)
+    assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
+    assert _status() == 0
+
+
+def test_decode_scalar_scale_many_buckets():
+    n, m = 1000, 640
+    bf, q, sc_u16 = synth(n, m, seed=11)
+    sc = oracle.encode(bf, q, sc_u16[:1].copy(), 7, 512)
+    assert sc["bucket_table_i32"].shape[0] == 8  # ceil(1000/128) buckets of one scale
+    assert np.array_equal(_gpu_decode(sc, q), bf)
+
+
+def test_decode_block2d_scales():
+    n, m = 256, 384
+    bf, q, _ = synth(n, m, seed=12)
+    rng = np.random.default_rng(12)
+    scales = rng.integers(0x2000, 0x2010, size=(4, 3), dtype=np.uint16)  # 64x128 blocks
+    sc = oracle.encode(bf, q, scales, 7, 1024)
+    assert (sc["bucket_col_len_i32"] == 128).all() and sc["row_indices_i32"].size == n * 3
+    got = _gpu_decode(sc, q)
+    assert np.array_equal(got, bf)
+
+
+def _esc_inputs(n, m, seed, with_collision=False):
+    """One (scale, fp8) key carrying > 128 distinct BF16 symbols -> ESC codes."""
+    rng = np.random.default_rng(seed)
+    bf = rng.integers(0x3C00, 0x3C00 + 600, size=(n, m)).astype(np.uint16)
+    # a skewed head so that the kept set is well defined
+    head = rng.random((n, m)) < 0.5
+    bf[head] = (0x3C00 + rng.integers(0, 20, size=int(head.sum()))).astype(np.uint16)
+    if with_collision:
+        bf.flat[rng.choice(bf.size, 3, replace=False)] = 0  # esc_sym will be 0x0000
+    q = np.full((n, m), 0x38, dtype=np.uint8)
+    q[:, ::7] = 0x39  # a second, small key
+    return bf, q, np.array([0x1C00], dtype=np.uint16)
+
+
+def test_decode_esc_lossless():
+    n, m = 200, 512
+    bf, q, scales = _esc_inputs(n, m, 21)
+    sc, stats = oracle.encode(bf, q, scales, 7, 1024, with_stats=True)
+    assert stats["esc_keys"] >= 1 and stats["esc_elements"] > 0 and stats["esc_collisions"] == 0
+    got = _gpu_decode(sc, q)
+    assert np.array_equal(got, bf)
+    # the reference kernel ignores ESC (decode_huffman.cu:348-353): it loses those elements
+    ref_kernel = oracle.decode(sc, q, n, m, 7, mode=oracle.MODE_REFERENCE_KERNEL)
+    assert not np.array_equal(ref_kernel, bf)
+
+
+def test_decode_esc_collision_matches_oracle():
+    """esc_sym equal to a rare data symbol: the builder emits an ESC code without
+    raw bits (build_huffman.cu:850-864). Both decoders read 16 raw bits there;
+    the GPU must still agree with the oracle element for element."""
+    n, m = 120, 600
+    bf, q, scales = _esc_inputs(n, m, 22, with_collision=True)
+    sc, stats = oracle.encode(bf, q, scales, 7, 1024, with_stats=True)
+    assert stats["esc_collisions"] > 0
+    got = _gpu_decode(sc, q)
+    ref = oracle.decode(sc, q, n, m, 7)
+    assert np.array_equal(got, ref)
+    # the ambiguous code loses those elements (the lane usually re-synchronises
+    # within a few codes, so the lane-end check need not fire)
+    assert not np.array_equal(got, bf)
+    _status()
+
+
+def test_decode_reference_kernel_equivalence_on_wellformed():
+    """Where the reference kernel is well defined (no ESC, col_len >= k), the
+    lossless decode and the reference kernel's walk give the same output."""
+    n, m = 512, 2048
+    bf, q, sc_u16 = synth(n, m, seed=31)
+    sc = oracle.encode(bf, q, sc_u16, 7, 1024)
+    ref_kernel = oracle.decode(sc, q, n, m, 7, mode=oracle.MODE_REFERENCE_KERNEL)
+    assert np.array_equal(ref_kernel, bf)
+    assert np.array_equal(_gpu_decode(sc, q), ref_kernel)
+
+
+def test_decode_safetensors_dtype_views():
+    """Sidecar as stored by the compress script (int64/int16/int32 casts) and
+    viewed back the way apply() does (mpserve_vllm_fp8_huffman.py:457-472)."""
+    import MPServe_cuda
+
+    n, m = 333, 1024
+    bf, q, sc_u16 = synth(n, m, seed=41)
+    sc = oracle.encode(bf, q, sc_u16, 7, 1024)
+    st = to_torch(sc, DEV)
+    stored = {
+        "bitstream": st["bitstream_u64"].to(torch.int64), "syms": st["decode_syms_u16"].to(torch.int16),
+        "sb": st["bucket_thread_startbit_u32"].to(torch.int32),
+    }
+    q_t = torch.from_numpy(q).to(DEV)
+    out = MPServe_cuda.huffman_decode_fp8(
+        q_t, stored["bitstream"].view(torch.uint64), stored["syms"].view(torch.uint16), st["decode_lens_u8"],
+        st["bucket_table_i32"], st["bucket_col_start_i32"], st["bucket_col_len_i32"],
+        st["bucket_row_offsets_i32"], st["row_indices_i32"], stored["sb"].view(torch.uint32),
+        st["bucket_bit_base_i64"], n, m, 7)
+    assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf)
+
+
+def test_decode_on_side_stream_and_out_buffer():
+    import MPServe_cuda
+
+    n, m = 700, 2048
+    bf, q, sc_u16 = synth(n, m, seed=51)
+    sc_t = to_torch(oracle.encode(bf, q, sc_u16, 7, 1024), DEV)
+    q_t = torch.from_numpy(q).to(DEV)
+    side = torch.cuda.Stream()
+    buf = torch.full((n * m,), float("nan"), dtype=torch.bfloat16, device=DEV)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        MPServe_cuda.huffman_decode_fp8(*decode_args(sc_t, q_t), out=buf)
+    torch.cuda.current_stream().wait_stream(side)
+    assert np.array_equal(buf.view(torch.uint16).cpu().numpy().reshape(n, m), bf)
+
+
+def test_plan_decodes_many_tensors():
+    from mpserve_amd.decode import DecodePlan
+
+    shapes = [(256, 1024, 1024), (64, 4096, 1024), (300, 700, 512), (5, 9, 3)]
+    items, refs = [], []
+    for i, (n, m, k) in enumerate(shapes):
+        bf, q, sc_u16 = synth(n, m, seed=60 + i)
+        sc_t = to_torch(oracle.encode(bf, q, sc_u16, 7, k), DEV)
+        items.append((torch.from_numpy(q).to(DEV), sc_t))
+        refs.append(bf)
+    outs = [torch.empty((q.shape[0], q.shape[1]), dtype=torch.bfloat16, device=DEV) for q, _ in items]
+    plan = DecodePlan([(q, sc, o) for (q, sc), o in zip(items, outs)])
+    for _ in range(2):
+        plan.decode()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, refs):
+            assert np.array_equal(o.view(torch.uint16).cpu().numpy(), r)
+    assert _status() == 0
+
+
+def test_integrity_flags_on_corrupt_sidecar():
+    """Corrupt lane starts / row indices / table ids are flagged, never written out of bounds."""
+    import MPServe_cuda
+
+    n, m = 256, 1024
+    bf, q, sc_u16 = synth(n, m, seed=71)
+    sc = oracle.encode(bf, q, sc_u16, 7, 1024)
+    q_t = torch.from_numpy(q).to(DEV)
+    guard = torch.zeros(4096, dtype=torch.uint16, device=DEV)
+
+    bad = {k: v.copy() for k, v in sc.items()}
+    bad["bucket_thread_startbit_u32"][0, 5] += 3
+    out = MPServe_cuda.huffman_decode_fp8(*decode_args(to_torch(bad, DEV), q_t))
+    assert _status() & 0x8
+
+    bad = {k: v.copy() for k, v in sc.items()}
+    bad["row_indices_i32"][3] = n + 1000
+    MPServe_cuda.huffman_decode_fp8(*decode_args(to_torch(bad, DEV), q_t))
+    assert _status() & 0x2
+
+    bad = {k: v.copy() for k, v in sc.items()}
+    bad["bucket_table_i32"][0, 10] = 10 ** 8
+    MPServe_cuda.huffman_decode_fp8(*decode_args(to_torch(bad, DEV), q_t))
+    assert _status() & 0x4
+    assert int(guard.sum().item()) == 0 and out.shape == (n, m)

@@ -1,0 +1,71 @@
+"""Argument checks of the drop-in ops: same exception types and messages as the
+reference's entry points (decode_huffman.cu:606-697, build_huffman.cu:298-366)."""
+import numpy as np
+import pytest
+import torch
+
+import MPServe_cuda
+import oracle
+from tests.helpers import decode_args, synth, to_torch
+
+
+def _cpu_args():
+    bf, q, sc = synth(16, 64, seed=1)
+    s = to_torch(oracle.encode(bf, q, sc, 7, 32), "cpu")
+    return list(decode_args(s, torch.from_numpy(q)))
+
+
+def test_decode_rejects_cpu_tensors():
+    with pytest.raises(ValueError, match="fp8_params_u8 must be a CUDA tensor"):
+        MPServe_cuda.huffman_decode_fp8(*_cpu_args())
+
+
+def test_decode_default_max_len_is_12_and_rejected(monkeypatch):
+    # the reference binds max_len=12 by default (wrapper.cpp:502) and the kernel rejects it
+    import inspect
+
+    assert inspect.signature(MPServe_cuda.huffman_decode_fp8).parameters["max_len"].default == 12
+    assert inspect.signature(MPServe_cuda.huffman_build_fp8_decode_tables).parameters["max_len"].default == 12
+    assert inspect.signature(MPServe_cuda.huffman_build_fp8_decode_tables).parameters[
+        "threads_per_block"].default == 256
+
+
+def test_sidecar_keys_match_reference_order():
+    assert MPServe_cuda.SIDECAR_KEYS == (
+        "decode_syms_u16", "decode_lens_u8", "table_scale_u16", "table_fp8_u16", "bucket_scale_u16",
+        "bucket_row_offsets_i32", "row_indices_i32", "bucket_table_i32", "bucket_col_start_i32",
+        "bucket_col_len_i32", "bucket_thread_startbit_u32", "bucket_bit_base_i64", "bitstream_u64",
+        "shape_nmk_i64", "bucket_U_i32", "bucket_unique_gid_i32", "bucket_fp8_uidx_i16")
+
+
+def test_out_of_scope_ops_raise_not_implemented():
+    for name in ("dequantize_awq", "huffman_decode_awq_int4_bucket", "build_trie"):
+        with pytest.raises(NotImplementedError):
+            getattr(MPServe_cuda, name)()
+
+
+def test_decode_validation_messages_via_meta_checks(monkeypatch):
+    """Run the checks past the device test by faking is_cuda, to pin each message."""
+    from mpserve_amd import mpserve_cuda as mc
+
+    monkeypatch.setattr(mc, "_check_cuda_contig", lambda t, name, dev: None)
+    args = _cpu_args()
+    cases = [
+        (0, args[0].to(torch.int8), "fp8_params_u8 must be uint8 CUDA"),
+        (1, args[1].view(torch.int64), "bitstream_u64 must be uint64 1D CUDA"),
+        (2, args[2].view(torch.int16), r"decode_syms_u16 must be uint16 2D CUDA \[G, 2\^L\]"),
+        (4, args[4][:, :255].contiguous(), r"bucket_table_i32 must be int32 CUDA \[B,256\]"),
+        (9, args[9].view(torch.int32), r"bucket_thread_startbit_u32 must be uint32 2D CUDA \[B,k\+1\]"),
+        (13, 12, "decode kernel is specialized: max_len must be 7"),
+        (13, 0, r"max_len must be in \[1,15\]"),
+        (11, 0, "n,m must be > 0"),
+        (12, 63, "fp8_params_u8 numel must equal n\\*m"),
+        (5, args[5][:-1], "bucket_col_start_i32 length must be B"),
+        (7, args[7][:-1], r"bucket_row_offsets_i32 length must be B\+1"),
+    ]
+    for i, val, msg in cases:
+        a = list(args)
+        a[i] = val
+        with pytest.raises(ValueError, match=msg):
+            mc.validate_decode_args(*a)
+    mc.validate_decode_args(*args)
