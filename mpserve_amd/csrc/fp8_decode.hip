@@ -34,7 +34,7 @@ constexpr int kTable = 1 << kL;           // 128 entries per code table
 constexpr int kPacked = kTable / 2;       // 64 bytes of packed 4-bit lengths
 constexpr int kBlock = 1024;              // work-items per bucket workgroup (>= k)
 constexpr int kRowsLds = 256;             // row indices staged in LDS
-constexpr uint32_t kEscBit = 1u << 19;
+constexpr uint32_t kEscBit = 1u << 31;
 constexpr int kMaxDevices = 64;
 
 // Integrity flags go to a per-device status word passed to every launch.
@@ -57,9 +57,20 @@ struct WorkItem {
   int32_t bucket;
 };
 
-// One lane: decode its substream. Elements are processed in blocks of kDepth;
-// the FP8 bytes of block j+1 are loaded while block j decodes, so their memory
-// latency overlaps the table lookups instead of stalling each element.
+// One lane: decode its substream.
+//
+// Memory discipline (gfx9 counts loads and stores in one in-order vmcnt): all
+// global loads of a block of kDepth elements - the block's FP8 bytes and the
+// next two bitstream chunks - are issued together one block ahead, and no load
+// is issued inside the element loop. The wait at the top of a block is then a
+// static vmcnt(kDepth) (the previous block's stores may stay in flight) on
+// loads issued a whole block earlier.
+//
+// Bit supply: a 64-bit MSB-aligned buffer `buf` holding `cnt` bits, topped up
+// by 32 bits from a 4-chunk register queue whenever cnt < 32. Without ESC a
+// block consumes <= 7*kDepth = 56 bits, i.e. at most two chunks; the two
+// chunks staged per block keep the queue at >= 2 chunks at every block start.
+// ESC payloads can drain the queue; then a chunk is read directly (slow path).
 constexpr int kDepth = 8;
 
 template <typename Idx>
@@ -70,12 +81,16 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, const uint3
   const bool empty = T.bitstream_words <= 0;
   const uint32_t *__restrict__ bs32 = empty ? g_zero_chunks : reinterpret_cast<const uint32_t *>(T.bitstream);
   const uint64_t nchunks = empty ? 2u : (uint64_t)T.bitstream_words * 2u;
-  uint64_t c = pos0 >> 5;
+
+  // Initial fill: buffer from chunks c0, c0+1; queue = c0+2 .. c0+5; tail = c0+6.
+  const uint64_t cb = pos0 >> 5;
   const int skip = (int)(pos0 & 31u);
-  uint64_t buf = (((uint64_t)chunk_at(bs32, nchunks, c) << 32) | chunk_at(bs32, nchunks, c + 1)) << skip;
+  uint64_t buf = (((uint64_t)chunk_at(bs32, nchunks, cb) << 32) | chunk_at(bs32, nchunks, cb + 1)) << skip;
   int cnt = 64 - skip;
-  c += 2;
-  uint32_t nxt = chunk_at(bs32, nchunks, c);
+  uint32_t q0 = chunk_at(bs32, nchunks, cb + 2), q1 = chunk_at(bs32, nchunks, cb + 3);
+  uint32_t q2 = chunk_at(bs32, nchunks, cb + 4), q3 = chunk_at(bs32, nchunks, cb + 5);
+  int qn = 4;
+  uint64_t tail = cb + 6;  // index of the first chunk not yet in buf/queue
 
   // Element walk e = lane + i*k_eff -> (rr, cc) = (e / cl, e % cl), incrementally.
   int32_t rr = lane / cl;
@@ -83,72 +98,339 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, const uint3
   const int32_t dr = k_eff / cl;
   const int32_t dc = k_eff - dr * cl;
   const int32_t count = (int32_t)((total - lane + k_eff - 1) / k_eff);
-  const Idx m = (Idx)T.m;
   const int32_t last_row = (int32_t)((total - 1) / cl);
-  Idx rowbase = (Idx)s_rows[rr] * m + (Idx)c0;
-  auto step = [&]() -> Idx {
-    const Idx v = rowbase + (Idx)cc;
-    cc += dc;
-    rr += dr;
-    if (cc >= cl) {
-      cc -= cl;
-      rr += 1;
-    }
-    if (dr != 0 || cc < dc) rowbase = (Idx)s_rows[rr < last_row ? rr : last_row] * m + (Idx)c0;
-    return v;
-  };
+  const Idx m = (Idx)T.m;
   const uint8_t *__restrict__ fp8 = T.fp8;
   uint16_t *__restrict__ out = T.out;
 
-  Idx idx_cur[kDepth], idx_nxt[kDepth];
-  uint32_t q_cur[kDepth], q_nxt[kDepth];
-  const Idx first = rowbase + (Idx)cc;
-#pragma unroll
-  for (int j = 0; j < kDepth; ++j) {
-    idx_cur[j] = (j < count) ? step() : first;
-    q_cur[j] = fp8[idx_cur[j]];
-  }
-  for (int32_t i0 = 0; i0 < count; i0 += kDepth) {
+  // Addresses of the next kDepth elements (elements past `count` repeat the
+  // lane's first element, whose address is always valid).
+  const Idx first = (Idx)s_rows[rr] * m + (Idx)c0 + (Idx)cc;
+  int32_t walked = 0;
+  auto next_block = [&](Idx (&idx)[kDepth]) {
+    int32_t rrs[kDepth], ccs[kDepth];
 #pragma unroll
     for (int j = 0; j < kDepth; ++j) {
-      idx_nxt[j] = (i0 + kDepth + j < count) ? step() : first;
-      q_nxt[j] = fp8[idx_nxt[j]];
-    }
-#pragma unroll
-    for (int j = 0; j < kDepth; ++j) {
-      if (i0 + j < count) {
-        const uint32_t peek = (uint32_t)(buf >> (64 - kL));
-        const uint32_t ent = lut[(q_cur[j] << kL) | peek];
-        const int len = (int)((ent >> 16) & 7u);
-        buf <<= len;
-        cnt -= len;
-        uint32_t sym = ent & 0xFFFFu;
-        if (ent & kEscBit) {
-          sym = (uint32_t)(buf >> 48);
-          buf <<= 16;
-          cnt -= 16;
-        }
-        out[idx_cur[j]] = (uint16_t)sym;
-        if (cnt < 32) {
-          buf |= (uint64_t)nxt << (32 - cnt);
-          cnt += 32;
-          ++c;
-          nxt = chunk_at(bs32, nchunks, c);
-        }
+      rrs[j] = rr < last_row ? rr : last_row;
+      ccs[j] = cc;
+      cc += dc;
+      rr += dr;
+      if (cc >= cl) {
+        cc -= cl;
+        rr += 1;
       }
     }
 #pragma unroll
     for (int j = 0; j < kDepth; ++j) {
-      idx_cur[j] = idx_nxt[j];
-      q_cur[j] = q_nxt[j];
+      const Idx v = (Idx)s_rows[rrs[j]] * m + (Idx)c0 + (Idx)ccs[j];
+      idx[j] = (walked + j < count) ? v : first;
     }
+    walked += kDepth;
+  };
+
+  Idx ia[kDepth], ib[kDepth];
+  uint32_t qa[kDepth], qb[kDepth];
+  next_block(ia);
+#pragma unroll
+  for (int j = 0; j < kDepth; ++j) qa[j] = fp8[ia[j]];
+  uint32_t s0 = chunk_at(bs32, nchunks, tail), s1 = chunk_at(bs32, nchunks, tail + 1);
+  bool stale = false;  // the staged pair no longer starts at `tail`
+
+  // Each branch merges its own chunk into buf: a loaded value that both
+  // branches shared would force a full vmcnt wait on every element.
+  auto refill = [&]() {
+    if (cnt < 32) {
+      if (qn > 0) {
+        buf |= (uint64_t)q0 << (32 - cnt);
+        q0 = q1;
+        q1 = q2;
+        q2 = q3;
+        --qn;
+      } else {
+        // Queue drained by ESC payloads: read the chunk straight from memory.
+        const uint32_t ch = chunk_at(bs32, nchunks, tail);
+        buf |= (uint64_t)ch << (32 - cnt);
+        ++tail;
+        stale = true;
+      }
+      cnt += 32;
+    }
+  };
+  auto decode_one = [&](uint32_t q, Idx idx) {
+    const uint32_t peek = (uint32_t)(buf >> (64 - kL));
+    const uint32_t ent = lut[(q << kL) | peek];
+    const int len = (int)((ent >> 16) & 7u);
+    buf <<= len;
+    cnt -= len;
+    uint32_t sym = ent & 0xFFFFu;
+    if (ent & kEscBit) {
+      sym = (uint32_t)(buf >> 48);
+      buf <<= 16;
+      cnt -= 16;
+    }
+    out[idx] = (uint16_t)sym;
+    refill();
+  };
+  // One block: decode (qc, ic) while (qn_, in_) receive the next block's loads.
+  auto block = [&](int32_t i0, uint32_t (&qc)[kDepth], Idx (&ic)[kDepth], uint32_t (&qnx)[kDepth],
+                   Idx (&inx)[kDepth]) {
+    // Append the pair staged one block ago if it is current and fits.
+    if (!stale && qn <= 2) {
+      q0 = (qn == 0) ? s0 : q0;
+      q1 = (qn == 0) ? s1 : (qn == 1) ? s0 : q1;
+      q2 = (qn == 1) ? s1 : (qn == 2) ? s0 : q2;
+      q3 = (qn == 2) ? s1 : q3;
+      qn += 2;
+      tail += 2;
+    }
+    stale = false;
+    next_block(inx);
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) qnx[j] = fp8[inx[j]];
+    s0 = chunk_at(bs32, nchunks, tail);
+    s1 = chunk_at(bs32, nchunks, tail + 1);
+    if (i0 + kDepth <= count) {
+#pragma unroll
+      for (int j = 0; j < kDepth; ++j) decode_one(qc[j], ic[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kDepth; ++j)
+        if (i0 + j < count) decode_one(qc[j], ic[j]);
+    }
+  };
+  for (int32_t i0 = 0; i0 < count; i0 += 2 * kDepth) {
+    block(i0, qa, ia, qb, ib);
+    if (i0 + kDepth >= count) break;
+    block(i0 + kDepth, qb, ib, qa, ia);
   }
-  // The next unread bit must be where the next lane's substream begins.
-  if (c * 32u - (uint64_t)cnt != pos_end) flag(status, MPS_STATUS_DESYNC);
+  // The next unread bit must be where the next lane's substream begins:
+  // buf holds cnt bits and the queue qn chunks, all before chunk `tail`.
+  if (tail * 32u - (uint64_t)(cnt + 32 * qn) != pos_end) flag(status, MPS_STATUS_DESYNC);
+}
+
+// Buffer resource over [base, base + bytes): raw buffer loads past the end
+// return 0 and stores past the end are dropped (gfx9 V# with stride 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Fast path for buckets whose column range is a multiple of k_eff (every
+// Llama-shaped tensor with k = 1024) and that hold at most 128 rows (every
+// bucket the reference builder makes). Then lane t's i-th element lies in row
+// i / P, column c0 + t + (i % P) * k_eff with P = col_len / k_eff: row and
+// column phase are the same for every lane. The walk over elements lives in
+// scalar registers and enters the FP8 loads and BF16 stores as the buffer
+// soffset; the per-lane voffset is just the lane (x2 for BF16). Row offsets
+// sit one per lane in two VGPRs and are fetched with v_readlane.
+//
+// Memory pipeline (gfx9 keeps one in-order vmcnt for loads and stores):
+// elements go in blocks of kDepth; FP8 bytes of block b+3 are loaded while
+// block b decodes (4-slot register ring) and the next two bitstream chunks
+// are staged one block ahead. The loop body issues the same loads and stores
+// on every path: elements past the lane's last are phantoms whose offsets lie
+// beyond the buffers (reads give 0, stores are dropped by the hardware range
+// check).
+//
+// Bit supply: `buf` (64-bit, MSB-aligned) holds `cnt` bits; it is topped up
+// from a 4-chunk register queue once per kG = 4 elements (<= 28 bits without
+// ESC). The staged pair is appended at each block start when the queue has
+// room, which keeps >= 2 chunks queued at block starts and makes the queue
+// last a whole block of non-ESC codes. ESC codes (16 raw bits follow) are
+// handled on a branch only waves with an ESC lane take; if the payload leaves
+// too few queued bits for the rest of the block, the lane "parks": it records
+// its element index and bit position and moves its store offsets out of
+// range, keeps running the loop on garbage (nothing of it is stored), and
+// finishes in a plain loop at the end.
+constexpr int kG = 4;
+constexpr int kRing = 4;
+constexpr uint32_t kPast = 0x40000000u;  // offset beyond every fast-path buffer (2*n*m <= 2^30)
+
+__device__ __forceinline__ void decode_lane_rows(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+                                                 const int32_t *__restrict__ s_rows, uint32_t *s_sink,
+                                                 int32_t lane, int32_t k_eff,
+                                                 int32_t rows, int32_t c0, int32_t P, uint64_t pos0,
+                                                 uint64_t pos_end, uint32_t *status) {
+  const uint32_t nm = (uint32_t)(T.n * T.m);
+  const __amdgpu_buffer_rsrc_t r_fp8 = make_rsrc(T.fp8, nm);
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(T.out, 2u * nm);
+  const __amdgpu_buffer_rsrc_t r_bs =
+      make_rsrc(T.bitstream, T.bitstream_words > 0 ? (uint32_t)(T.bitstream_words * 8) : 0u);
+  auto chunk = [&](uint32_t c) -> uint32_t {  // stream chunk c = u32 at byte (c ^ 1) * 4
+    return __builtin_amdgcn_raw_buffer_load_b32(r_bs, (c ^ 1u) << 2, 0, 0);
+  };
+
+  const uint32_t m = (uint32_t)T.m;
+  const uint32_t cl = (uint32_t)(P * k_eff);
+  const int32_t count = rows * P;
+  const uint32_t vlane = (uint32_t)lane;
+  uint32_t vstore = 2u * (uint32_t)lane;  // + kPast once the lane parks
+  // Row offsets (row * m + c0) of the bucket's rows 0..63 and 64..127, one per lane.
+  const int wl = lane & 63;
+  const uint32_t rowoff_lo = wl < rows ? (uint32_t)s_rows[wl] * m + (uint32_t)c0 : 0u;
+  const uint32_t rowoff_hi = wl + 64 < rows ? (uint32_t)s_rows[wl + 64] * m + (uint32_t)c0 : 0u;
+  auto row_offset = [&](int32_t r) -> uint32_t {
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_lo, r & 63);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_hi, r & 63);
+    return r < 64 ? a : b;
+  };
+  // Uniform element walker: offset of the next element, then advance.
+  struct Walker {
+    int32_t r;
+    uint32_t col, rowoff;
+  };
+  auto walk = [&](Walker &w) -> uint32_t {
+    const uint32_t so = w.r < rows ? w.rowoff + w.col : kPast;
+    w.col += (uint32_t)k_eff;
+    if (w.col == cl) {
+      w.col = 0;
+      ++w.r;
+      w.rowoff = row_offset(w.r < rows ? w.r : rows - 1);
+    }
+    return so;
+  };
+  Walker wload{0, 0, row_offset(0)}, wstore{0, 0, row_offset(0)};
+
+  // Bit reader state.
+  const uint32_t cb = (uint32_t)(pos0 >> 5);
+  const int skip = (int)(pos0 & 31u);
+  uint64_t buf = (((uint64_t)chunk(cb) << 32) | chunk(cb + 1)) << skip;
+  int cnt = 64 - skip;
+  uint32_t q0 = chunk(cb + 2), q1 = chunk(cb + 3), q2 = chunk(cb + 4), q3 = chunk(cb + 5);
+  int qn = 4;
+  uint32_t tail = cb + 6;
+  auto bitpos = [&]() -> uint32_t { return tail * 32u - (uint32_t)cnt - 32u * (uint32_t)qn; };
+  // Parking state.
+  bool parked = false;
+  int32_t park_i = count;
+  uint32_t park_bit = 0;
+  bool stale = false;
+
+  auto pop = [&]() {
+    buf |= (uint64_t)q0 << (32 - cnt);
+    q0 = q1;
+    q1 = q2;
+    q2 = q3;
+    --qn;
+    cnt += 32;
+  };
+  auto park = [&](int32_t i, uint32_t bit) {
+    parked = true;
+    park_i = i;
+    park_bit = bit;
+    vstore = kPast + 2u * vlane;
+  };
+  auto decode_one = [&](int32_t i, uint32_t q) {
+    const uint32_t so = walk(wstore);
+    const uint32_t hi = (uint32_t)(buf >> 32);
+    const uint32_t ent = lut[(q << kL) | (hi >> (32 - kL))];
+    const int len = (int)((ent >> 16) & 7u);
+    buf <<= len;
+    cnt -= len;
+    uint32_t sym = ent;
+    const bool esc = (int32_t)ent < 0;
+    if (__builtin_amdgcn_ballot_w64(esc)) {
+      if (esc) {
+        // ESC: the symbol is the next 16 raw bits.
+        if (!parked && cnt + 32 * qn < 16) park(i, bitpos() + (uint32_t)len);
+        if (cnt < 16) pop();
+        sym = (uint32_t)(buf >> 48);
+        buf <<= 16;
+        cnt -= 16;
+        if (cnt < 32 && qn > 0) pop();
+        // Keep enough queued for the rest of the block (<= 7 codes of 7 bits).
+        if (!parked && (cnt < 32 || qn < 2)) park(i + 1, bitpos());
+      }
+    }
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sym, r_out, vstore, 2u * so, 0);
+  };
+
+  uint32_t qr[kRing][kDepth];
+  uint32_t s0, s1;
+  // L2 touch of the bitstream kTouch chunks ahead of the staged pair, so that
+  // the staged loads (one block of lead) hit L2. The touch is an LDS-DMA
+  // buffer load into a scratch sink: it writes no VGPR, so no wait in the
+  // loop ever depends on it.
+  constexpr uint32_t kTouch = 16;
+  auto touch = [&](uint32_t c) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r_bs, (__attribute__((address_space(3))) void *)s_sink, 4,
+                                             (c ^ 1u) << 2, 0, 0, 0);
+  };
+  // Prologue: blocks 0..kRing-2 in flight.
+#pragma unroll
+  for (int b = 0; b < kRing - 1; ++b)
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) qr[b][j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, vlane, walk(wload), 0);
+  s0 = chunk(tail);
+  s1 = chunk(tail + 1);
+#pragma unroll
+  for (int t = 0; t < kRing; ++t) touch(tail + kTouch - 8 + 2 * t);
+
+  uint32_t end_bit = 0;
+  auto ring = [&](int32_t i0, bool last) {
+#pragma unroll
+    for (int slot = 0; slot < kRing; ++slot) {
+      const int32_t b0 = i0 + slot * kDepth;
+      // 1. queue the pair staged one block ago, if it is current and fits
+      if (!stale && qn <= 2) {
+        q0 = (qn == 0) ? s0 : q0;
+        q1 = (qn == 0) ? s1 : (qn == 1) ? s0 : q1;
+        q2 = (qn == 1) ? s1 : (qn == 2) ? s0 : q2;
+        q3 = (qn == 2) ? s1 : q3;
+        qn += 2;
+        tail += 2;
+      }
+      stale = false;
+      // 2. stage the next pair, touch further ahead
+      s0 = chunk(tail);
+      s1 = chunk(tail + 1);
+      touch(tail + kTouch);
+      // 3. FP8 bytes of block + 3
+#pragma unroll
+      for (int j = 0; j < kDepth; ++j)
+        qr[(slot + kRing - 1) % kRing][j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, vlane, walk(wload), 0);
+      // 4. decode this block
+#pragma unroll
+      for (int j = 0; j < kDepth; ++j) {
+        if (last && b0 + j == count) end_bit = bitpos();
+        if (j % kG == 0 && cnt < 32) pop();
+        decode_one(b0 + j, qr[slot][j]);
+      }
+    }
+  };
+  constexpr int32_t kSpan = kRing * kDepth;
+  const int32_t last0 = ((count - 1) / kSpan) * kSpan;
+  for (int32_t i0 = 0; i0 < last0; i0 += kSpan) ring(i0, false);
+  ring(last0, true);
+  if (last0 + kSpan == count) end_bit = bitpos();
+
+  if (!parked || park_i >= count) {
+    if ((uint64_t)(parked ? park_bit : end_bit) != pos_end) flag(status, MPS_STATUS_DESYNC);
+    return;
+  }
+  // Parked lane: finish elements park_i.. with direct loads.
+  uint64_t pos = park_bit;
+  for (int32_t i = park_i; i < count; ++i) {
+    const int32_t r = i / P, p = i - r * P;
+    const uint32_t off = (uint32_t)s_rows[r] * m + (uint32_t)c0 + (uint32_t)(p * k_eff) + vlane;
+    const uint32_t q = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, off, 0, 0);
+    const uint32_t c = (uint32_t)(pos >> 5), sh = (uint32_t)(pos & 31u);
+    const uint64_t w = (((uint64_t)chunk(c) << 32) | chunk(c + 1)) << sh;  // >= 32 valid bits
+    const uint32_t ent = lut[(q << kL) | (uint32_t)(w >> (64 - kL))];
+    const int len = (int)((ent >> 16) & 7u);
+    pos += (uint32_t)len;
+    uint32_t sym = ent;
+    if ((int32_t)ent < 0) {
+      const uint32_t c2 = (uint32_t)(pos >> 5), sh2 = (uint32_t)(pos & 31u);
+      sym = (uint32_t)(((((uint64_t)chunk(c2) << 32) | chunk(c2 + 1)) << sh2) >> 48);
+      pos += 16;
+    }
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sym, r_out, 2u * off, 0, 0);
+  }
+  if (pos != pos_end) flag(status, MPS_STATUS_DESYNC);
 }
 
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b, uint32_t *lut, int32_t *s_gid,
-                                              int32_t *s_rows, int *s_bad, uint32_t *status) {
+                                              int32_t *s_rows, int *s_bad, uint32_t *s_sink, uint32_t *status) {
   const int tid = threadIdx.x;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(T.decode_syms) & 15u) == 0) &&
                       ((reinterpret_cast<uintptr_t>(T.decode_lens) & 3u) == 0);
@@ -226,7 +508,10 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   const uint64_t base = (uint64_t)T.bucket_bit_base[b];
   const uint64_t pos0 = base + sb[lane];
   const uint64_t pos_end = base + sb[lane + 1];
-  if ((uint64_t)T.n * (uint64_t)T.m <= 0xFFFFFFFFull)
+  const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
+  if (cl % k_eff == 0 && rows <= 128 && nm <= (1ull << 29) && (uint64_t)T.bitstream_words < 0x10000000ull)
+    decode_lane_rows(T, lut, s_rows, s_sink, lane, k_eff, rows, c0, cl / k_eff, pos0, pos_end, status);
+  else if (nm <= 0xFFFFFFFFull)
     decode_lane<uint32_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pos_end, status);
   else
     decode_lane<uint64_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pos_end, status);
@@ -237,7 +522,8 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
   __shared__ int32_t s_gid[256];
   __shared__ int32_t s_rows[kRowsLds];
   __shared__ int s_bad;
-  decode_bucket(T, blockIdx.x, lut, s_gid, s_rows, &s_bad, status);
+  __shared__ uint32_t s_sink[64];
+  decode_bucket(T, blockIdx.x, lut, s_gid, s_rows, &s_bad, s_sink, status);
 }
 
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
@@ -246,8 +532,9 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
   __shared__ int32_t s_gid[256];
   __shared__ int32_t s_rows[kRowsLds];
   __shared__ int s_bad;
+  __shared__ uint32_t s_sink[64];
   const WorkItem w = work[blockIdx.x];
-  decode_bucket(tensors[w.tensor], w.bucket, lut, s_gid, s_rows, &s_bad, status);
+  decode_bucket(tensors[w.tensor], w.bucket, lut, s_gid, s_rows, &s_bad, s_sink, status);
 }
 
 int check_tensor(const mps_fp8_tensor *t) {
