@@ -83,6 +83,45 @@ int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream);
 int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes);
 int mps_fp8_plan_destroy(mps_fp8_plan *plan);
 
+/* Inputs of the GPU sidecar builder, all device pointers: BF16 bit patterns
+ * and FP8 bytes of the same tensor (`numel` elements, shape dims[0..ndim)),
+ * and the u16 scale keys (shape scale_dims[0..scale_ndim), scale_numel
+ * values). */
+typedef struct mps_fp8_encode_in {
+  const uint16_t *bf16;
+  const uint8_t *fp8;
+  const uint16_t *scales;
+  int64_t numel;
+  int32_t ndim;
+  int32_t scale_ndim;
+  int64_t dims[8];
+  int64_t scale_dims[8];
+  int64_t scale_numel;
+  int64_t max_len;           /* 1..15 (decoding needs 7) */
+  int64_t threads_per_block; /* k: substreams per bucket, 1..1024 */
+} mps_fp8_encode_in;
+
+/* Build the Huffman sidecar of one tensor on the GPU, byte-identical to the
+ * reference builder. Replaces huffman_cpp::huffman_build_fp8_decode_tables_entry
+ * (reference kernel/build_huffman.cu:292-969, bound as
+ * MPServe_cuda.huffman_build_fp8_decode_tables at kernel/wrapper.cpp:418-454),
+ * which runs single-threaded on the host; same argument checks and messages.
+ * Synchronises `stream` (output sizes are data dependent). The result lives in
+ * device memory owned by the returned handle. */
+typedef struct mps_fp8_sidecar mps_fp8_sidecar;
+int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **out);
+/* Element counts of the 17 outputs, in the reference's order (kernel/wrapper.cpp:429-446):
+ * decode_syms_u16, decode_lens_u8, table_scale_u16, table_fp8_u16, bucket_scale_u16,
+ * bucket_row_offsets_i32, row_indices_i32, bucket_table_i32, bucket_col_start_i32,
+ * bucket_col_len_i32, bucket_thread_startbit_u32, bucket_bit_base_i64, bitstream_u64,
+ * shape_nmk_i64, bucket_U_i32, bucket_unique_gid_i32, bucket_fp8_uidx_i16. */
+int mps_fp8_sidecar_sizes(const mps_fp8_sidecar *sc, int64_t *sizes17);
+/* Copy the 17 outputs into caller buffers (host or device; hipMemcpyDefault); synchronises. */
+int mps_fp8_sidecar_copy(const mps_fp8_sidecar *sc, void *const *dst17, void *stream);
+/* {keys coded with ESC, elements equal to their key's esc_sym, distinct (key, symbol) pairs, hash slots}. */
+int mps_fp8_sidecar_stats(const mps_fp8_sidecar *sc, int64_t *stats4);
+int mps_fp8_sidecar_free(mps_fp8_sidecar *sc);
+
 /* Read and clear the MPS_STATUS_* flags the decodes on `device` recorded
  * since the last call. Synchronises `stream` first. */
 int mps_fp8_read_status(int device, void *stream, uint32_t *status_out);

@@ -1,0 +1,1179 @@
+// GPU sidecar builder for the FP8 + Huffman weight path (MI355X, gfx950).
+//
+// Produces byte for byte what the reference's host builder
+// huffman_build_fp8_decode_tables_entry (kernel/build_huffman.cu:292-969) produces:
+//   1. histogram of (scale, fp8) keys x BF16 symbols    (:392-401)   -> LDS-atomic pre-aggregation
+//                                                                        into a global open-addressing table
+//   2. keys in ascending order -> table id (gid)         (:403-412)   -> ballot/prefix-scan compaction,
+//                                                                        counting sort by key, scans
+//   3. per key: ESC selection, package-merge lengths,    (:445-578)   -> one work-item per key
+//      canonical codes in (count asc, sym asc) order,
+//      decode LUT and packed 4-bit lengths
+//   4. row buckets, bucket_table, U/uniq/uidx            (:582-783)   -> host (O(rows)) + one work-item
+//                                                                        per bucket
+//   5. per-lane bit counts, u32 lane starts, 64-bit      (:786-925)   -> two passes over the lanes with a
+//      aligned bucket bases, MSB-first packing                           scan between them; words shared by
+//                                                                        two lanes are merged with atomicOr
+// The reference is single-threaded; here every O(N) pass runs on the GPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "mps_common.h"
+
+namespace mps {
+namespace {
+
+constexpr uint64_t kEmpty = ~0ull;
+constexpr uint32_t kRaw = 1u << 31;  // code word flag: 16 raw symbol bits follow the code
+
+// Code word of one element: bits 0..15 code, 16..20 length, bit 31 raw16 follows.
+__device__ __forceinline__ uint32_t cw_len(uint32_t cw) { return (cw >> 16) & 0x1Fu; }
+
+__device__ __forceinline__ uint64_t hash64(uint64_t k) {
+  k ^= k >> 33;
+  k *= 0xff51afd7ed558ccdull;
+  k ^= k >> 33;
+  k *= 0xc4ceb9fe1a85ec53ull;
+  k ^= k >> 33;
+  return k;
+}
+
+// ---------------------------------------------------------------------------
+// Element addressing shared by the passes.
+// ---------------------------------------------------------------------------
+struct ScaleMap {
+  // mode 0: scalar/per-row (row_sidx[row]); mode 1: block-2D (block_sidx[br*nb1+bc])
+  int32_t mode;
+  const uint16_t *row_sidx;
+  const uint16_t *block_sidx;
+  int64_t sb0, sb1, nb1;
+};
+
+__device__ __forceinline__ uint32_t sidx_of(const ScaleMap &S, int64_t row, int64_t col) {
+  if (S.mode == 0) return S.row_sidx[row];
+  return S.block_sidx[(row / S.sb0) * S.nb1 + col / S.sb1];
+}
+
+// key40 = sidx << 24 | fp8 << 16 | sym
+__device__ __forceinline__ uint64_t key40(uint32_t sidx, uint32_t q, uint32_t sym) {
+  return ((uint64_t)sidx << 24) | ((uint64_t)q << 16) | (uint64_t)sym;
+}
+
+// ---------------------------------------------------------------------------
+// 1. Histogram
+// ---------------------------------------------------------------------------
+constexpr int kHistBlock = 256;
+constexpr int kLdsSlots = 2048;
+
+__device__ bool global_insert(uint64_t *keys, uint32_t *counts, uint64_t cap_mask, uint64_t k, uint32_t add) {
+  uint64_t h = hash64(k) & cap_mask;
+  for (uint64_t probe = 0; probe <= cap_mask; ++probe) {
+    unsigned long long *slot = reinterpret_cast<unsigned long long *>(keys + h);
+    unsigned long long cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cur == kEmpty) {
+      cur = atomicCAS(slot, (unsigned long long)kEmpty, (unsigned long long)k);
+      if (cur == kEmpty) cur = k;
+    }
+    if (cur == k) {
+      atomicAdd(counts + h, add);
+      return true;
+    }
+    h = (h + 1) & cap_mask;
+  }
+  return false;
+}
+
+__global__ __launch_bounds__(kHistBlock) void hist_kernel(const uint16_t *__restrict__ bf16, const uint8_t *__restrict__ fp8,
+                                                          int64_t n, int64_t m, ScaleMap S, int64_t elems_per_block,
+                                                          uint64_t *keys, uint32_t *counts, uint64_t cap_mask,
+                                                          uint32_t *overflow) {
+  __shared__ unsigned long long s_keys[kLdsSlots];
+  __shared__ uint32_t s_cnt[kLdsSlots];
+  for (int i = threadIdx.x; i < kLdsSlots; i += kHistBlock) {
+    s_keys[i] = kEmpty;
+    s_cnt[i] = 0;
+  }
+  __syncthreads();
+  const int64_t numel = n * m;
+  const int64_t e0 = (int64_t)blockIdx.x * elems_per_block;
+  const int64_t e1 = e0 + elems_per_block < numel ? e0 + elems_per_block : numel;
+  for (int64_t e = e0 + threadIdx.x; e < e1; e += kHistBlock) {
+    const int64_t row = e / m, col = e - row * m;
+    const uint64_t k = key40(sidx_of(S, row, col), fp8[e], bf16[e]);
+    // LDS first: a short probe, then the global table.
+    uint32_t h = (uint32_t)(hash64(k) & (kLdsSlots - 1));
+    bool done = false;
+    for (int probe = 0; probe < 16 && !done; ++probe) {
+      unsigned long long cur = s_keys[h];
+      if (cur == kEmpty) {
+        cur = atomicCAS(&s_keys[h], (unsigned long long)kEmpty, (unsigned long long)k);
+        if (cur == kEmpty) cur = k;
+      }
+      if (cur == k) {
+        atomicAdd(&s_cnt[h], 1u);
+        done = true;
+      }
+      h = (h + 1) & (kLdsSlots - 1);
+    }
+    if (!done && !global_insert(keys, counts, cap_mask, k, 1)) atomicOr(overflow, 1u);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kLdsSlots; i += kHistBlock) {
+    if (s_keys[i] != kEmpty && !global_insert(keys, counts, cap_mask, s_keys[i], s_cnt[i])) atomicOr(overflow, 1u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Compaction (ballot + prefix within the wave, one atomic per wave)
+// ---------------------------------------------------------------------------
+__global__ void compact_kernel(const uint64_t *__restrict__ keys, const uint32_t *__restrict__ counts, uint64_t cap,
+                               uint64_t *ckey, uint32_t *ccount, uint32_t *cslot, uint32_t *num) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = i < cap && keys[i] != kEmpty;
+  const uint64_t mask = __ballot(live);
+  const int lane = threadIdx.x & 63;
+  const uint32_t below = (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
+  uint32_t base = 0;
+  if (lane == 0 && mask) base = atomicAdd(num, (uint32_t)__popcll(mask));
+  base = __shfl(base, 0);
+  if (live) {
+    ckey[base + below] = keys[i];
+    ccount[base + below] = counts[i];
+    cslot[base + below] = (uint32_t)i;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic exclusive scan of u32 (two levels, up to 2^24 elements per level pair)
+// ---------------------------------------------------------------------------
+constexpr int kScanBlock = 1024;
+constexpr int kScanItems = 4;  // per thread
+constexpr int kScanTile = kScanBlock * kScanItems;
+
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s_tmp, uint32_t *total) {
+  // wave-level inclusive scan, then across waves
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) s_tmp[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    const int nw = blockDim.x >> 6;
+    uint32_t w = lane < nw ? s_tmp[lane] : 0u;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t y = __shfl_up(w, d);
+      if (lane >= d) w += y;
+    }
+    if (lane < nw) s_tmp[lane] = w;
+  }
+  __syncthreads();
+  const uint32_t before = wave > 0 ? s_tmp[wave - 1] : 0u;
+  if (total) *total = s_tmp[(blockDim.x >> 6) - 1];
+  __syncthreads();
+  return before + x - v;
+}
+
+__global__ __launch_bounds__(kScanBlock) void scan_tiles(const uint32_t *in, uint32_t *out, uint64_t n,
+                                                         uint32_t *tile_sums) {
+  __shared__ uint32_t s_tmp[16];
+  const uint64_t base = (uint64_t)blockIdx.x * kScanTile + (uint64_t)threadIdx.x * kScanItems;
+  uint32_t v[kScanItems], s = 0;
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) {
+    v[j] = base + j < n ? in[base + j] : 0u;
+    s += v[j];
+  }
+  uint32_t total = 0;
+  uint32_t ex = block_exclusive_scan(s, s_tmp, &total);
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) {
+    if (base + j < n) out[base + j] = ex;
+    ex += v[j];
+  }
+  if (threadIdx.x == 0 && tile_sums) tile_sums[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kScanBlock) void scan_add(uint32_t *out, uint64_t n, const uint32_t *tile_offsets) {
+  const uint64_t base = (uint64_t)blockIdx.x * kScanTile + (uint64_t)threadIdx.x * kScanItems;
+  const uint32_t add = tile_offsets[blockIdx.x];
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j)
+    if (base + j < n) out[base + j] += add;
+}
+
+// ---------------------------------------------------------------------------
+// Table grouping
+// ---------------------------------------------------------------------------
+__global__ void table_count_kernel(const uint64_t *ckey, uint32_t num, uint32_t *tcount) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < num) atomicAdd(tcount + (ckey[i] >> 16), 1u);
+}
+
+__global__ void nonzero_kernel(const uint32_t *tcount, uint64_t T, uint32_t *nz) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < T) nz[i] = tcount[i] ? 1u : 0u;
+}
+
+__global__ void scatter_kernel(const uint64_t *ckey, const uint32_t *ccount, const uint32_t *cslot, uint32_t num,
+                               const uint32_t *toff, uint32_t *tfill, uint16_t *seg_sym, uint32_t *seg_cnt,
+                               uint32_t *seg_slot) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= num) return;
+  const uint64_t tk = ckey[i] >> 16;
+  const uint32_t pos = toff[tk] + atomicAdd(tfill + tk, 1u);
+  seg_sym[pos] = (uint16_t)(ckey[i] & 0xFFFF);
+  seg_cnt[pos] = ccount[i];
+  seg_slot[pos] = cslot[i];
+}
+
+// gid -> table key, for the non-empty table keys in ascending order
+__global__ void table_list_kernel(const uint32_t *tcount, const uint32_t *tgid, uint64_t T, uint32_t *gid_tkey) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < T && tcount[i]) gid_tkey[tgid[i]] = (uint32_t)i;
+}
+
+// ---------------------------------------------------------------------------
+// 3. Code book of one key (one work-item per key)
+// ---------------------------------------------------------------------------
+// Items (count, sym) compare as the reference's std::pair<int, uint16_t>.
+__device__ __forceinline__ bool item_less(int32_t ca, uint32_t sa, int32_t cb, uint32_t sb) {
+  return ca != cb ? ca < cb : sa < sb;
+}
+
+// Leaf counts per level of the package-merge (build_huffman.cu:46-118), in the
+// equivalent form: with cur_0 = leaves and cur_j = merge(leaves, pairs of
+// cur_{j-1}) (leaf first on equal weight), the reference selects the first
+// 2(n-1) items of cur_{L-1} and, recursively, the first 2p items of cur_{j-1}
+// for the p packages selected in cur_j. A leaf's length is the number of
+// levels whose selected prefix contains it; leaves keep their sorted order in
+// every cur_j, so that prefix holds leaves 0..x_j-1. cur_j is rebuilt from
+// the leaves for each level (O(L^2 n) time, O(n) memory per key).
+__device__ void package_merge_lengths(const int32_t *w, int n, int L, int32_t *A, int32_t *Bv, uint8_t *Aleaf,
+                                      uint8_t *Bleaf, int32_t *lens) {
+  for (int i = 0; i < n; ++i) lens[i] = 0;
+  if (n == 1) {
+    lens[0] = 1;
+    return;
+  }
+  const int keep = 4 * (n - 1);
+  int c = 2 * (n - 1);  // selected prefix at the top level
+  for (int level = L - 1; level >= 0 && c > 0; --level) {
+    // build cur_level
+    int na = n < keep ? n : keep;
+    for (int i = 0; i < na; ++i) {
+      A[i] = w[i];
+      Aleaf[i] = 1;
+    }
+    for (int r = 0; r < level; ++r) {
+      const int t = na < keep ? na : keep;
+      // packages are pairs (0,1), (2,3), ... of A, in order (sorted, since A is sorted)
+      const int np = t / 2;
+      int a = 0, b = 0, o = 0;
+      while (o < keep && (a < n || b < np)) {
+        const bool take_leaf =
+            a < n && (b >= np || w[a] <= (int32_t)((uint32_t)A[2 * b] + (uint32_t)A[2 * b + 1]));
+        if (take_leaf) {
+          Bv[o] = w[a++];
+          Bleaf[o] = 1;
+        } else {
+          Bv[o] = (int32_t)((uint32_t)A[2 * b] + (uint32_t)A[2 * b + 1]);
+          ++b;
+          Bleaf[o] = 0;
+        }
+        ++o;
+      }
+      for (int i = 0; i < o; ++i) {
+        A[i] = Bv[i];
+        Aleaf[i] = Bleaf[i];
+      }
+      na = o;
+    }
+    // leaves among the first c items of cur_level
+    const int cc = c < na ? c : na;
+    int x = 0;
+    for (int i = 0; i < cc; ++i) x += Aleaf[i];
+    for (int i = 0; i < x; ++i) lens[i] += 1;
+    c = 2 * (cc - x);
+  }
+}
+
+struct CodebookArgs {
+  const uint32_t *gid_tkey;
+  const uint32_t *toff;
+  const uint32_t *tcount;
+  uint16_t *seg_sym;  // sorted in place
+  uint32_t *seg_cnt;
+  uint32_t *seg_slot;  // hash slot of each entry; sorted along with seg_sym/seg_cnt
+  int32_t *ws;        // 6 ints per segment entry + 2^(L+2) per key headroom
+  const uint32_t *ws_off;
+  const uint16_t *scale_values;  // sidx -> scale u16
+  uint32_t *cw_slot;             // hash slot -> code word
+  uint16_t *decode_syms;         // [G, 2^L]
+  uint8_t *decode_lens;          // [G, 2^(L-1)] (or [G,1] when L == 1)
+  uint16_t *table_scale;
+  uint16_t *table_fp8;
+  uint32_t G;
+  int L;
+  uint32_t *err;
+  uint32_t *esc_stats;  // [0] keys with ESC, [1] collisions (elements)
+};
+
+__global__ void codebook_kernel(CodebookArgs a) {
+  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= a.G) return;
+  const int L = a.L;
+  const uint32_t T = 1u << L;
+  const uint32_t tk = a.gid_tkey[g];
+  const uint32_t off = a.toff[tk];
+  const uint32_t ni = a.tcount[tk];
+  uint16_t *sym = a.seg_sym + off;
+  uint32_t *cnt = a.seg_cnt + off;
+  uint32_t *slot = a.seg_slot + off;
+  a.table_scale[g] = a.scale_values[tk >> 8];
+  a.table_fp8[g] = (uint16_t)(tk & 0xFF);
+  uint16_t *dsyms = a.decode_syms + (uint64_t)g * T;
+  uint8_t *dlens = a.decode_lens + (uint64_t)g * (T / 2 > 0 ? T / 2 : 1);
+
+  if (ni == 1) {
+    for (uint32_t j = 0; j < T; ++j) dsyms[j] = sym[0];
+    for (uint32_t j = 0; j < T / 2; ++j) dlens[j] = 0x11;  // len 1 in both nibbles
+    a.cw_slot[slot[0]] = (1u << 16) | 0u;
+    return;
+  }
+  // (count asc, sym asc); counts are compared as int like the reference's items
+  for (uint32_t i = 1; i < ni; ++i) {
+    const uint16_t s = sym[i];
+    const uint32_t c = cnt[i], h = slot[i];
+    int64_t j = (int64_t)i - 1;
+    while (j >= 0 && item_less((int32_t)c, s, (int32_t)cnt[j], sym[j])) {
+      sym[j + 1] = sym[j];
+      cnt[j + 1] = cnt[j];
+      slot[j + 1] = slot[j];
+      --j;
+    }
+    sym[j + 1] = s;
+    cnt[j + 1] = c;
+    slot[j + 1] = h;
+  }
+  // workspace of kWsPerItem ints per list item (see ws_size_kernel)
+  const uint32_t nmax = ni < T ? ni : T;
+  int32_t *ws = a.ws + a.ws_off[g];
+  int32_t *lw = ws;                 // weights of the coded list
+  int32_t *ls = ws + nmax;          // its symbols
+  int32_t *lens = ws + 2 * nmax;
+  int32_t *A = ws + 3 * nmax;       // two merge lists of <= 4 nmax items
+  int32_t *Bv = A + 4 * nmax;
+  uint8_t *Al = reinterpret_cast<uint8_t *>(Bv + 4 * nmax);
+  uint8_t *Bl = Al + 4 * nmax;
+  uint32_t nl = 0;
+  bool use_esc = false;
+  uint32_t esc_sym = 0;
+  if (ni > T) {
+    // ESC (build_huffman.cu:485-535): keep the 2^L-1 most frequent by (count
+    // desc, sym asc); ESC weight = sum of the rest; esc_sym = smallest u16 not kept.
+    use_esc = true;
+    const uint32_t keep = T - 1;
+    // the list is (count asc, sym asc): the kept items are the last `keep`
+    // in (count desc, sym asc) order, i.e. ties on count break toward the
+    // smaller symbol, which is the earlier one in this order. Select them by
+    // walking count groups from the top.
+    // Mark kept items in cnt's high bit-free copy: use lens[] as scratch flags over ni is not
+    // possible (ni > T), so select in place by moving kept items to the end.
+    uint32_t taken = 0;
+    int64_t i = (int64_t)ni - 1;
+    // walk groups of equal count from the largest count down
+    while (taken < keep && i >= 0) {
+      int64_t j = i;
+      while (j > 0 && cnt[j - 1] == cnt[i]) --j;
+      // group [j, i] has equal count, syms ascending; take from the smallest sym
+      const uint32_t gsize = (uint32_t)(i - j + 1);
+      const uint32_t take = gsize < keep - taken ? gsize : keep - taken;
+      for (uint32_t t = 0; t < take; ++t) {
+        lw[nl] = (int32_t)cnt[j + t];
+        ls[nl] = sym[j + t];
+        ++nl;
+      }
+      taken += take;
+      i = j - 1;
+    }
+    // ESC weight: total minus kept (int sums as in the reference)
+    uint32_t total = 0;
+    for (uint32_t t = 0; t < ni; ++t) total += cnt[t];
+    uint32_t kept_sum = 0;
+    for (uint32_t t = 0; t < nl; ++t) kept_sum += (uint32_t)lw[t];
+    const uint32_t esc_w = total - kept_sum;
+    // smallest u16 not among the kept: sort kept syms (insertion, <= 2^15 items)
+    for (uint32_t p = 1; p < nl; ++p) {
+      const int32_t v = ls[p], vw = lw[p];
+      int64_t q = (int64_t)p - 1;
+      while (q >= 0 && ls[q] > v) {
+        ls[q + 1] = ls[q];
+        lw[q + 1] = lw[q];
+        --q;
+      }
+      ls[q + 1] = v;
+      lw[q + 1] = vw;
+    }
+    uint32_t cand = 0;
+    for (uint32_t p = 0; p < nl; ++p) {
+      if ((uint32_t)ls[p] == cand) ++cand;
+      else if ((uint32_t)ls[p] > cand) break;
+    }
+    esc_sym = cand & 0xFFFF;
+    lw[nl] = (int32_t)esc_w;
+    ls[nl] = (int32_t)esc_sym;
+    ++nl;
+    // back to (count asc, sym asc)
+    for (uint32_t p = 1; p < nl; ++p) {
+      const int32_t v = ls[p], vw = lw[p];
+      int64_t q = (int64_t)p - 1;
+      while (q >= 0 && item_less(vw, (uint32_t)v, lw[q], (uint32_t)ls[q])) {
+        ls[q + 1] = ls[q];
+        lw[q + 1] = lw[q];
+        --q;
+      }
+      ls[q + 1] = v;
+      lw[q + 1] = vw;
+    }
+    atomicAdd(&a.esc_stats[0], 1u);
+  } else {
+    for (uint32_t t = 0; t < ni; ++t) {
+      lw[t] = (int32_t)cnt[t];
+      ls[t] = sym[t];
+    }
+    nl = ni;
+  }
+  // weights are ascending (as int); package-merge expects that order
+  package_merge_lengths(lw, (int)nl, L, A, Bv, Al, Bl, lens);
+  // canonical codes (build_huffman.cu:171-203), handed out in list order
+  uint32_t bl_count[16], next_code[16];
+  for (int b = 0; b < 16; ++b) bl_count[b] = 0;
+  for (uint32_t t = 0; t < nl; ++t) {
+    if (lens[t] <= 0 || lens[t] > L) {
+      atomicOr(a.err, 2u);
+      return;
+    }
+    bl_count[lens[t]]++;
+  }
+  uint32_t code = 0;
+  next_code[0] = 0;
+  for (int b = 1; b < 16; ++b) {
+    code = (code + bl_count[b - 1]) << 1;
+    next_code[b] = code;
+  }
+  for (uint32_t j = 0; j < T; ++j) dsyms[j] = 0;
+  for (uint32_t j = 0; j < T / 2; ++j) dlens[j] = 0;
+  uint32_t esc_cw = 0;
+  for (uint32_t t = 0; t < nl; ++t) {
+    const int len = lens[t];
+    const uint32_t c = next_code[len]++;
+    const uint32_t fill = 1u << (L - len);
+    const uint32_t base = c << (L - len);
+    const bool is_esc = use_esc && (uint32_t)ls[t] == esc_sym;
+    const uint32_t nib = is_esc ? ((uint32_t)len | 0x8u) : (uint32_t)len;
+    for (uint32_t f = 0; f < fill; ++f) {
+      const uint32_t e = base + f;
+      dsyms[e] = (uint16_t)ls[t];
+      if (T >= 2) dlens[e >> 1] |= (uint8_t)((nib & 0xF) << ((e & 1) * 4));
+    }
+    const uint32_t cw = ((uint32_t)len << 16) | (c & 0xFFFF);
+    if (is_esc) esc_cw = cw;
+  }
+  // code word of every histogram entry of this key
+  for (uint32_t t = 0; t < ni; ++t) {
+    const uint32_t s = sym[t];
+    // find s in the coded list (ls is sorted by (count, sym): linear scan)
+    uint32_t cw = 0;
+    bool found = false;
+    for (uint32_t p = 0; p < nl; ++p) {
+      if ((uint32_t)ls[p] == s) {
+        // recompute this item's code: codes were handed out in list order, so
+        // walk again per length (cheap: nl <= 2^L)
+        found = true;
+        uint32_t nc[16];
+        uint32_t cd = 0;
+        nc[0] = 0;
+        for (int b = 1; b < 16; ++b) {
+          cd = (cd + bl_count[b - 1]) << 1;
+          nc[b] = cd;
+        }
+        for (uint32_t r = 0; r <= p; ++r) {
+          const uint32_t cr = nc[lens[r]]++;
+          if (r == p) cw = ((uint32_t)lens[r] << 16) | (cr & 0xFFFF);
+        }
+        break;
+      }
+    }
+    if (!found) {
+      cw = esc_cw | kRaw;  // outside the map: ESC code + raw16
+    } else if (use_esc && s == esc_sym) {
+      atomicAdd(&a.esc_stats[1], cnt[t]);  // data symbol equal to esc_sym: ESC code, no raw bits
+    }
+    a.cw_slot[slot[t]] = cw;
+  }
+}
+
+constexpr uint32_t kWsPerItem = 13;  // 3 list arrays + 2 x 4 merge ints + 2 x 4 merge bytes
+
+__global__ void ws_size_kernel(const uint32_t *gid_tkey, const uint32_t *tcount, uint32_t G, uint32_t T,
+                               uint32_t *sz) {
+  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  const uint32_t ni = tcount[gid_tkey[g]];
+  sz[g] = kWsPerItem * (ni < T ? ni : T) + 4;
+}
+
+// ---------------------------------------------------------------------------
+// 4. bucket_table, U / unique gids / fp8 -> uidx (one work-item per bucket)
+// ---------------------------------------------------------------------------
+__global__ void bucket_table_kernel(const uint16_t *bucket_sidx, uint32_t B, const uint32_t *tcount,
+                                    const uint32_t *tgid, int32_t *btab, int32_t *bU, int32_t *uniq, int16_t *uidx) {
+  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const uint64_t t0 = (uint64_t)bucket_sidx[b] * 256;
+  int32_t U = 0;
+  for (int c = 0; c < 256; ++c) {
+    const int32_t gid = tcount[t0 + c] ? (int32_t)tgid[t0 + c] : -1;
+    btab[b * 256 + c] = gid;
+    uniq[b * 256 + c] = -1;
+    uidx[b * 256 + c] = -1;
+  }
+  // gids of one bucket are distinct (one scale, distinct fp8 bytes): first-appearance order is fp8 order
+  for (int c = 0; c < 256; ++c) {
+    const int32_t gid = btab[b * 256 + c];
+    if (gid < 0) continue;
+    uniq[b * 256 + U] = gid;
+    uidx[b * 256 + c] = (int16_t)U;
+    ++U;
+  }
+  bU[b] = U;
+}
+
+// ---------------------------------------------------------------------------
+// 5. Bitstream
+// ---------------------------------------------------------------------------
+struct LaneArgs {
+  const uint16_t *bf16;
+  const uint8_t *fp8;
+  ScaleMap S;
+  int64_t m;
+  const int32_t *row_offsets;
+  const int32_t *row_indices;
+  const int32_t *col_start;
+  const int32_t *col_len;
+  const uint32_t *lane_base;  // [B+1] cumulative k_eff
+  uint32_t B;
+  int64_t k;
+  const uint64_t *keys;
+  const uint32_t *cw_slot;
+  uint64_t cap_mask;
+  uint32_t *cw_elem;    // [numel]
+  uint32_t *lane_bits;  // [B, k+1] (count of lane t at [b][t+1])
+  uint32_t *err;
+};
+
+__device__ __forceinline__ uint32_t find_bucket(const uint32_t *lane_base, uint32_t B, uint32_t g) {
+  uint32_t lo = 0, hi = B;  // largest b with lane_base[b] <= g
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (lane_base[mid] <= g) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+__global__ void lane_bits_kernel(LaneArgs a) {
+  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= a.lane_base[a.B]) return;
+  const uint32_t b = find_bucket(a.lane_base, a.B, g);
+  const uint32_t t = g - a.lane_base[b];
+  const int32_t ra = a.row_offsets[b], rows = a.row_offsets[b + 1] - ra;
+  const int32_t c0 = a.col_start[b], cl = a.col_len[b];
+  const int64_t total = (int64_t)rows * cl;
+  const int64_t k_eff = a.lane_base[b + 1] - a.lane_base[b];
+  uint64_t bits = 0;
+  for (int64_t e = t; e < total; e += k_eff) {
+    const int64_t rr = e / cl, cc = e - rr * cl;
+    const int64_t row = a.row_indices[ra + rr];
+    const int64_t col = c0 + cc;
+    const int64_t idx = row * a.m + col;
+    const uint64_t k = key40(sidx_of(a.S, row, col), a.fp8[idx], a.bf16[idx]);
+    uint64_t h = hash64(k) & a.cap_mask;
+    while (a.keys[h] != k) {
+      if (a.keys[h] == kEmpty) {
+        atomicOr(a.err, 4u);
+        return;
+      }
+      h = (h + 1) & a.cap_mask;
+    }
+    const uint32_t cw = a.cw_slot[h];
+    a.cw_elem[idx] = cw;
+    bits += cw_len(cw) + ((cw & kRaw) ? 16u : 0u);
+  }
+  a.lane_bits[(uint64_t)b * (a.k + 1) + t + 1] = (uint32_t)bits;
+}
+
+// per bucket: inclusive scan of lane bits -> u32 starts; inactive lanes -> starts[k_eff]
+__global__ __launch_bounds__(1024) void lane_starts_kernel(uint32_t *startbit, const uint32_t *lane_base, int64_t k,
+                                                           uint32_t *bucket_bits) {
+  __shared__ uint32_t s_tmp[16];
+  const uint32_t b = blockIdx.x;
+  const int64_t k_eff = lane_base[b + 1] - lane_base[b];
+  uint32_t *sb = startbit + (uint64_t)b * (k + 1);
+  const int t = threadIdx.x;
+  const uint32_t v = t < k_eff ? sb[t + 1] : 0u;
+  uint32_t total = 0;
+  const uint32_t ex = block_exclusive_scan(v, s_tmp, &total);
+  __syncthreads();
+  if (t == 0) sb[0] = 0;
+  if (t < k) sb[t + 1] = t < k_eff ? ex + v : total;
+  if (t == 0) bucket_bits[b] = total;
+}
+
+struct PackArgs {
+  const uint16_t *bf16;
+  int64_t m;
+  const int32_t *row_offsets;
+  const int32_t *row_indices;
+  const int32_t *col_start;
+  const int32_t *col_len;
+  const uint32_t *lane_base;
+  uint32_t B;
+  int64_t k;
+  const uint32_t *cw_elem;
+  const uint32_t *startbit;
+  const int64_t *bit_base;
+  unsigned long long *bits;  // zeroed
+};
+
+__device__ __forceinline__ void flush_word(unsigned long long *bits, uint64_t w, uint64_t v, uint64_t first_w,
+                                           uint64_t last_w) {
+  if (v == 0) return;
+  if (w == first_w || w == last_w) atomicOr(bits + w, (unsigned long long)v);
+  else bits[w] = v;
+}
+
+__global__ void pack_kernel(PackArgs a) {
+  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= a.lane_base[a.B]) return;
+  const uint32_t b = find_bucket(a.lane_base, a.B, g);
+  const uint32_t t = g - a.lane_base[b];
+  const int32_t ra = a.row_offsets[b], rows = a.row_offsets[b + 1] - ra;
+  const int32_t c0 = a.col_start[b], cl = a.col_len[b];
+  const int64_t total = (int64_t)rows * cl;
+  const int64_t k_eff = a.lane_base[b + 1] - a.lane_base[b];
+  const uint32_t *sb = a.startbit + (uint64_t)b * (a.k + 1);
+  const uint64_t p0 = (uint64_t)a.bit_base[b] + sb[t];
+  const uint64_t p1 = (uint64_t)a.bit_base[b] + sb[t + 1];
+  if (p1 == p0) return;
+  const uint64_t first_w = p0 >> 6, last_w = (p1 - 1) >> 6;
+  uint64_t w = first_w;
+  uint64_t acc = 0;          // current word, MSB-first
+  uint32_t used = (uint32_t)(p0 & 63);  // bits of the current word already taken by earlier lanes
+  auto put = [&](uint32_t v, uint32_t n) {  // append the low n bits of v
+    while (n > 0) {
+      const uint32_t room = 64 - used;
+      const uint32_t take = n < room ? n : room;
+      const uint64_t part = (uint64_t)((v >> (n - take)) & ((take == 32) ? 0xFFFFFFFFu : ((1u << take) - 1u)));
+      acc |= part << (room - take);
+      used += take;
+      n -= take;
+      if (used == 64) {
+        flush_word(a.bits, w, acc, first_w, last_w);
+        ++w;
+        acc = 0;
+        used = 0;
+      }
+    }
+  };
+  for (int64_t e = t; e < total; e += k_eff) {
+    const int64_t rr = e / cl, cc = e - rr * cl;
+    const int64_t idx = (int64_t)a.row_indices[ra + rr] * a.m + c0 + cc;
+    const uint32_t cw = a.cw_elem[idx];
+    put(cw & 0xFFFF, cw_len(cw));
+    if (cw & kRaw) put(a.bf16[idx], 16);
+  }
+  if (used > 0) flush_word(a.bits, w, acc, first_w, last_w);
+}
+
+// ---------------------------------------------------------------------------
+// Host orchestration
+// ---------------------------------------------------------------------------
+template <typename T>
+struct DevBuf {
+  T *p = nullptr;
+  size_t n = 0;
+  ~DevBuf() { reset(); }
+  void reset() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  hipError_t alloc(size_t count) {
+    reset();
+    n = count;
+    return hipMalloc(&p, sizeof(T) * (count > 0 ? count : 1));
+  }
+};
+
+hipError_t device_scan(const uint32_t *in, uint32_t *out, uint64_t n, hipStream_t s, uint32_t *total_out) {
+  // exclusive scan; total (sum of all) written to host *total_out when non-null (synchronises)
+  if (n == 0) {
+    if (total_out) *total_out = 0;
+    return hipSuccess;
+  }
+  const uint64_t tiles = (n + kScanTile - 1) / kScanTile;
+  DevBuf<uint32_t> sums, sums_ex;
+  hipError_t e = sums.alloc(tiles + 1);
+  if (e != hipSuccess) return e;
+  if ((e = sums_ex.alloc(tiles + 1)) != hipSuccess) return e;
+  hipLaunchKernelGGL(scan_tiles, dim3((unsigned)tiles), dim3(kScanBlock), 0, s, in, out, n, sums.p);
+  if (tiles > 1) {
+    if ((e = device_scan(sums.p, sums_ex.p, tiles, s, nullptr)) != hipSuccess) return e;
+    hipLaunchKernelGGL(scan_add, dim3((unsigned)tiles), dim3(kScanBlock), 0, s, out, n, sums_ex.p);
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (total_out) {
+    uint32_t last_in = 0, last_out = 0;
+    if ((e = hipMemcpyAsync(&last_in, in + n - 1, 4, hipMemcpyDeviceToHost, s)) != hipSuccess) return e;
+    if ((e = hipMemcpyAsync(&last_out, out + n - 1, 4, hipMemcpyDeviceToHost, s)) != hipSuccess) return e;
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+    *total_out = last_in + last_out;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+}  // namespace mps
+
+using namespace mps;
+
+// Result object: device arrays in the reference's 17-output order.
+struct mps_fp8_sidecar {
+  DevBuf<uint16_t> decode_syms, table_scale, table_fp8, bucket_scale;
+  DevBuf<uint8_t> decode_lens;
+  DevBuf<int32_t> bucket_row_offsets, row_indices, bucket_table, bucket_col_start, bucket_col_len, bucket_U,
+      bucket_unique_gid;
+  DevBuf<uint32_t> bucket_thread_startbit;
+  DevBuf<int64_t> bucket_bit_base, shape_nmk;
+  DevBuf<uint64_t> bitstream;
+  DevBuf<int16_t> bucket_fp8_uidx;
+  int64_t sizes[17] = {};
+  int64_t stats[4] = {};  // esc keys, esc collision elements, distinct (key, symbol) pairs, hash capacity
+};
+
+extern "C" {
+
+int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **out) {
+  last_error().clear();
+  if (!in || !out) return fail(MPS_ERR_INVALID_ARGUMENT, "inputs must be defined");
+  *out = nullptr;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t L = in->max_len, kth = in->threads_per_block;
+  if (L <= 0 || L > 15) return fail(MPS_ERR_INVALID_ARGUMENT, "max_len must be in [1, 15]");
+  if (kth <= 0 || kth > 1024) return fail(MPS_ERR_INVALID_ARGUMENT, "threads_per_block must be in [1, 1024]");
+  const int64_t numel = in->numel;
+  if (in->ndim < 0 || in->ndim > 8 || in->scale_ndim < 0 || in->scale_ndim > 8)
+    return fail(MPS_ERR_INVALID_ARGUMENT, "too many dimensions");
+  // scale modes (build_huffman.cu:325-366)
+  const int64_t scale_numel = in->scale_numel;
+  const bool scale_scalar = scale_numel == 1;
+  const bool scale_per_elem = scale_numel == numel;
+  bool scale_per_row = false, scale_block2d = false;
+  int64_t n_rows = -1, n_cols = -1, sb0 = -1, sb1 = -1, nb0 = -1, nb1 = -1;
+  if (!scale_scalar && !scale_per_elem && in->ndim == 2) {
+    n_rows = in->dims[0];
+    n_cols = in->dims[1];
+    scale_per_row = scale_numel == n_rows;
+    if (!scale_per_row && in->scale_ndim == 2) {
+      nb0 = in->scale_dims[0];
+      nb1 = in->scale_dims[1];
+      if (nb0 > 0 && nb1 > 0 && n_rows % nb0 == 0 && n_cols % nb1 == 0) {
+        sb0 = n_rows / nb0;
+        sb1 = n_cols / nb1;
+        if (sb0 > 0 && sb1 > 0) scale_block2d = true;
+      }
+    }
+  }
+  if (!scale_scalar && !scale_per_elem && !scale_per_row && !scale_block2d)
+    return fail(MPS_ERR_INVALID_ARGUMENT,
+                "unsupported scales shape: use scalar, per-row (n,), per-element (numel), or 2D block-wise "
+                "[n/bs0,m/bs1]");
+  // The reference builds the tables before it checks the bucket layout; the
+  // checks below raise the same errors without the wasted work.
+  if (in->ndim != 2) return fail(MPS_ERR_INVALID_ARGUMENT, "bucket packing requires bf16_params to be 2D [n,m]");
+  const int64_t n = in->dims[0], m = in->dims[1];
+  if (n <= 0 || m <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "bf16_params shape must be non-empty");
+  if (!scale_block2d && !(scale_scalar || (!scale_per_elem && scale_per_row)))
+    return fail(MPS_ERR_INVALID_ARGUMENT,
+                "bucket packing requires scales to be scalar, per-row (n,), or 2D block-wise");
+  if (numel != n * m) return fail(MPS_ERR_INVALID_ARGUMENT, "bf16_params and fp8_params must have same numel");
+  if (numel >= (int64_t)1 << 32) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor too large for the GPU builder");
+
+  hipError_t e;
+#define HC(x)                                                   \
+  do {                                                          \
+    if ((e = (x)) != hipSuccess) return hip_fail(e, #x);        \
+  } while (0)
+
+  // --- scales to host, dense scale index (sorted unique values) ---
+  std::vector<uint16_t> hsc((size_t)scale_numel);
+  HC(hipMemcpyAsync(hsc.data(), in->scales, sizeof(uint16_t) * scale_numel, hipMemcpyDeviceToHost, s));
+  HC(hipStreamSynchronize(s));
+  std::vector<uint16_t> uniq_sc(hsc);
+  std::sort(uniq_sc.begin(), uniq_sc.end());
+  uniq_sc.erase(std::unique(uniq_sc.begin(), uniq_sc.end()), uniq_sc.end());
+  const uint32_t S = (uint32_t)uniq_sc.size();
+  auto sidx_of_value = [&](uint16_t v) -> uint16_t {
+    return (uint16_t)(std::lower_bound(uniq_sc.begin(), uniq_sc.end(), v) - uniq_sc.begin());
+  };
+
+  // --- buckets (build_huffman.cu:611-696), host ---
+  std::vector<int32_t> row_indices, row_offsets{0}, col_start, col_len;
+  std::vector<uint16_t> bucket_scale;
+  std::vector<uint16_t> row_sidx, block_sidx;
+  if (!scale_block2d) {
+    row_sidx.resize((size_t)n);
+    std::vector<std::pair<uint16_t, int32_t>> order((size_t)n);
+    for (int64_t r = 0; r < n; ++r) {
+      const uint16_t v = scale_scalar ? hsc[0] : hsc[(size_t)r];
+      order[(size_t)r] = {v, (int32_t)r};
+      row_sidx[(size_t)r] = sidx_of_value(v);
+    }
+    std::stable_sort(order.begin(), order.end(),
+                     [](const std::pair<uint16_t, int32_t> &x, const std::pair<uint16_t, int32_t> &y) {
+                       return x.first < y.first;
+                     });
+    size_t i = 0;
+    while (i < order.size()) {
+      size_t j = i;
+      while (j < order.size() && order[j].first == order[i].first) ++j;
+      for (size_t off = i; off < j; off += 128) {
+        const size_t take = std::min<size_t>(128, j - off);
+        for (size_t q = 0; q < take; ++q) row_indices.push_back(order[off + q].second);
+        bucket_scale.push_back(order[i].first);
+        col_start.push_back(0);
+        col_len.push_back((int32_t)m);
+        row_offsets.push_back((int32_t)row_indices.size());
+      }
+      i = j;
+    }
+  } else {
+    block_sidx.resize((size_t)(nb0 * nb1));
+    for (int64_t i = 0; i < nb0 * nb1; ++i) block_sidx[(size_t)i] = sidx_of_value(hsc[(size_t)i]);
+    for (int64_t br = 0; br < nb0; ++br) {
+      for (int64_t bc = 0; bc < nb1; ++bc) {
+        const uint16_t sc = hsc[(size_t)(br * nb1 + bc)];
+        for (int64_t off = 0; off < sb0; off += 128) {
+          const int64_t take = std::min<int64_t>(128, sb0 - off);
+          for (int64_t q = 0; q < take; ++q) row_indices.push_back((int32_t)(br * sb0 + off + q));
+          bucket_scale.push_back(sc);
+          col_start.push_back((int32_t)(bc * sb1));
+          col_len.push_back((int32_t)sb1);
+          row_offsets.push_back((int32_t)row_indices.size());
+        }
+      }
+    }
+  }
+  const uint32_t B = (uint32_t)bucket_scale.size();
+  std::vector<uint32_t> lane_base(B + 1, 0);
+  std::vector<uint16_t> bucket_sidx(B);
+  for (uint32_t b = 0; b < B; ++b) {
+    const int64_t total = (int64_t)(row_offsets[b + 1] - row_offsets[b]) * col_len[b];
+    const int64_t k_eff = std::min<int64_t>(kth, std::max<int64_t>(1, total));
+    lane_base[b + 1] = lane_base[b] + (uint32_t)k_eff;
+    bucket_sidx[b] = sidx_of_value(bucket_scale[b]);
+  }
+
+  auto sc = std::make_unique<mps_fp8_sidecar>();
+  DevBuf<uint16_t> d_row_sidx, d_block_sidx, d_bucket_sidx, d_scale_values;
+  DevBuf<uint32_t> d_lane_base;
+  HC(d_row_sidx.alloc(row_sidx.size()));
+  HC(d_block_sidx.alloc(block_sidx.size()));
+  HC(d_bucket_sidx.alloc(B));
+  HC(d_scale_values.alloc(S));
+  HC(d_lane_base.alloc(B + 1));
+  if (!row_sidx.empty())
+    HC(hipMemcpyAsync(d_row_sidx.p, row_sidx.data(), 2 * row_sidx.size(), hipMemcpyHostToDevice, s));
+  if (!block_sidx.empty())
+    HC(hipMemcpyAsync(d_block_sidx.p, block_sidx.data(), 2 * block_sidx.size(), hipMemcpyHostToDevice, s));
+  HC(hipMemcpyAsync(d_bucket_sidx.p, bucket_sidx.data(), 2 * (size_t)B, hipMemcpyHostToDevice, s));
+  HC(hipMemcpyAsync(d_scale_values.p, uniq_sc.data(), 2 * (size_t)S, hipMemcpyHostToDevice, s));
+  HC(hipMemcpyAsync(d_lane_base.p, lane_base.data(), 4 * (size_t)(B + 1), hipMemcpyHostToDevice, s));
+
+  HC(sc->bucket_scale.alloc(B));
+  HC(sc->bucket_row_offsets.alloc(B + 1));
+  HC(sc->row_indices.alloc(row_indices.size()));
+  HC(sc->bucket_col_start.alloc(B));
+  HC(sc->bucket_col_len.alloc(B));
+  HC(hipMemcpyAsync(sc->bucket_scale.p, bucket_scale.data(), 2 * (size_t)B, hipMemcpyHostToDevice, s));
+  HC(hipMemcpyAsync(sc->bucket_row_offsets.p, row_offsets.data(), 4 * (size_t)(B + 1), hipMemcpyHostToDevice, s));
+  if (!row_indices.empty())
+    HC(hipMemcpyAsync(sc->row_indices.p, row_indices.data(), 4 * row_indices.size(), hipMemcpyHostToDevice, s));
+  HC(hipMemcpyAsync(sc->bucket_col_start.p, col_start.data(), 4 * (size_t)B, hipMemcpyHostToDevice, s));
+  HC(hipMemcpyAsync(sc->bucket_col_len.p, col_len.data(), 4 * (size_t)B, hipMemcpyHostToDevice, s));
+
+  ScaleMap smap;
+  smap.mode = scale_block2d ? 1 : 0;
+  smap.row_sidx = d_row_sidx.p;
+  smap.block_sidx = d_block_sidx.p;
+  smap.sb0 = sb0;
+  smap.sb1 = sb1;
+  smap.nb1 = nb1;
+
+  // --- 1. histogram (retry with a larger table on overflow) ---
+  DevBuf<uint64_t> keys;
+  DevBuf<uint32_t> counts, flags;  // flags: [0] overflow, [1] error bits, [2..3] esc stats, [4] compact count
+  HC(flags.alloc(8));
+  uint64_t cap = 1u << 16;
+  while (cap < (uint64_t)std::min<int64_t>(numel, (int64_t)1 << 22) * 2) cap <<= 1;
+  const int64_t per_block = 1 << 14;
+  const unsigned hist_blocks = (unsigned)((numel + per_block - 1) / per_block);
+  uint32_t hflags[8] = {};
+  for (;;) {
+    HC(keys.alloc(cap));
+    HC(counts.alloc(cap));
+    HC(hipMemsetAsync(keys.p, 0xFF, sizeof(uint64_t) * cap, s));
+    HC(hipMemsetAsync(counts.p, 0, sizeof(uint32_t) * cap, s));
+    HC(hipMemsetAsync(flags.p, 0, sizeof(uint32_t) * 8, s));
+    hipLaunchKernelGGL(hist_kernel, dim3(hist_blocks), dim3(kHistBlock), 0, s, in->bf16, in->fp8, n, m, smap,
+                       per_block, keys.p, counts.p, cap - 1, flags.p);
+    HC(hipGetLastError());
+    HC(hipMemcpyAsync(hflags, flags.p, sizeof(hflags), hipMemcpyDeviceToHost, s));
+    HC(hipStreamSynchronize(s));
+    if (!hflags[0]) break;
+    if (cap >= ((uint64_t)1 << 34)) return fail(MPS_ERR_RUNTIME, "histogram table overflow");
+    cap <<= 1;
+  }
+
+  // --- 2. compaction and grouping by (scale, fp8) key ---
+  DevBuf<uint64_t> ckey;
+  DevBuf<uint32_t> ccount, cslot;
+  // bound for the compact arrays: count first
+  uint32_t D = 0;
+  {
+    HC(ckey.alloc(cap));
+    HC(ccount.alloc(cap));
+    HC(cslot.alloc(cap));
+    hipLaunchKernelGGL(compact_kernel, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, s, keys.p, counts.p, cap,
+                       ckey.p, ccount.p, cslot.p, flags.p + 4);
+    HC(hipGetLastError());
+    HC(hipMemcpyAsync(&D, flags.p + 4, 4, hipMemcpyDeviceToHost, s));
+    HC(hipStreamSynchronize(s));
+  }
+  const uint64_t T = (uint64_t)S * 256;
+  DevBuf<uint32_t> tcount, toff, tfill, tnz, tgid;
+  HC(tcount.alloc(T));
+  HC(toff.alloc(T));
+  HC(tfill.alloc(T));
+  HC(tnz.alloc(T));
+  HC(tgid.alloc(T));
+  HC(hipMemsetAsync(tcount.p, 0, 4 * T, s));
+  HC(hipMemsetAsync(tfill.p, 0, 4 * T, s));
+  hipLaunchKernelGGL(table_count_kernel, dim3((D + 255) / 256), dim3(256), 0, s, ckey.p, D, tcount.p);
+  HC(hipGetLastError());
+  uint32_t D_check = 0, G = 0;
+  HC(device_scan(tcount.p, toff.p, T, s, &D_check));
+  hipLaunchKernelGGL(nonzero_kernel, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s, tcount.p, T, tnz.p);
+  HC(hipGetLastError());
+  HC(device_scan(tnz.p, tgid.p, T, s, &G));
+  if (D_check != D) return fail(MPS_ERR_RUNTIME, "internal error: histogram grouping mismatch");
+  DevBuf<uint16_t> seg_sym;
+  DevBuf<uint32_t> seg_cnt, seg_slot, gid_tkey, ws_off, cw_slot;
+  HC(seg_sym.alloc(D));
+  HC(seg_cnt.alloc(D));
+  HC(seg_slot.alloc(D));
+  HC(gid_tkey.alloc(G));
+  hipLaunchKernelGGL(scatter_kernel, dim3((D + 255) / 256), dim3(256), 0, s, ckey.p, ccount.p, cslot.p, D, toff.p,
+                     tfill.p, seg_sym.p, seg_cnt.p, seg_slot.p);
+  hipLaunchKernelGGL(table_list_kernel, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s, tcount.p, tgid.p, T,
+                     gid_tkey.p);
+  HC(hipGetLastError());
+
+  // --- 3. code books ---
+  const uint32_t Tsz = 1u << L;
+  const uint32_t packed = Tsz / 2 > 0 ? Tsz / 2 : 1;
+  HC(sc->decode_syms.alloc((size_t)G * Tsz));
+  HC(sc->decode_lens.alloc((size_t)G * packed));
+  HC(sc->table_scale.alloc(G));
+  HC(sc->table_fp8.alloc(G));
+  HC(cw_slot.alloc(cap));
+  // per-key workspace, sized by each key's list length
+  DevBuf<uint32_t> ws_sz;
+  HC(ws_sz.alloc(G));
+  HC(ws_off.alloc(G));
+  uint32_t ws_total = 0;
+  if (G) {
+    hipLaunchKernelGGL(ws_size_kernel, dim3((G + 255) / 256), dim3(256), 0, s, gid_tkey.p, tcount.p, G, Tsz,
+                       ws_sz.p);
+    HC(hipGetLastError());
+    HC(device_scan(ws_sz.p, ws_off.p, G, s, &ws_total));
+  }
+  DevBuf<int32_t> ws;
+  HC(ws.alloc(ws_total));
+  CodebookArgs cba;
+  cba.gid_tkey = gid_tkey.p;
+  cba.toff = toff.p;
+  cba.tcount = tcount.p;
+  cba.seg_sym = seg_sym.p;
+  cba.seg_cnt = seg_cnt.p;
+  cba.seg_slot = seg_slot.p;
+  cba.ws = ws.p;
+  cba.ws_off = ws_off.p;
+  cba.scale_values = d_scale_values.p;
+  cba.cw_slot = cw_slot.p;
+  cba.decode_syms = sc->decode_syms.p;
+  cba.decode_lens = sc->decode_lens.p;
+  cba.table_scale = sc->table_scale.p;
+  cba.table_fp8 = sc->table_fp8.p;
+  cba.G = G;
+  cba.L = (int)L;
+  cba.err = flags.p + 1;
+  cba.esc_stats = flags.p + 2;
+  if (G) hipLaunchKernelGGL(codebook_kernel, dim3((G + 63) / 64), dim3(64), 0, s, cba);
+  HC(hipGetLastError());
+
+  // --- 4. bucket tables ---
+  HC(sc->bucket_table.alloc((size_t)B * 256));
+  HC(sc->bucket_U.alloc(B));
+  HC(sc->bucket_unique_gid.alloc((size_t)B * 256));
+  HC(sc->bucket_fp8_uidx.alloc((size_t)B * 256));
+  if (B)
+    hipLaunchKernelGGL(bucket_table_kernel, dim3((B + 63) / 64), dim3(64), 0, s, d_bucket_sidx.p, B, tcount.p,
+                       tgid.p, sc->bucket_table.p, sc->bucket_U.p, sc->bucket_unique_gid.p, sc->bucket_fp8_uidx.p);
+  HC(hipGetLastError());
+
+  // --- 5. bitstream ---
+  HC(sc->bucket_thread_startbit.alloc((size_t)B * (kth + 1)));
+  HC(hipMemsetAsync(sc->bucket_thread_startbit.p, 0, 4 * (size_t)B * (kth + 1), s));
+  DevBuf<uint32_t> cw_elem, bucket_bits;
+  HC(cw_elem.alloc((size_t)numel));
+  HC(bucket_bits.alloc(B));
+  const uint32_t lanes = lane_base[B];
+  LaneArgs la;
+  la.bf16 = in->bf16;
+  la.fp8 = in->fp8;
+  la.S = smap;
+  la.m = m;
+  la.row_offsets = sc->bucket_row_offsets.p;
+  la.row_indices = sc->row_indices.p;
+  la.col_start = sc->bucket_col_start.p;
+  la.col_len = sc->bucket_col_len.p;
+  la.lane_base = d_lane_base.p;
+  la.B = B;
+  la.k = kth;
+  la.keys = keys.p;
+  la.cw_slot = cw_slot.p;
+  la.cap_mask = cap - 1;
+  la.cw_elem = cw_elem.p;
+  la.lane_bits = sc->bucket_thread_startbit.p;
+  la.err = flags.p + 1;
+  if (lanes) hipLaunchKernelGGL(lane_bits_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, la);
+  HC(hipGetLastError());
+  if (B) hipLaunchKernelGGL(lane_starts_kernel, dim3(B), dim3(1024), 0, s, sc->bucket_thread_startbit.p,
+                            d_lane_base.p, kth, bucket_bits.p);
+  HC(hipGetLastError());
+  std::vector<uint32_t> h_bucket_bits(B);
+  if (B) HC(hipMemcpyAsync(h_bucket_bits.data(), bucket_bits.p, 4 * (size_t)B, hipMemcpyDeviceToHost, s));
+  HC(hipMemcpyAsync(hflags, flags.p, sizeof(hflags), hipMemcpyDeviceToHost, s));
+  HC(hipStreamSynchronize(s));
+  if (hflags[1] & 2u) return fail(MPS_ERR_RUNTIME, "invalid code length");
+  if (hflags[1] & 4u) return fail(MPS_ERR_RUNTIME, "missing enc table for (scale,fp8) key");
+  // 64-bit aligned bucket bases (build_huffman.cu:813-818), final cursor unaligned
+  std::vector<int64_t> bit_base(B + 1, 0);
+  int64_t pos = 0;
+  for (uint32_t b = 0; b < B; ++b) {
+    if (pos & 63) pos = (pos + 63) & ~(int64_t)63;
+    bit_base[b] = pos;
+    pos += h_bucket_bits[b];
+  }
+  bit_base[B] = pos;
+  const int64_t W = (pos + 63) >> 6;
+  HC(sc->bucket_bit_base.alloc(B + 1));
+  HC(hipMemcpyAsync(sc->bucket_bit_base.p, bit_base.data(), 8 * (size_t)(B + 1), hipMemcpyHostToDevice, s));
+  HC(sc->bitstream.alloc((size_t)W));
+  if (W) HC(hipMemsetAsync(sc->bitstream.p, 0, 8 * (size_t)W, s));
+  PackArgs pa;
+  pa.bf16 = in->bf16;
+  pa.m = m;
+  pa.row_offsets = sc->bucket_row_offsets.p;
+  pa.row_indices = sc->row_indices.p;
+  pa.col_start = sc->bucket_col_start.p;
+  pa.col_len = sc->bucket_col_len.p;
+  pa.lane_base = d_lane_base.p;
+  pa.B = B;
+  pa.k = kth;
+  pa.cw_elem = cw_elem.p;
+  pa.startbit = sc->bucket_thread_startbit.p;
+  pa.bit_base = sc->bucket_bit_base.p;
+  pa.bits = reinterpret_cast<unsigned long long *>(sc->bitstream.p);
+  if (lanes && W) hipLaunchKernelGGL(pack_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, pa);
+  HC(hipGetLastError());
+  const int64_t shape[3] = {n, m, kth};
+  HC(sc->shape_nmk.alloc(3));
+  HC(hipMemcpyAsync(sc->shape_nmk.p, shape, sizeof(shape), hipMemcpyHostToDevice, s));
+  HC(hipMemcpyAsync(hflags, flags.p, sizeof(hflags), hipMemcpyDeviceToHost, s));
+  HC(hipStreamSynchronize(s));
+
+  const int64_t sizes[17] = {(int64_t)G * Tsz, (int64_t)G * packed, G, G, B, B + 1, (int64_t)row_indices.size(),
+                             (int64_t)B * 256, B, B, (int64_t)B * (kth + 1), B + 1, W, 3, B, (int64_t)B * 256,
+                             (int64_t)B * 256};
+  std::memcpy(sc->sizes, sizes, sizeof(sizes));
+  sc->stats[0] = hflags[2];
+  sc->stats[1] = hflags[3];
+  sc->stats[2] = D;
+  sc->stats[3] = (int64_t)cap;
+  *out = sc.release();
+  return MPS_OK;
+#undef HC
+}
+
+int mps_fp8_sidecar_sizes(const mps_fp8_sidecar *sc, int64_t *sizes17) {
+  if (!sc || !sizes17) return fail(MPS_ERR_INVALID_ARGUMENT, "NULL argument");
+  std::memcpy(sizes17, sc->sizes, sizeof(sc->sizes));
+  return MPS_OK;
+}
+
+int mps_fp8_sidecar_stats(const mps_fp8_sidecar *sc, int64_t *stats4) {
+  if (!sc || !stats4) return fail(MPS_ERR_INVALID_ARGUMENT, "NULL argument");
+  std::memcpy(stats4, sc->stats, sizeof(sc->stats));
+  return MPS_OK;
+}
+
+int mps_fp8_sidecar_copy(const mps_fp8_sidecar *sc, void *const *dst17, void *stream) {
+  last_error().clear();
+  if (!sc || !dst17) return fail(MPS_ERR_INVALID_ARGUMENT, "NULL argument");
+  const void *src[17] = {sc->decode_syms.p, sc->decode_lens.p, sc->table_scale.p, sc->table_fp8.p,
+                         sc->bucket_scale.p, sc->bucket_row_offsets.p, sc->row_indices.p, sc->bucket_table.p,
+                         sc->bucket_col_start.p, sc->bucket_col_len.p, sc->bucket_thread_startbit.p,
+                         sc->bucket_bit_base.p, sc->bitstream.p, sc->shape_nmk.p, sc->bucket_U.p,
+                         sc->bucket_unique_gid.p, sc->bucket_fp8_uidx.p};
+  const int esize[17] = {2, 1, 2, 2, 2, 4, 4, 4, 4, 4, 4, 8, 8, 8, 4, 4, 2};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int i = 0; i < 17; ++i) {
+    const size_t bytes = (size_t)sc->sizes[i] * esize[i];
+    if (bytes == 0) continue;
+    if (!dst17[i]) return fail(MPS_ERR_INVALID_ARGUMENT, "NULL destination %d", i);
+    MPS_HIP_CHECK(hipMemcpyAsync(dst17[i], src[i], bytes, hipMemcpyDefault, s));
+  }
+  MPS_HIP_CHECK(hipStreamSynchronize(s));
+  return MPS_OK;
+}
+
+int mps_fp8_sidecar_free(mps_fp8_sidecar *sc) {
+  delete sc;
+  return MPS_OK;
+}
+
+}  // extern "C"

@@ -69,3 +69,21 @@ def test_decode_validation_messages_via_meta_checks(monkeypatch):
         with pytest.raises(ValueError, match=msg):
             mc.validate_decode_args(*a)
     mc.validate_decode_args(*args)
+
+
+def test_build_dtype_checks_run_before_any_gpu_work():
+    bf = torch.zeros((4, 8), dtype=torch.bfloat16)
+    q = torch.zeros((4, 8), dtype=torch.uint8)
+    sc = torch.zeros(4, dtype=torch.uint16)
+    with pytest.raises(ValueError, match="bf16_params must be torch.bfloat16"):
+        MPServe_cuda.huffman_build_fp8_decode_tables(bf.float(), q, sc, 7, 16)
+    with pytest.raises(ValueError, match="fp8_params must be torch.uint8"):
+        MPServe_cuda.huffman_build_fp8_decode_tables(bf, q.to(torch.int8), sc, 7, 16)
+    with pytest.raises(ValueError, match=r"max_len must be in \[1, 15\]"):
+        MPServe_cuda.huffman_build_fp8_decode_tables(bf, q, sc, 16, 16)
+    with pytest.raises(ValueError, match=r"threads_per_block must be in \[1, 1024\]"):
+        MPServe_cuda.huffman_build_fp8_decode_tables(bf, q, sc, 7, 0)
+    with pytest.raises(ValueError, match="bf16_params and fp8_params must have same numel"):
+        MPServe_cuda.huffman_build_fp8_decode_tables(bf, q[:2], sc, 7, 16)
+    with pytest.raises(ValueError, match="scales must be torch.uint16 or torch.bfloat16"):
+        MPServe_cuda.huffman_build_fp8_decode_tables(bf, q, sc.to(torch.int32), 7, 16)
