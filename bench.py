@@ -1,0 +1,261 @@
+#!/usr/bin/env python3
+"""FP8 + Huffman sidecar -> BF16 decode throughput on one MI355X.
+
+Workload (default ``model8b``): every linear weight of a Llama-3-8B-shaped
+random-init model -- 32 layers x {q, k, v, o, gate, up, down} plus lm_head
+128256x4096 -- as seeded N(0, 0.02^2) BF16, quantized per output channel to
+FP8 e4m3, with its Huffman sidecar (max_len 7, 1024 substreams per bucket)
+built by the GPU sidecar builder. A step is one pass that rebuilds all 225
+BF16 weights from FP8 bytes + sidecar, in one launch of the batched decode
+plan; every input is resident in HBM before the timed region starts.
+
+Output: one JSON line on stdout (progress goes to stderr). ``value`` is the
+BF16 bytes written per second (GB/s) over the timed steps; ``roofline``
+prices the decode kernel's algorithmic bytes per launch (FP8 bytes, bitstream,
+LUTs, bucket metadata, BF16 output) against MI355X's 8 TB/s HBM peak, with the
+kernel's duration taken from HIP events on the launch stream; ``cpu_baseline``
+is the CPU restatement of the same decode, multi-threaded on this host's
+cores, over a bounded sample (layer-0 weights, repeated up to a time budget).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "BF16 decompress GB/s (out) + % HBM peak; full 8B-model FP8→BF16 ms"
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "fp8_decode_model8b_traffic.md")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", choices=("model8b", "layer8b"), default="model8b",
+                   help="model8b: full Llama-3-8B-shaped model (the headline); layer8b: one layer")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="time budget of the CPU baseline sample")
+    p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: min(16, cpu_count))")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-verify", action="store_true", help="skip the bit-exact check of the outputs")
+    return p.parse_args(argv)
+
+
+def weight_list(workload: str):
+    from mpserve_amd.synthetic import LLAMA3_8B_LAYER, LLAMA3_8B_LM_HEAD
+
+    layers = 32 if workload == "model8b" else 1
+    out = []
+    for layer in range(layers):
+        for j, (name, n, m) in enumerate(LLAMA3_8B_LAYER):
+            out.append((f"layers.{layer}.{name}", n, m, 100 + 16 * layer + j))
+    if workload == "model8b":
+        name, n, m = LLAMA3_8B_LM_HEAD
+        out.append((name, n, m, 99))
+    return out
+
+
+def algorithmic_bytes(n: int, m: int, sc) -> int:
+    """Bytes a decode of one tensor must move: FP8 bytes + bitstream + LUTs +
+    bucket metadata read, BF16 written."""
+    N = n * m
+    W = sc["bitstream_u64"].numel()
+    G = sc["decode_syms_u16"].shape[0]
+    B = sc["bucket_table_i32"].shape[0]
+    k = sc["bucket_thread_startbit_u32"].shape[1] - 1
+    R = sc["row_indices_i32"].numel()
+    return N + 8 * W + 320 * G + B * (1024 + 4 * (k + 1) + 8 + 4 + 8) + 8 + 4 + 4 * R + 2 * N
+
+
+# builder outputs the compress script does not persist (bucket_U/unique_gid/fp8_uidx)
+_NOT_STORED = ("bucket_U_i32", "bucket_unique_gid_i32", "bucket_fp8_uidx_i16")
+
+
+def sidecar_bytes(sc) -> int:
+    """Bytes of the sidecar tensors a checkpoint stores next to the FP8 bytes."""
+    return sum(t.numel() * t.element_size() for k, t in sc.items() if k not in _NOT_STORED)
+
+
+def read_traffic(workload: str):
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary, if it covers this workload."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None, None
+    m = re.search(r"^traffic_bytes_per_launch\[%s\]\s*=\s*([0-9.eE+]+)" % re.escape(workload), text, re.M)
+    if not m:
+        return None, None
+    return float(m.group(1)), os.path.relpath(TRAFFIC_PROFILE, ROOT)
+
+
+def cpu_baseline(items, seconds: float, threads: int):
+    """Oracle (CPU restatement) decode of layer-0 weights, repeated until ``seconds`` pass."""
+    import numpy as np
+    import oracle
+
+    host = []
+    for name, fp8, sc, src in items:
+        n, m = fp8.shape
+        host.append((name, fp8.cpu().numpy(), {k: v.cpu().numpy() for k, v in sc.items()},
+                     src.view(__import__("torch").uint16).cpu().numpy(), n, m))
+    done_elems = 0
+    elapsed = 0.0
+    names = []
+    while elapsed < seconds:
+        for name, q, sc, ref, n, m in host:
+            out = np.empty((n, m), dtype=np.uint16)
+            t0 = time.perf_counter()
+            oracle.decode(sc, q, n, m, 7, oracle.MODE_LOSSLESS, threads, out)
+            elapsed += time.perf_counter() - t0
+            if not np.array_equal(out, ref):
+                raise RuntimeError(f"CPU baseline decode of {name} is not bit-exact")
+            done_elems += n * m
+            names.append(name)
+            if elapsed >= seconds:
+                break
+    gbs = 2.0 * done_elems / elapsed / 1e9
+    sample = (f"{len(names)} decodes of layer-0 weights ({done_elems / 1e6:.1f} M elements, "
+              f"{2 * done_elems / 1e9:.2f} GB BF16 out) in {elapsed:.2f} s")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port", "sample": sample}
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the FP8+Huffman decode shards by "
+              "bucket with no exchange step, so there is no multi-GPU figure to report", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from mpserve_amd.encode import build_fp8_sidecar
+    from mpserve_amd.decode import DecodePlan
+    from mpserve_amd.synthetic import make_weight
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    weights = weight_list(args.workload)
+    log(f"workload {args.workload}: {len(weights)} tensors, building inputs on {torch.cuda.get_device_name(dev)}")
+
+    t_build = time.perf_counter()
+    entries = []  # (name, fp8, sidecar, src)
+    total_alg = 0
+    total_side = 0
+    for i, (name, n, m, seed) in enumerate(weights):
+        w = make_weight(n, m, sigma=0.02, seed=seed, device=dev)
+        sc = build_fp8_sidecar(w.bf16, w.fp8_u8, w.scale_u16, max_len=7, threads_per_block=1024)
+        entries.append((name, w.fp8_u8, sc, w.bf16))
+        total_alg += algorithmic_bytes(n, m, sc)
+        total_side += sidecar_bytes(sc)
+        del w
+        if i % 7 == 6 or i == len(weights) - 1:
+            log(f"built {i + 1}/{len(weights)} ({time.perf_counter() - t_build:.1f} s)")
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t_build
+
+    outs = [torch.empty(src.shape, dtype=torch.bfloat16, device=dev) for _, _, _, src in entries]
+    plan = DecodePlan((fp8, sc, o) for (_, fp8, sc, _), o in zip(entries, outs))
+    elems = sum(o.numel() for o in outs)
+    bf16_bytes = 2 * elems
+    stream = torch.cuda.current_stream(dev)
+
+    for _ in range(max(1, args.warmup)):
+        plan.decode(stream)
+    torch.cuda.synchronize()
+    if not args.no_verify:
+        for (name, _, _, src), o in zip(entries, outs):
+            if not torch.equal(o.view(torch.uint16), src.view(torch.uint16)):
+                raise RuntimeError(f"decode of {name} is not bit-exact")
+        log("warm-up outputs bit-exact")
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        plan.decode(stream)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    ms_per_step = wall * 1e3 / args.steps
+    log(f"{args.steps} steps: {ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms per decode launch (events)")
+
+    if not args.no_verify:
+        for (name, _, _, src), o in zip(entries, outs):
+            if not torch.equal(o.view(torch.uint16), src.view(torch.uint16)):
+                raise RuntimeError(f"timed decode of {name} is not bit-exact")
+
+    value = bf16_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = total_alg / (kernel_ms * 1e-3) / 1e9
+    traffic, traffic_src = read_traffic(args.workload)
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        layer0 = [e for e in entries if e[0].startswith("layers.0.")]
+        log(f"CPU baseline: oracle decode on {threads} threads, ~{args.cpu_seconds:.0f} s budget")
+        cpu = cpu_baseline(layer0, args.cpu_seconds, threads)
+
+    fp8_bytes = elems
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u16",
+        "data": "synthetic: seeded N(0,0.02^2) BF16, per-channel FP8 e4m3, sidecar built on the GPU",
+        "config": {
+            "workload": ("cfg5: Llama-3-8B-shaped full model, 32 layers x 7 linears + lm_head 128256x4096"
+                         if args.workload == "model8b" else "cfg2: one Llama-3-8B layer, 7 linears"),
+            "tensors": len(entries),
+            "elements": elems,
+            "max_len": 7,
+            "threads_per_block": 1024,
+            "full_decode_ms": round(kernel_ms, 4),
+            "pct_hbm_peak_out": round(100.0 * value / HBM_PEAK_GBS, 2),
+            "pct_hbm_peak_rw": round(100.0 * achieved / HBM_PEAK_GBS, 2),
+            "sidecar_over_bf16": round(total_side / bf16_bytes, 4),
+            "sidecar_plus_fp8_over_bf16": round((total_side + fp8_bytes) / bf16_bytes, 4),
+            "build_s": round(build_s, 2),
+            "plan": plan.info(),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": total_alg,
+            "kernel_ms": round(kernel_ms, 4),
+            "traffic_source": traffic_src,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
