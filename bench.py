@@ -50,6 +50,9 @@ def parse_args(argv=None):
     p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: min(16, cpu_count))")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-verify", action="store_true", help="skip the bit-exact check of the outputs")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="after the timed steps, run 3 plain int32 elementwise copies of MIB MiB each "
+                        "(reference kernel of known bytes for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args(argv)
 
 
@@ -200,6 +203,17 @@ def main(argv=None) -> int:
         for (name, _, _, src), o in zip(entries, outs):
             if not torch.equal(o.view(torch.uint16), src.view(torch.uint16)):
                 raise RuntimeError(f"timed decode of {name} is not bit-exact")
+
+    if args.copy_calibration > 0:
+        n32 = args.copy_calibration * (1 << 20) // 4
+        src32 = torch.ones(n32, dtype=torch.int32, device=dev)
+        dst32 = torch.empty_like(src32)
+        for _ in range(3):
+            torch.bitwise_not(src32, out=dst32)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 x bitwise_not over {args.copy_calibration} MiB int32 "
+            f"(reads and writes {n32 * 4} bytes each)")
+        del src32, dst32
 
     value = bf16_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = total_alg / (kernel_ms * 1e-3) / 1e9
