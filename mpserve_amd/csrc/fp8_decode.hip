@@ -214,237 +214,216 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Fast path for buckets whose column range is a multiple of k_eff (every
-// Llama-shaped tensor with k = 1024) and that hold at most 128 rows (every
-// bucket the reference builder makes). Then lane t's i-th element lies in row
-// i / P, column c0 + t + (i % P) * k_eff with P = col_len / k_eff: row and
-// column phase are the same for every lane. The walk over elements lives in
-// scalar registers and enters the FP8 loads and BF16 stores as the buffer
-// soffset; the per-lane voffset is just the lane (x2 for BF16). Row offsets
-// sit one per lane in two VGPRs and are fetched with v_readlane.
+// ---------------------------------------------------------------------------
+// Fast path: buckets whose column range is a multiple of k_eff and that hold
+// at most 128 rows (every bucket of a Llama-shaped tensor with k = 1024).
+// Then every lane owns exactly rows * P elements (P = col_len / k_eff), and
+// lane t's i-th element sits at row i / P, column c0 + t + (i % P) * k_eff:
+// the walk is the same for every lane. It runs in scalar registers and feeds
+// the FP8 loads and BF16 stores as the buffer soffset; the per-lane voffset
+// is the lane (x2 for BF16).
 //
-// Memory pipeline (gfx9 keeps one in-order vmcnt for loads and stores):
-// elements go in blocks of kDepth; FP8 bytes of block b+3 are loaded while
-// block b decodes (4-slot register ring) and the next two bitstream chunks
-// are staged one block ahead. The loop body issues the same loads and stores
-// on every path: elements past the lane's last are phantoms whose offsets lie
-// beyond the buffers (reads give 0, stores are dropped by the hardware range
-// check).
-//
-// Bit supply: `buf` (64-bit, MSB-aligned) holds `cnt` bits; it is topped up
-// from a 4-chunk register queue once per kG = 4 elements (<= 28 bits without
-// ESC). The staged pair is appended at each block start when the queue has
-// room, which keeps >= 2 chunks queued at block starts and makes the queue
-// last a whole block of non-ESC codes. ESC codes (16 raw bits follow) are
-// handled on a branch only waves with an ESC lane take; if the payload leaves
-// too few queued bits for the rest of the block, the lane "parks": it records
-// its element index and bit position and moves its store offsets out of
-// range, keeps running the loop on garbage (nothing of it is stored), and
-// finishes in a plain loop at the end.
+// Bit supply. Each lane keeps the next chunks (32 stream bits) of its
+// substream in an 8-deep LDS queue (slot-major: chunk c of lane t at
+// [(c % 8) * 1024 + t], so a wave's accesses hit 64 distinct banks). Chunks
+// arrive in aligned pairs (one u64 bitstream word): every block of kDepth
+// elements each lane requests the next pair if it holds fewer than kAhead
+// chunks ahead of its read position, and writes the pair requested kRing
+// blocks earlier into the queue. The request is one unconditional
+// buffer_load_dwordx2 per block (lanes that do not need a pair read out of
+// range and ignore the zeros), so every block issues the same memory
+// instructions - 1 bitstream load, kDepth FP8 loads, kDepth stores - and the
+// compiler's in-order vmcnt waits stay kRing - 1 blocks deep. A group of kG = 4
+// elements decodes from a 32-bit window cut out of two queued chunks (4 codes
+// of <= 7 bits). An ESC code (16 raw bits follow) re-reads the window; a
+// lane whose queue has run dry reads its two chunks from memory directly.
+// ---------------------------------------------------------------------------
 constexpr int kG = 4;
-constexpr int kRing = 4;
-constexpr uint32_t kPast = 0x40000000u;  // offset beyond every fast-path buffer (2*n*m <= 2^30)
+#ifndef MPS_DECODE_RING
+#define MPS_DECODE_RING 4
+#endif
+constexpr int kRing = MPS_DECODE_RING;     // blocks in flight: FP8 ring slots and bitstream request slots
+constexpr uint32_t kAhead = 7;             // request while fewer chunks than this are queued ahead
+constexpr int kQSlots = 8;                 // LDS queue depth (chunks per lane)
+constexpr uint32_t kPast = 0x40000000u;    // offset beyond every fast-path buffer (2*n*m <= 2^30)
+constexpr uint32_t kBsPast = 0x80000000u;  // bitstream offset beyond every bucket's range
 
-__device__ __forceinline__ void decode_lane_rows(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
-                                                 const int32_t *__restrict__ s_rows, uint32_t *s_sink,
-                                                 int32_t lane, int32_t k_eff,
-                                                 int32_t rows, int32_t c0, int32_t P, uint64_t pos0,
-                                                 uint64_t pos_end, uint32_t *status) {
+// LDS: 256 tables x 128 u32 entries, then the queue (kQSlots x kBlock u32).
+// During set-up the queue region also holds the fp8 -> table map; the generic
+// path keeps the bucket's row indices there.
+constexpr int kLutWords = 256 * kTable;
+constexpr int kLdsWords = kLutWords + kQSlots * kBlock;
+
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+
+__device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+                                                 uint32_t *__restrict__ queue, uint32_t lane, uint32_t k_eff,
+                                                 uint32_t rows, uint32_t P, uint32_t rowoff_lo,
+                                                 uint32_t rowoff_hi, uint64_t bucket_bit,
+                                                 uint2 first[3], uint32_t pos, uint32_t pos_end,
+                                                 uint32_t *status) {
+  // Uniform values computed on the VALU (the division above, selects) would
+  // otherwise stay in VGPRs and drag the whole walk, and the buffer offsets it
+  // feeds, into vector registers.
+  k_eff = uni(k_eff);
+  rows = uni(rows);
+  P = uni(P);
+  bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
   const uint32_t nm = (uint32_t)(T.n * T.m);
   const __amdgpu_buffer_rsrc_t r_fp8 = make_rsrc(T.fp8, nm);
   const __amdgpu_buffer_rsrc_t r_out = make_rsrc(T.out, 2u * nm);
+  // Bitstream window of this bucket: from its 64-bit aligned base to the end.
+  const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
+  const uint64_t base_byte = bucket_bit >> 3;
+  const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
   const __amdgpu_buffer_rsrc_t r_bs =
-      make_rsrc(T.bitstream, T.bitstream_words > 0 ? (uint32_t)(T.bitstream_words * 8) : 0u);
-  auto chunk = [&](uint32_t c) -> uint32_t {  // stream chunk c = u32 at byte (c ^ 1) * 4
+      make_rsrc(reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+  // Stream chunk c (relative to the bucket base): u32 at byte (c ^ 1) * 4.
+  auto chunk_mem = [&](uint32_t c) -> uint32_t {
     return __builtin_amdgcn_raw_buffer_load_b32(r_bs, (c ^ 1u) << 2, 0, 0);
   };
+  auto qidx = [&](uint32_t c) -> uint32_t { return ((c & (kQSlots - 1)) * kBlock) + lane; };
 
-  const uint32_t m = (uint32_t)T.m;
-  const uint32_t cl = (uint32_t)(P * k_eff);
-  const int32_t count = rows * P;
-  const uint32_t vlane = (uint32_t)lane;
-  uint32_t vstore = 2u * (uint32_t)lane;  // + kPast once the lane parks
-  // Row offsets (row * m + c0) of the bucket's rows 0..63 and 64..127, one per lane.
-  const int wl = lane & 63;
-  const uint32_t rowoff_lo = wl < rows ? (uint32_t)s_rows[wl] * m + (uint32_t)c0 : 0u;
-  const uint32_t rowoff_hi = wl + 64 < rows ? (uint32_t)s_rows[wl + 64] * m + (uint32_t)c0 : 0u;
-  auto row_offset = [&](int32_t r) -> uint32_t {
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_lo, r & 63);
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_hi, r & 63);
-    return r < 64 ? a : b;
+  // Initial queue: the three pairs loaded during set-up.
+  const uint32_t rq0 = (pos >> 5) & ~1u;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    queue[qidx(rq0 + 2 * i)] = first[i].y;      // high half = first chunk of the pair
+    queue[qidx(rq0 + 2 * i + 1)] = first[i].x;
+  }
+  uint32_t rq = rq0 + 6;  // next pair to request
+  uint32_t wq = rq0 + 6;  // chunks below wq are (or were) in the queue
+
+  // Uniform element walker: offset (elements) of the next element, then advance.
+  const uint32_t count = rows * P;
+  auto row_offset = [&](uint32_t r) -> uint32_t {
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_lo, (int)(r & 63u));
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_hi, (int)(r & 63u));
+    return r < 64u ? a : b;
   };
-  // Uniform element walker: offset of the next element, then advance.
   struct Walker {
-    int32_t r;
-    uint32_t col, rowoff;
+    uint32_t r, p, off;
   };
   auto walk = [&](Walker &w) -> uint32_t {
-    const uint32_t so = w.r < rows ? w.rowoff + w.col : kPast;
-    w.col += (uint32_t)k_eff;
-    if (w.col == cl) {
-      w.col = 0;
+    const uint32_t so = w.r < rows ? w.off : kPast;
+    w.off += k_eff;
+    if (++w.p == P) {
+      w.p = 0;
       ++w.r;
-      w.rowoff = row_offset(w.r < rows ? w.r : rows - 1);
+      w.off = row_offset(w.r < rows ? w.r : rows - 1u);
     }
     return so;
   };
-  Walker wload{0, 0, row_offset(0)}, wstore{0, 0, row_offset(0)};
+  Walker wl{0u, 0u, row_offset(0)}, ws{0u, 0u, row_offset(0)};
 
-  // Bit reader state.
-  const uint32_t cb = (uint32_t)(pos0 >> 5);
-  const int skip = (int)(pos0 & 31u);
-  uint64_t buf = (((uint64_t)chunk(cb) << 32) | chunk(cb + 1)) << skip;
-  int cnt = 64 - skip;
-  uint32_t q0 = chunk(cb + 2), q1 = chunk(cb + 3), q2 = chunk(cb + 4), q3 = chunk(cb + 5);
-  int qn = 4;
-  uint32_t tail = cb + 6;
-  auto bitpos = [&]() -> uint32_t { return tail * 32u - (uint32_t)cnt - 32u * (uint32_t)qn; };
-  // Parking state.
-  bool parked = false;
-  int32_t park_i = count;
-  uint32_t park_bit = 0;
-  bool stale = false;
-
-  auto pop = [&]() {
-    buf |= (uint64_t)q0 << (32 - cnt);
-    q0 = q1;
-    q1 = q2;
-    q2 = q3;
-    --qn;
-    cnt += 32;
-  };
-  auto park = [&](int32_t i, uint32_t bit) {
-    parked = true;
-    park_i = i;
-    park_bit = bit;
-    vstore = kPast + 2u * vlane;
-  };
-  auto decode_one = [&](int32_t i, uint32_t q) {
-    const uint32_t so = walk(wstore);
-    const uint32_t hi = (uint32_t)(buf >> 32);
-    const uint32_t ent = lut[(q << kL) | (hi >> (32 - kL))];
-    const int len = (int)((ent >> 16) & 7u);
-    buf <<= len;
-    cnt -= len;
-    uint32_t sym = ent;
-    const bool esc = (int32_t)ent < 0;
-    if (__builtin_amdgcn_ballot_w64(esc)) {
-      if (esc) {
-        // ESC: the symbol is the next 16 raw bits.
-        if (!parked && cnt + 32 * qn < 16) park(i, bitpos() + (uint32_t)len);
-        if (cnt < 16) pop();
-        sym = (uint32_t)(buf >> 48);
-        buf <<= 16;
-        cnt -= 16;
-        if (cnt < 32 && qn > 0) pop();
-        // Keep enough queued for the rest of the block (<= 7 codes of 7 bits).
-        if (!parked && (cnt < 32 || qn < 2)) park(i + 1, bitpos());
-      }
-    }
-    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sym, r_out, vstore, 2u * so, 0);
-  };
-
-  uint32_t qr[kRing][kDepth];
-  uint32_t s0, s1;
-  // L2 touch of the bitstream kTouch chunks ahead of the staged pair, so that
-  // the staged loads (one block of lead) hit L2. The touch is an LDS-DMA
-  // buffer load into a scratch sink: it writes no VGPR, so no wait in the
-  // loop ever depends on it.
-  constexpr uint32_t kTouch = 16;
-  auto touch = [&](uint32_t c) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r_bs, (__attribute__((address_space(3))) void *)s_sink, 4,
-                                             (c ^ 1u) << 2, 0, 0, 0);
-  };
-  // Prologue: blocks 0..kRing-2 in flight.
+  uint32_t qr[kRing][kDepth];  // FP8 bytes, one ring slot per block
+  uint2 inflight[kRing];       // requested pairs, one slot per block of the ring
+  bool valid[kRing];
+#pragma unroll
+  for (int s = 0; s < kRing; ++s) valid[s] = false;
 #pragma unroll
   for (int b = 0; b < kRing - 1; ++b)
 #pragma unroll
-    for (int j = 0; j < kDepth; ++j) qr[b][j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, vlane, walk(wload), 0);
-  s0 = chunk(tail);
-  s1 = chunk(tail + 1);
+    for (int j = 0; j < kDepth; ++j) qr[b][j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, lane, walk(wl), 0);
 #pragma unroll
-  for (int t = 0; t < kRing; ++t) touch(tail + kTouch - 8 + 2 * t);
+  for (int s = 0; s < kRing; ++s) inflight[s] = make_uint2(0u, 0u);
 
-  uint32_t end_bit = 0;
-  auto ring = [&](int32_t i0, bool last) {
-#pragma unroll
-    for (int slot = 0; slot < kRing; ++slot) {
-      const int32_t b0 = i0 + slot * kDepth;
-      // 1. queue the pair staged one block ago, if it is current and fits
-      if (!stale && qn <= 2) {
-        q0 = (qn == 0) ? s0 : q0;
-        q1 = (qn == 0) ? s1 : (qn == 1) ? s0 : q1;
-        q2 = (qn == 1) ? s1 : (qn == 2) ? s0 : q2;
-        q3 = (qn == 2) ? s1 : q3;
-        qn += 2;
-        tail += 2;
+  // Window of the next 32 stream bits at `pos`, from the queue or (if the
+  // queue has not got them yet) from memory.
+  auto window_at = [&](uint32_t p) -> uint32_t {
+    const uint32_t c = p >> 5;
+    uint32_t c0 = queue[qidx(c)];
+    uint32_t c1 = queue[qidx(c + 1)];
+    const bool dry = c + 1u >= wq;
+    if (__builtin_amdgcn_ballot_w64(dry)) {
+      if (dry) {
+        c0 = chunk_mem(c);
+        c1 = chunk_mem(c + 1);
+        __asm__ volatile("" ::"v"(c0), "v"(c1));  // wait for the loads here, not at a later join
       }
-      stale = false;
-      // 2. stage the next pair, touch further ahead
-      s0 = chunk(tail);
-      s1 = chunk(tail + 1);
-      touch(tail + kTouch);
-      // 3. FP8 bytes of block + 3
+    }
+    const uint64_t w = ((uint64_t)c0 << 32) | c1;
+    return (uint32_t)(w >> (32u - (p & 31u)));
+  };
+
+  auto decode_block = [&](uint32_t (&q)[kDepth], uint32_t nvalid) {
 #pragma unroll
-      for (int j = 0; j < kDepth; ++j)
-        qr[(slot + kRing - 1) % kRing][j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, vlane, walk(wload), 0);
-      // 4. decode this block
+    for (int g = 0; g < kDepth; g += kG) {
+      uint32_t win = window_at(pos);
 #pragma unroll
-      for (int j = 0; j < kDepth; ++j) {
-        if (last && b0 + j == count) end_bit = bitpos();
-        if (j % kG == 0 && cnt < 32) pop();
-        decode_one(b0 + j, qr[slot][j]);
+      for (int j = g; j < g + kG; ++j) {
+        if ((uint32_t)j < nvalid) {
+          const uint32_t so = walk(ws);
+          const uint32_t idx = (q[j] << kL) | (win >> (32 - kL));
+          uint32_t ent = lut[idx];
+          const uint32_t len = (ent >> 16) & 7u;
+          win <<= len;
+          pos += len;
+          if ((int32_t)ent < 0) {
+            // ESC: the symbol is the next 16 raw bits.
+            ent = window_at(pos) >> 16;
+            pos += 16;
+            win = window_at(pos);
+          }
+          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)ent, r_out, 2u * lane, 2u * so, 0);
+        }
       }
     }
   };
-  constexpr int32_t kSpan = kRing * kDepth;
-  const int32_t last0 = ((count - 1) / kSpan) * kSpan;
-  for (int32_t i0 = 0; i0 < last0; i0 += kSpan) ring(i0, false);
-  ring(last0, true);
-  if (last0 + kSpan == count) end_bit = bitpos();
 
-  if (!parked || park_i >= count) {
-    if ((uint64_t)(parked ? park_bit : end_bit) != pos_end) flag(status, MPS_STATUS_DESYNC);
-    return;
-  }
-  // Parked lane: finish elements park_i.. with direct loads.
-  uint64_t pos = park_bit;
-  for (int32_t i = park_i; i < count; ++i) {
-    const int32_t r = i / P, p = i - r * P;
-    const uint32_t off = (uint32_t)s_rows[r] * m + (uint32_t)c0 + (uint32_t)(p * k_eff) + vlane;
-    const uint32_t q = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, off, 0, 0);
-    const uint32_t c = (uint32_t)(pos >> 5), sh = (uint32_t)(pos & 31u);
-    const uint64_t w = (((uint64_t)chunk(c) << 32) | chunk(c + 1)) << sh;  // >= 32 valid bits
-    const uint32_t ent = lut[(q << kL) | (uint32_t)(w >> (64 - kL))];
-    const int len = (int)((ent >> 16) & 7u);
-    pos += (uint32_t)len;
-    uint32_t sym = ent;
-    if ((int32_t)ent < 0) {
-      const uint32_t c2 = (uint32_t)(pos >> 5), sh2 = (uint32_t)(pos & 31u);
-      sym = (uint32_t)(((((uint64_t)chunk(c2) << 32) | chunk(c2 + 1)) << sh2) >> 48);
-      pos += 16;
+  auto block = [&](int slot, uint32_t nvalid) {
+    const int ps = slot;
+    // 1. the pair requested kRing blocks ago joins the queue
+    if (valid[ps]) {
+      queue[qidx(wq)] = inflight[ps].y;
+      queue[qidx(wq + 1)] = inflight[ps].x;
+      wq += 2;
     }
-    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sym, r_out, 2u * off, 0, 0);
+    // 2. request the next pair if fewer than kAhead chunks are queued ahead
+    const bool need = (int32_t)(rq - (pos >> 5)) < (int32_t)kAhead;
+    {
+      const uint32_t off = need ? rq * 4u : kBsPast;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r_bs, off, 0, 0);
+      inflight[ps] = make_uint2(v[0], v[1]);
+    }
+    valid[ps] = need;
+    rq += need ? 2u : 0u;
+    // 3. FP8 bytes kRing - 1 blocks ahead
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j)
+      qr[(slot + kRing - 1) % kRing][j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, lane, walk(wl), 0);
+    // 4. decode this block
+    decode_block(qr[slot], nvalid);
+  };
+
+  const uint32_t nfull = count / kDepth;
+  const uint32_t rem = count % kDepth;
+  uint32_t b0 = 0;
+  for (; b0 + kRing <= nfull; b0 += kRing) {
+#pragma unroll
+    for (int slot = 0; slot < kRing; ++slot) block(slot, kDepth);
+  }
+  // last round: remaining full blocks, then the partial block
+#pragma unroll
+  for (int slot = 0; slot < kRing; ++slot) {
+    const uint32_t bi = b0 + (uint32_t)slot;
+    if (bi < nfull) block(slot, kDepth);
+    else if (bi == nfull && rem) block(slot, rem);
   }
   if (pos != pos_end) flag(status, MPS_STATUS_DESYNC);
 }
 
-__device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b, uint32_t *lut, int32_t *s_gid,
-                                              int32_t *s_rows, int *s_bad, uint32_t *s_sink, uint32_t *status) {
+__device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b, uint32_t *lds, uint32_t *status) {
+  uint32_t *lut = lds;
+  uint32_t *qregion = lds + kLutWords;
+  int32_t *s_gid = reinterpret_cast<int32_t *>(qregion) + 7 * kBlock;   // queue slot 7 during set-up
+  int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;  // queue slot 6 (generic path)
+  int32_t *s_flag = reinterpret_cast<int32_t *>(qregion) + 5 * kBlock;  // queue slot 5 during set-up
   const int tid = threadIdx.x;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(T.decode_syms) & 15u) == 0) &&
                       ((reinterpret_cast<uintptr_t>(T.decode_lens) & 3u) == 0);
-  if (tid == 0) *s_bad = 0;
+  if (tid == 0) *s_flag = 0;
 
-  // fp8 byte -> table id, validated.
-  for (int i = tid; i < 256; i += kBlock) {
-    int32_t g = T.bucket_table[b * 256 + i];
-    if (g < -1 || g >= T.num_tables) {
-      flag(status, MPS_STATUS_BAD_TABLE);
-      g = -1;
-    }
-    s_gid[i] = g;
-  }
   const int32_t ra = T.bucket_row_offsets[b];
   const int32_t rb = T.bucket_row_offsets[b + 1];
   const int32_t c0 = T.bucket_col_start[b];
@@ -452,14 +431,73 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   const bool bucket_ok = ra >= 0 && rb >= ra && (int64_t)rb <= T.num_row_indices && rb - ra <= kRowsLds &&
                          cl > 0 && c0 >= 0 && (int64_t)c0 + cl <= T.m;
   const int32_t rows = bucket_ok ? rb - ra : 0;
-  __syncthreads();
-  for (int i = tid; i < rows; i += kBlock) {
-    const int32_t r = T.row_indices[ra + i];
-    if (r < 0 || r >= T.n) *s_bad = 1;
-    s_rows[i] = r;
-  }
+  const int64_t total = (int64_t)rows * cl;
+  const int32_t k_eff = (int32_t)(T.k < total ? T.k : (total > 0 ? total : 1));
+  const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
+  const bool fast = bucket_ok && rows <= 128 && cl % k_eff == 0 && nm <= (1ull << 29) &&
+                    (uint64_t)T.bitstream_words < 0x10000000ull;
+  const int lane = tid;
+  const bool active = bucket_ok && rows > 0 && lane < k_eff;
+  const uint32_t *sb = T.bucket_thread_startbit + b * (T.k + 1);
+  const uint64_t base = (uint64_t)T.bucket_bit_base[b];
 
-  // Expand the 256 tables into 32-bit LDS entries, 8 entries per work item.
+  // fp8 byte -> table id, validated.
+  bool bad_table = false;
+  for (int i = tid; i < 256; i += kBlock) {
+    int32_t g = T.bucket_table[b * 256 + i];
+    if (g < -1 || g >= T.num_tables) {
+      bad_table = true;
+      g = -1;
+    }
+    s_gid[i] = g;
+  }
+  if (bad_table) flag(status, MPS_STATUS_BAD_TABLE);
+
+  // Row offsets: fast path keeps rows 0..63 / 64..127 one per lane in VGPRs.
+  bool bad_row = false;
+  uint32_t rowoff_lo = 0, rowoff_hi = 0;
+  if (fast) {
+    const int wl = lane & 63;
+    if (wl < rows) {
+      const int32_t r = T.row_indices[ra + wl];
+      bad_row |= r < 0 || r >= T.n;
+      rowoff_lo = (uint32_t)r * (uint32_t)T.m + (uint32_t)c0;
+    }
+    if (wl + 64 < rows) {
+      const int32_t r = T.row_indices[ra + wl + 64];
+      bad_row |= r < 0 || r >= T.n;
+      rowoff_hi = (uint32_t)r * (uint32_t)T.m + (uint32_t)c0;
+    }
+  }
+  // First three bitstream pairs of this lane, loaded before the table set-up.
+  uint32_t pos = 0, pos_end = 0;
+  uint2 first[3] = {make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0)};
+  if (fast && active) {
+    pos = sb[lane];
+    pos_end = sb[lane + 1];
+    const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
+    const uint64_t base_byte = base >> 3;
+    const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+    const __amdgpu_buffer_rsrc_t r_bs = make_rsrc(
+        reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+    const uint32_t rq0 = (pos >> 5) & ~1u;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r_bs, (rq0 + 2 * i) * 4u, 0, 0);
+      first[i] = make_uint2(v[0], v[1]);
+    }
+  }
+  __syncthreads();
+  if (!fast) {
+    for (int i = tid; i < rows; i += kBlock) {
+      const int32_t r = T.row_indices[ra + i];
+      bad_row |= r < 0 || r >= T.n;
+      s_rows[i] = r;
+    }
+  }
+  if (bad_row) *s_flag = 1;
+
+  // Expand the 256 tables into 32-bit LDS entries {sym:16 | len:3 | ... | esc:1<<31}.
   for (int w = tid; w < 256 * (kTable / 8); w += kBlock) {
     const int f = w >> 4;
     const int part = w & 15;
@@ -494,47 +532,37 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
     dst[1] = make_uint4(e[4], e[5], e[6], e[7]);
   }
   __syncthreads();
+  const bool any_bad_row = *s_flag != 0;
+  __syncthreads();  // the flag's word belongs to the queue from here on
 
-  if (!bucket_ok || *s_bad) {
+  if (!bucket_ok || any_bad_row) {
     if (tid == 0) flag(status, !bucket_ok ? MPS_STATUS_BAD_BUCKET : MPS_STATUS_BAD_ROW);
     return;
   }
-  if (rows == 0) return;
-  const int64_t total = (int64_t)rows * cl;
-  const int32_t k_eff = (int32_t)(T.k < total ? T.k : total);
-  const int lane = tid;
-  if (lane >= k_eff) return;
-  const uint32_t *sb = T.bucket_thread_startbit + b * (T.k + 1);
-  const uint64_t base = (uint64_t)T.bucket_bit_base[b];
-  const uint64_t pos0 = base + sb[lane];
-  const uint64_t pos_end = base + sb[lane + 1];
-  const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
-  if (cl % k_eff == 0 && rows <= 128 && nm <= (1ull << 29) && (uint64_t)T.bitstream_words < 0x10000000ull)
-    decode_lane_rows(T, lut, s_rows, s_sink, lane, k_eff, rows, c0, cl / k_eff, pos0, pos_end, status);
-  else if (nm <= 0xFFFFFFFFull)
-    decode_lane<uint32_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pos_end, status);
-  else
-    decode_lane<uint64_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pos_end, status);
+  if (!active) return;
+  if (fast) {
+    decode_rows_fast(T, lut, qregion, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows, (uint32_t)(cl / k_eff),
+                     rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
+  } else {
+    const uint64_t pos0 = base + sb[lane];
+    const uint64_t pend = base + sb[lane + 1];
+    if (nm <= 0xFFFFFFFFull)
+      decode_lane<uint32_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
+    else
+      decode_lane<uint64_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
+  }
 }
 
 __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
-  __shared__ __attribute__((aligned(16))) uint32_t lut[256 * kTable];
-  __shared__ int32_t s_gid[256];
-  __shared__ int32_t s_rows[kRowsLds];
-  __shared__ int s_bad;
-  __shared__ uint32_t s_sink[64];
-  decode_bucket(T, blockIdx.x, lut, s_gid, s_rows, &s_bad, s_sink, status);
+  __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+  decode_bucket(T, blockIdx.x, lds, status);
 }
 
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
                                                           const WorkItem *__restrict__ work, uint32_t *status) {
-  __shared__ __attribute__((aligned(16))) uint32_t lut[256 * kTable];
-  __shared__ int32_t s_gid[256];
-  __shared__ int32_t s_rows[kRowsLds];
-  __shared__ int s_bad;
-  __shared__ uint32_t s_sink[64];
+  __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   const WorkItem w = work[blockIdx.x];
-  decode_bucket(tensors[w.tensor], w.bucket, lut, s_gid, s_rows, &s_bad, s_sink, status);
+  decode_bucket(tensors[w.tensor], w.bucket, lds, status);
 }
 
 int check_tensor(const mps_fp8_tensor *t) {
@@ -669,7 +697,7 @@ int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream) {
 int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes) {
   if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
   if (work_items) *work_items = plan->work_items;
-  if (lds_bytes) *lds_bytes = (int64_t)(256 * kTable * 4 + 256 * 4 + kRowsLds * 4);
+  if (lds_bytes) *lds_bytes = (int64_t)kLdsWords * 4;
   return MPS_OK;
 }
 
