@@ -21,6 +21,7 @@
 #include <cstdint>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "mps_common.h"
@@ -34,7 +35,9 @@ constexpr int kTable = 1 << kL;           // 128 entries per code table
 constexpr int kPacked = kTable / 2;       // 64 bytes of packed 4-bit lengths
 constexpr int kBlock = 1024;              // work-items per bucket workgroup (>= k)
 constexpr int kRowsLds = 256;             // row indices staged in LDS
-constexpr uint32_t kEscBit = 1u << 31;
+// LDS code table entry: sym << 16 | esc << 4 | len. A shift by the whole entry
+// shifts by len (its low 5 bits), and a 16-bit store of the high half stores sym.
+constexpr uint32_t kEscBit = 1u << 4;
 constexpr int kMaxDevices = 64;
 
 // Integrity flags go to a per-device status word passed to every launch.
@@ -159,10 +162,10 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, const uint3
   auto decode_one = [&](uint32_t q, Idx idx) {
     const uint32_t peek = (uint32_t)(buf >> (64 - kL));
     const uint32_t ent = lut[(q << kL) | peek];
-    const int len = (int)((ent >> 16) & 7u);
+    const int len = (int)(ent & 7u);
     buf <<= len;
     cnt -= len;
-    uint32_t sym = ent & 0xFFFFu;
+    uint32_t sym = ent >> 16;
     if (ent & kEscBit) {
       sym = (uint32_t)(buf >> 48);
       buf <<= 16;
@@ -248,11 +251,12 @@ constexpr int kQSlots = 8;                 // LDS queue depth (chunks per lane)
 constexpr uint32_t kPast = 0x40000000u;    // offset beyond every fast-path buffer (2*n*m <= 2^30)
 constexpr uint32_t kBsPast = 0x80000000u;  // bitstream offset beyond every bucket's range
 
-// LDS: 256 tables x 128 u32 entries, then the queue (kQSlots x kBlock u32).
-// During set-up the queue region also holds the fp8 -> table map; the generic
-// path keeps the bucket's row indices there.
+// LDS: the queue (kQSlots x kBlock u32) at offset 0, then 256 tables x 128 u32
+// entries. During set-up the queue region also holds the fp8 -> table map; the
+// generic path keeps the bucket's row indices there.
+constexpr int kQWords = kQSlots * kBlock;
 constexpr int kLutWords = 256 * kTable;
-constexpr int kLdsWords = kLutWords + kQSlots * kBlock;
+constexpr int kLdsWords = kQWords + kLutWords;
 
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 
@@ -356,16 +360,17 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, const 
           const uint32_t so = walk(ws);
           const uint32_t idx = (q[j] << kL) | (win >> (32 - kL));
           uint32_t ent = lut[idx];
-          const uint32_t len = (ent >> 16) & 7u;
+          const uint32_t len = ent & 7u;
           win <<= len;
           pos += len;
-          if ((int32_t)ent < 0) {
+          uint32_t sym = ent >> 16;
+          if (ent & kEscBit) {
             // ESC: the symbol is the next 16 raw bits.
-            ent = window_at(pos) >> 16;
+            sym = window_at(pos) >> 16;
             pos += 16;
             win = window_at(pos);
           }
-          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)ent, r_out, 2u * lane, 2u * so, 0);
+          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)sym, r_out, 2u * lane, 2u * so, 0);
         }
       }
     }
@@ -413,16 +418,240 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, const 
   if (pos != pos_end) flag(status, MPS_STATUS_DESYNC);
 }
 
+// ---------------------------------------------------------------------------
+// k = 1024 path: every bucket of a checkpoint written with the compress CLI's
+// default of 1024 substreams, whose column range is a multiple of 1024 (every
+// Llama linear). Lane t's i-th element is row i / P, column c0 + t + (i % P) *
+// 1024 (P = col_len / 1024), so a row splits into P / G blocks of G elements
+// that share one scalar offset: element j of a block is at voffset lane + j *
+// 1024 (BF16: 2 * lane + j * 2048), the block offset goes in soffset and the
+// j-dependent part in the 12-bit immediate. The walk costs a few scalar
+// instructions per block and none per element.
+//
+// A step is S blocks (S * G <= 8 elements). Each step: the bitstream pair
+// requested R steps earlier joins the lane's LDS queue, a new pair is
+// requested if fewer than kAhead chunks are queued ahead, the FP8 bytes of the
+// step R - 1 ahead are loaded, and the step is decoded. Every step issues the
+// same memory instructions, so the in-order vmcnt waits stay static.
+//
+// Queue indices are biased by two chunks: queue chunk h holds stream chunk
+// h - 2 and bit position p is kept as p + 64, so a bitstream word (a pair of
+// chunks) starts at an even h and fills queue slots 2i and 2i + 1. The 32-bit
+// window at biased position p is alignbit(Q[(p-1)/32], Q[(p-1)/32 + 1], -p),
+// whose shift (-p) & 31 is exact for every p (for p % 32 == 0 it selects the
+// second chunk whole, and the first may be anything).
+//
+// Without ESC codes a window of 32 bits covers 4 codes of <= 7 bits: the
+// decode shifts the window by the table entry itself (its low bits are the
+// length) and sums the entries, whose low halves sum to the bits consumed. A
+// step first checks (one ballot) that every lane has the bits of the whole
+// step queued; otherwise that step reads windows through the checked path,
+// which falls back to memory. Buckets with ESC tables use the checked path
+// throughout and track the position per code.
+// ---------------------------------------------------------------------------
+template <int G, bool kEsc>
+__device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+                                             uint32_t *__restrict__ queue, uint32_t lane, uint32_t rows,
+                                             uint32_t P, uint32_t rowoff_lo, uint32_t rowoff_hi,
+                                             uint64_t bucket_bit, const uint2 (&first)[3], uint32_t pos,
+                                             uint32_t pos_end, uint32_t *status) {
+  constexpr uint32_t K = 1024;
+  constexpr int S = G >= 8 ? 1 : 8 / G;  // blocks per step
+  constexpr int SG = S * G;              // elements per step
+  constexpr int R = 4;                   // steps in flight
+  constexpr int kLastW = G - 4 * ((G - 1) / 4);                // codes in a block's last window
+  constexpr uint32_t kNeed = 7u * (uint32_t)(SG - kLastW) + 32u;  // bits a step may need queued
+  rows = uni(rows);
+  P = uni(P);
+  bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
+  const uint32_t NB = P / (uint32_t)G;
+  const uint32_t nblocks = rows * NB;
+  const uint32_t nsteps = (nblocks + S - 1) / S;
+  const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
+  const uint64_t base_byte = bucket_bit >> 3;
+  const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+  const __amdgpu_buffer_rsrc_t r_bs =
+      make_rsrc(reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+  const uint32_t lane4 = lane << 2;
+  const char *qbytes = reinterpret_cast<const char *>(queue);
+  const __amdgpu_buffer_rsrc_t r_fp8 = make_rsrc(T.fp8, (uint32_t)(T.n * T.m));
+
+  // Window at biased position p from the queue (its chunks must be there).
+  auto window_q = [&](uint32_t p) -> uint32_t {
+    const uint32_t a0 = (((p << 7) - 128u) & 0x7000u) | lane4;
+    const uint32_t a1 = (((p << 7) + 3968u) & 0x7000u) | lane4;
+    const uint32_t c0 = *reinterpret_cast<const uint32_t *>(qbytes + a0);
+    const uint32_t c1 = *reinterpret_cast<const uint32_t *>(qbytes + a1);
+    return __builtin_amdgcn_alignbit(c0, c1, 0u - p);
+  };
+  // Biased chunk h straight from memory (h < 2 reads out of range: zeros).
+  auto chunk_mem = [&](uint32_t h) -> uint32_t {
+    return __builtin_amdgcn_raw_buffer_load_b32(r_bs, ((h - 2u) ^ 1u) << 2, 0, 0);
+  };
+  uint32_t wq;  // queue chunks below wq are (or were) written
+  auto window_chk = [&](uint32_t p) -> uint32_t {
+    uint32_t w = window_q(p);
+    const uint32_t h = (p - 1u) >> 5;
+    const bool dry = h + 1u >= wq;
+    if (__builtin_amdgcn_ballot_w64(dry)) {
+      if (dry) {
+        w = __builtin_amdgcn_alignbit(chunk_mem(h), chunk_mem(h + 1u), 0u - p);
+        __asm__ volatile("" ::"v"(w));  // wait for the loads here, not at a later join
+      }
+    }
+    return w;
+  };
+  // Write the pair whose first (biased, even) chunk is h: slots h & 7 and h & 7 | 1.
+  auto put_pair = [&](uint32_t h, uint32_t hi, uint32_t lo) {
+    uint32_t *slot = queue + (((h & (kQSlots - 1)) << 10) | lane);
+    slot[0] = hi;  // the high half of a bitstream word is its first chunk
+    slot[K] = lo;
+  };
+
+  // Initial queue: the three pairs loaded during set-up.
+  const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
+  uint32_t rq = rq0 + 6;  // next pair to request (biased index of its first chunk)
+  wq = rq0 + 6;
+  uint32_t pb = pos + 64u;
+
+  // Uniform block walker: element offset of the next block, clamped to the last one.
+  auto row_offset = [&](uint32_t r) -> uint32_t {
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_lo, (int)(r & 63u));
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_hi, (int)(r & 63u));
+    return r < 64u ? a : b;
+  };
+  // Branch-free (scalar selects): a taken branch costs the wave an instruction refetch.
+  uint32_t w_blk = 0, w_row = 0;
+  uint32_t w_rowoff = row_offset(0);
+  auto walk = [&]() -> uint32_t {
+    const uint32_t off = w_rowoff + w_blk * (uint32_t)(G * K);
+    const bool wrap = w_blk + 1u == NB;
+    const bool more = w_row + 1u < rows;
+    const uint32_t next_row = w_row + ((wrap && more) ? 1u : 0u);
+    const uint32_t next_off = row_offset(next_row);
+    // past the last block the walk stays on it (its loads are in bounds)
+    w_blk = wrap ? (more ? 0u : w_blk) : w_blk + 1u;
+    w_rowoff = next_row != w_row ? next_off : w_rowoff;
+    w_row = next_row;
+    return off;
+  };
+
+  uint32_t qr[R][SG];
+  uint32_t so[R][S];
+  uint2 infl[R];
+  bool valid[R];
+  auto load_step = [&](int s) {
+#pragma unroll
+    for (int b = 0; b < S; ++b) {
+      so[s][b] = walk();
+#pragma unroll
+      for (int j = 0; j < G; ++j)
+        qr[s][b * G + j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, lane + (uint32_t)j * K, so[s][b], 0);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < R; ++s) {
+    valid[s] = false;
+    infl[s] = make_uint2(0u, 0u);
+  }
+#pragma unroll
+  for (int s = 0; s < R - 1; ++s) load_step(s);
+
+  // Decode block b of ring slot s. Entries are {sym << 16 | esc << 4 | len};
+  // the store writes the high half. Unchecked: the window position advances
+  // in pw by whole entries (only its low 16 bits are the position) and pb is
+  // brought up to date once per step.
+  auto decode_block = [&](auto chk, int s, int b, uint32_t &pw) {
+    constexpr bool kChk = decltype(chk)::value;
+    uint16_t *dst = T.out + so[s][b];
+#pragma unroll
+    for (int g = 0; g < G; g += 4) {
+      uint32_t win = kChk ? window_chk(pb) : window_q(pw);
+#pragma unroll
+      for (int j = g; j < (g + 4 < G ? g + 4 : G); ++j) {
+        const uint32_t q = qr[s][b * G + j];
+        __builtin_assume(q < 256u);  // buffer_load_ubyte zero-extends
+        uint32_t ent = lut[(q << kL) | (win >> (32 - kL))];
+        if constexpr (!kEsc) {
+          win <<= ent;
+          if constexpr (kChk) pb += ent & 7u;
+          else pw += ent;
+        } else {
+          const uint32_t len = ent & 7u;
+          win <<= len;
+          pb += len;
+          if (__builtin_amdgcn_ballot_w64((ent & kEscBit) != 0u)) {
+            if (ent & kEscBit) {
+              // ESC: the symbol is the next 16 raw bits (the window's high half).
+              ent = window_chk(pb);
+              pb += 16;
+              win = window_chk(pb);
+            }
+          }
+        }
+        dst[lane + (uint32_t)j * K] = (uint16_t)(ent >> 16);
+      }
+    }
+  };
+
+  auto step = [&](int slot, uint32_t si) {
+    // 1. the pair requested R steps ago joins the queue
+    if (valid[slot]) {
+      put_pair(wq, infl[slot].y, infl[slot].x);
+      wq += 2;
+    }
+    // 2. request the next pair if fewer than kAhead chunks are queued ahead
+    const bool need = (int32_t)(rq - (pb >> 5)) < (int32_t)kAhead;
+    {
+      const uint32_t off = need ? (rq - 2u) * 4u : kBsPast;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r_bs, off, 0, 0);
+      infl[slot] = make_uint2(v[0], v[1]);
+    }
+    valid[slot] = need;
+    rq += need ? 2u : 0u;
+    // 3. FP8 bytes R - 1 steps ahead
+    load_step((slot + R - 1) % R);
+    // 4. decode this step
+    if (si < nsteps) {
+      bool chk = kEsc;
+      if constexpr (!kEsc) chk = __builtin_amdgcn_ballot_w64((wq << 5) < pb + kNeed) != 0;
+      if (chk) {
+        uint32_t pw = 0;
+#pragma unroll
+        for (int b = 0; b < S; ++b)
+          if (S == 1 || si * S + (uint32_t)b < nblocks) decode_block(std::true_type{}, slot, b, pw);
+      } else {
+        uint32_t pw = pb;
+#pragma unroll
+        for (int b = 0; b < S; ++b)
+          if (S == 1 || si * S + (uint32_t)b < nblocks) decode_block(std::false_type{}, slot, b, pw);
+        pb += (pw - pb) & 0xFFFFu;
+      }
+    }
+  };
+
+  for (uint32_t s0 = 0; s0 < nsteps; s0 += R) {
+#pragma unroll
+    for (int slot = 0; slot < R; ++slot) step(slot, s0 + (uint32_t)slot);
+  }
+  if (pb - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
+}
+
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b, uint32_t *lds, uint32_t *status) {
-  uint32_t *lut = lds;
-  uint32_t *qregion = lds + kLutWords;
+  uint32_t *qregion = lds;
+  uint32_t *lut = lds + kQWords;
   int32_t *s_gid = reinterpret_cast<int32_t *>(qregion) + 7 * kBlock;   // queue slot 7 during set-up
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;  // queue slot 6 (generic path)
   int32_t *s_flag = reinterpret_cast<int32_t *>(qregion) + 5 * kBlock;  // queue slot 5 during set-up
   const int tid = threadIdx.x;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(T.decode_syms) & 15u) == 0) &&
                       ((reinterpret_cast<uintptr_t>(T.decode_lens) & 3u) == 0);
-  if (tid == 0) *s_flag = 0;
+  if (tid == 0) {
+    s_flag[0] = 0;  // a row index out of range
+    s_flag[1] = 0;  // some table of the bucket has an ESC entry
+  }
 
   const int32_t ra = T.bucket_row_offsets[b];
   const int32_t rb = T.bucket_row_offsets[b + 1];
@@ -434,8 +663,11 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   const int64_t total = (int64_t)rows * cl;
   const int32_t k_eff = (int32_t)(T.k < total ? T.k : (total > 0 ? total : 1));
   const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
-  const bool fast = bucket_ok && rows <= 128 && cl % k_eff == 0 && nm <= (1ull << 29) &&
-                    (uint64_t)T.bitstream_words < 0x10000000ull;
+  const bool small_stream = (uint64_t)T.bitstream_words < 0x10000000ull;
+  // k = 1024 path (any tensor below 2^31 elements) and the general fast path.
+  const bool k1024 = bucket_ok && rows <= 128 && k_eff == 1024 && cl % 1024 == 0 && nm < (1ull << 31) &&
+                     small_stream;
+  const bool fast = !k1024 && bucket_ok && rows <= 128 && cl % k_eff == 0 && nm <= (1ull << 29) && small_stream;
   const int lane = tid;
   const bool active = bucket_ok && rows > 0 && lane < k_eff;
   const uint32_t *sb = T.bucket_thread_startbit + b * (T.k + 1);
@@ -453,10 +685,10 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   }
   if (bad_table) flag(status, MPS_STATUS_BAD_TABLE);
 
-  // Row offsets: fast path keeps rows 0..63 / 64..127 one per lane in VGPRs.
+  // Row offsets: the fast paths keep rows 0..63 / 64..127 one per lane in VGPRs.
   bool bad_row = false;
   uint32_t rowoff_lo = 0, rowoff_hi = 0;
-  if (fast) {
+  if (k1024 || fast) {
     const int wl = lane & 63;
     if (wl < rows) {
       const int32_t r = T.row_indices[ra + wl];
@@ -472,7 +704,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   // First three bitstream pairs of this lane, loaded before the table set-up.
   uint32_t pos = 0, pos_end = 0;
   uint2 first[3] = {make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0)};
-  if (fast && active) {
+  if ((k1024 || fast) && active) {
     pos = sb[lane];
     pos_end = sb[lane + 1];
     const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
@@ -488,7 +720,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
     }
   }
   __syncthreads();
-  if (!fast) {
+  if (!k1024 && !fast) {
     for (int i = tid; i < rows; i += kBlock) {
       const int32_t r = T.row_indices[ra + i];
       bad_row |= r < 0 || r >= T.n;
@@ -497,7 +729,8 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   }
   if (bad_row) *s_flag = 1;
 
-  // Expand the 256 tables into 32-bit LDS entries {sym:16 | len:3 | ... | esc:1<<31}.
+  // Expand the 256 tables into 32-bit LDS entries {sym:16 | len:3 << 16 | esc << 20}.
+  uint32_t esc_seen = 0;
   for (int w = tid; w < 256 * (kTable / 8); w += kBlock) {
     const int f = w >> 4;
     const int part = w & 15;
@@ -521,18 +754,21 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
 #pragma unroll
       for (int j = 0; j < 8; ++j) syms[j] = 0;
     }
+    esc_seen |= nibs & 0x88888888u;
     uint32_t e[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t nib = (nibs >> (4 * j)) & 0xFu;
-      e[j] = syms[j] | ((nib & 7u) << 16) | ((nib & 8u) ? kEscBit : 0u);
+      e[j] = (syms[j] << 16) | (nib & 7u) | ((nib & 8u) ? kEscBit : 0u);
     }
     uint4 *dst = reinterpret_cast<uint4 *>(lut + f * kTable + part * 8);
     dst[0] = make_uint4(e[0], e[1], e[2], e[3]);
     dst[1] = make_uint4(e[4], e[5], e[6], e[7]);
   }
+  if (esc_seen) atomicOr(reinterpret_cast<uint32_t *>(s_flag) + 1, 1u);
   __syncthreads();
-  const bool any_bad_row = *s_flag != 0;
+  const bool has_esc = s_flag[1] != 0;
+  const bool any_bad_row = s_flag[0] != 0;
   __syncthreads();  // the flag's word belongs to the queue from here on
 
   if (!bucket_ok || any_bad_row) {
@@ -540,7 +776,24 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
     return;
   }
   if (!active) return;
-  if (fast) {
+  if (k1024) {
+    const uint32_t P = (uint32_t)cl / 1024u;
+#define MPS_K1024(GG)                                                                                         \
+  do {                                                                                                        \
+    if (has_esc)                                                                                              \
+      decode_k1024<GG, true>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base,  \
+                             first, pos, pos_end, status);                                                    \
+    else                                                                                                      \
+      decode_k1024<GG, false>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, \
+                              first, pos, pos_end, status);                                                   \
+  } while (0)
+    if (P % 8 == 0) MPS_K1024(8);
+    else if (P % 7 == 0) MPS_K1024(7);
+    else if (P % 4 == 0) MPS_K1024(4);
+    else if (P % 2 == 0) MPS_K1024(2);
+    else MPS_K1024(1);
+#undef MPS_K1024
+  } else if (fast) {
     decode_rows_fast(T, lut, qregion, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows, (uint32_t)(cl / k_eff),
                      rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
   } else {

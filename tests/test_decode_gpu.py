@@ -53,6 +53,40 @@ def test_decode_roundtrip_per_row(n, m, k, seed):
     assert _status() == 0
 
 
+@pytest.mark.parametrize("n,m,seed", [
+    (130, 1024, 100),    # P = 1 column block per row -> G = 1
+    (96, 2048, 101),     # P = 2 -> G = 2
+    (70, 3072, 102),     # P = 3 -> G = 1
+    (200, 4096, 103),    # P = 4 -> G = 4
+    (40, 7168, 104),     # P = 7 -> G = 7
+    (33, 8192, 105),     # P = 8 -> G = 8
+    (20, 14336, 106),    # P = 14 -> G = 7 (down_proj rows)
+    (9, 16384, 107),     # P = 16 -> G = 8
+    (3, 28672, 108),     # P = 28 -> G = 7 (70B down_proj rows)
+])
+def test_decode_k1024_block_sizes(n, m, seed):
+    """The k = 1024 path walks a row in blocks of G | P elements; every G it picks."""
+    bf, q, sc_u16 = synth(n, m, seed=seed)
+    sc = oracle.encode(bf, q, sc_u16, 7, 1024)
+    _status()
+    got = _gpu_decode(sc, q)
+    assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
+    assert _status() == 0
+
+
+@pytest.mark.parametrize("n,m,seed", [(40, 2048, 110), (48, 4096, 111), (30, 7168, 112), (17, 8192, 113),
+                                      (12, 3072, 114)])
+def test_decode_k1024_esc(n, m, seed):
+    """ESC buckets on the k = 1024 path: lossless, and the lane ends where the next begins."""
+    bf, q, scales = _esc_inputs(n, m, seed)
+    sc, stats = oracle.encode(bf, q, scales, 7, 1024, with_stats=True)
+    assert stats["esc_keys"] >= 1 and stats["esc_elements"] > 0 and stats["esc_collisions"] == 0
+    _status()
+    got = _gpu_decode(sc, q)
+    assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
+    assert _status() == 0
+
+
 def test_decode_scalar_scale_many_buckets():
     n, m = 1000, 640
     bf, q, sc_u16 = synth(n, m, seed=11)
