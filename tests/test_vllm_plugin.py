@@ -1,0 +1,193 @@
+"""The vLLM fp8_huffman surface, driven through a stand-in vLLM (tests/fakes/vllm).
+
+Covers the reference plugin's contract (scripts/mpserve_vllm_fp8_huffman.py):
+config keys, defaults and the env gate (:95-148), the thirteen huff_* params
+and their loaders with the shard map (:155-360), and apply() (:389-665) on the
+GPU, where a merged qkv layer must reproduce x @ W.T for the exact BF16 weights.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+FAKES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "fakes")
+if FAKES not in sys.path:
+    sys.path.insert(0, FAKES)
+
+import oracle  # noqa: E402
+from tests.helpers import synth  # noqa: E402
+
+vfh = pytest.importorskip("mpserve_amd.vllm_fp8_huffman")
+from vllm.model_executor.layers.linear import LinearBase, UnquantizedLinearMethod  # noqa: E402
+from vllm.model_executor.layers.quantization import REGISTRY  # noqa: E402
+
+
+def stored_sidecar(bf, q, sc, k=1024):
+    """Sidecar tensors as the compress script stores them (signed dtypes, huff_ names)."""
+    s = oracle.encode(bf, q, sc, 7, k)
+    t = {
+        "huff_fp8_u8": torch.from_numpy(np.ascontiguousarray(q)),
+        "huff_bitstream_u64": torch.from_numpy(s["bitstream_u64"].view(np.int64)),
+        "huff_decode_syms_u16": torch.from_numpy(s["decode_syms_u16"].view(np.int16)),
+        "huff_decode_lens_u8": torch.from_numpy(s["decode_lens_u8"]),
+        "huff_bucket_table_i32": torch.from_numpy(s["bucket_table_i32"]),
+        "huff_bucket_col_start_i32": torch.from_numpy(s["bucket_col_start_i32"]),
+        "huff_bucket_col_len_i32": torch.from_numpy(s["bucket_col_len_i32"]),
+        "huff_bucket_row_offsets_i32": torch.from_numpy(s["bucket_row_offsets_i32"]),
+        "huff_row_indices_i32": torch.from_numpy(s["row_indices_i32"]),
+        "huff_bucket_thread_startbit_u32": torch.from_numpy(s["bucket_thread_startbit_u32"].view(np.int32)),
+        "huff_bucket_bit_base_i64": torch.from_numpy(s["bucket_bit_base_i64"]),
+        "huff_attn_block_row_start_i32": torch.empty((0,), dtype=torch.int32),
+        "huff_attn_block_row_len_i32": torch.empty((0,), dtype=torch.int32),
+    }
+    return t
+
+
+def make_layer(prefix, out_sizes, k):
+    layer = LinearBase(prefix)
+    cfg = vfh.FP8HuffmanConfig.from_config({"max_len": 7})
+    cfg._enabled = True
+    method = cfg.get_quant_method(layer, prefix)
+    assert isinstance(method, vfh.FP8HuffmanLinearMethod)
+    method.create_weights(layer, k, list(out_sizes), k, sum(out_sizes), torch.bfloat16)
+    layer.quant_method = method
+    return layer, method
+
+
+def load(layer, tensors, shard_id=None):
+    for name, t in tensors.items():
+        p = getattr(layer, name)
+        if shard_id is None:
+            p.weight_loader(p, t)
+        else:
+            p.weight_loader(p, t, shard_id)
+
+
+# ---------------------------------------------------------------------------- CPU
+def test_config_surface(monkeypatch):
+    assert REGISTRY["fp8_huffman"] is vfh.FP8HuffmanConfig
+    cfg = vfh.FP8HuffmanConfig.from_config({"max_len": 7, "include_regex": r"self_attn"})
+    assert cfg.get_name() == "fp8_huffman"
+    assert cfg.get_supported_act_dtypes() == [torch.half, torch.bfloat16]
+    assert vfh.FP8HuffmanConfig.get_min_capability() == 90
+    assert vfh.FP8HuffmanConfig.get_config_filenames() == []
+    with pytest.raises(ValueError, match="requires max_len=7"):
+        vfh.FP8HuffmanConfig(max_len=12)
+    # from_config leaves ignore_regex None unless given; the constructor default ignores lm_head & co
+    assert vfh.FP8HuffmanConfig().ignore_regex == vfh.DEFAULT_IGNORE
+
+
+def test_env_gate_and_regex_filters(monkeypatch):
+    lin = LinearBase("model.layers.0.self_attn.qkv_proj")
+    monkeypatch.delenv("MPSERVE_ENABLE_FP8_HUFFMAN", raising=False)
+    assert isinstance(vfh.FP8HuffmanConfig().get_quant_method(lin, lin.prefix), UnquantizedLinearMethod)
+    monkeypatch.setenv("MPSERVE_ENABLE_FP8_HUFFMAN", "1")
+    cfg = vfh.FP8HuffmanConfig(include_regex=r"self_attn")
+    assert isinstance(cfg.get_quant_method(lin, lin.prefix), vfh.FP8HuffmanLinearMethod)
+    mlp = LinearBase("model.layers.0.mlp.gate_up_proj")
+    assert isinstance(cfg.get_quant_method(mlp, mlp.prefix), UnquantizedLinearMethod)
+    head = LinearBase("lm_head")
+    assert isinstance(vfh.FP8HuffmanConfig().get_quant_method(head, "lm_head"), UnquantizedLinearMethod)
+    assert vfh.FP8HuffmanConfig().get_quant_method(torch.nn.Linear(2, 2), "x") is None
+
+
+def test_create_weights_registers_reference_params():
+    layer, _ = make_layer("model.layers.0.self_attn.o_proj", [64], 32)
+    names = dict(layer.named_parameters())
+    for name, dt in vfh.HUFF_PARAMS:
+        assert names[name].dtype == dt, name
+    assert names["huff_attn_block_row_start_i32"].numel() == 0
+    assert names["weight"].dtype == torch.uint8
+    assert names["weight_scale_inv"].dtype == torch.float16 and names["weight_scale"].dtype == torch.float16
+    assert int(layer.huff_max_len) == 7 and int(layer.huff_in_features_i32) == 32
+    assert int(layer.huff_out_features_i32) == 64
+    assert "huff_max_len" not in layer.state_dict()  # non-persistent buffers
+
+
+def test_tp_greater_than_one_is_rejected():
+    layer = LinearBase("x")
+    layer.tp_size = 2
+    m = vfh.FP8HuffmanLinearMethod(vfh.FP8HuffmanParams())
+    with pytest.raises(NotImplementedError, match="tp_size=1"):
+        m.create_weights(layer, 8, [8], 8, 8, torch.bfloat16)
+
+
+def test_loaders_unsharded_and_sharded():
+    bf, q, sc = synth(40, 64, seed=1)
+    t = stored_sidecar(bf, q, sc, 64)
+    layer, method = make_layer("model.layers.0.self_attn.o_proj", [40], 64)
+    load(layer, t)
+    assert torch.equal(layer.huff_fp8_u8.data.cpu(), t["huff_fp8_u8"])
+    layer.weight.weight_loader(layer.weight, torch.ones(3))  # discarded
+    assert layer.weight.numel() == 1
+
+    merged, _ = make_layer("model.layers.0.self_attn.qkv_proj", [40, 8, 8], 64)
+    for sid in ("q", "k", "v"):
+        load(merged, t, sid)
+    assert sorted(merged._huff_fp8_u8_shards) == [0, 1, 2]
+    with pytest.raises(ValueError, match="Unknown shard_id"):
+        merged.huff_fp8_u8.weight_loader(merged.huff_fp8_u8, t["huff_fp8_u8"], "o")
+    method.process_weights_after_loading(layer)
+    assert isinstance(layer.huff_fp8_u8, torch.nn.Parameter)
+    assert vfh._PREFIX_TO_LAYER["model.layers.0.self_attn.o_proj"] is layer
+
+
+def test_apply_rejects_cpu_and_bad_dtypes():
+    layer, method = make_layer("p", [8], 8)
+    with pytest.raises(ValueError, match="requires CUDA tensors"):
+        method.apply(layer, torch.zeros(2, 8, dtype=torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------- GPU
+DEV = "cuda:0"
+
+
+def _to(tensors, dev):
+    return {k: v.to(dev) for k, v in tensors.items()}
+
+
+@pytest.mark.gpu
+def test_apply_merged_qkv_matches_exact_weights():
+    k = 2048
+    parts = [synth(256, k, seed=200), synth(64, k, seed=201), synth(64, k, seed=202)]
+    layer, method = make_layer("model.layers.3.self_attn.qkv_proj", [256, 64, 64], k)
+    for sid, (bf, q, sc) in zip(("q", "k", "v"), parts):
+        load(layer, _to(stored_sidecar(bf, q, sc), DEV), sid)
+    method.process_weights_after_loading(layer)
+    w = torch.from_numpy(np.concatenate([p[0] for p in parts])).view(torch.bfloat16).to(DEV)
+    got_w = method.decoded_weight(layer, k)
+    torch.cuda.synchronize()
+    assert torch.equal(got_w.view(torch.uint16), w.view(torch.uint16))
+    g = torch.Generator(device="cpu").manual_seed(5)
+    for t in (1, 16, 128):
+        x = torch.randn((t, k), generator=g).to(torch.bfloat16).to(DEV)
+        bias = torch.randn(384, generator=g).to(torch.bfloat16).to(DEV)
+        out = method.apply(layer, x, bias)
+        ref = torch.matmul(x, w.t()) + bias
+        assert out.shape == (t, 384)
+        assert torch.allclose(out.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    x16 = torch.randn((4, k), generator=g).to(torch.float16).to(DEV)
+    out16 = method.apply(layer, x16)
+    assert out16.dtype == torch.float16
+    assert torch.allclose(out16.float(), torch.matmul(x16, w.to(torch.float16).t()).float(), rtol=1e-2, atol=1e-2)
+    empty = method.apply(layer, torch.empty((0, k), dtype=torch.bfloat16, device=DEV))
+    assert empty.shape == (0, 384)
+
+
+@pytest.mark.gpu
+def test_prefetch_on_side_stream():
+    k = 1024
+    bf, q, sc = synth(512, k, seed=210)
+    layer, method = make_layer("model.layers.0.self_attn.o_proj", [512], k)
+    load(layer, _to(stored_sidecar(bf, q, sc), DEV))
+    method.process_weights_after_loading(layer)
+    w = torch.from_numpy(bf).view(torch.bfloat16).to(DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    method.prefetch(layer, k, side, slot=1)
+    x = torch.randn((8, k), device=DEV).to(torch.bfloat16)
+    out = method.apply(layer, x)
+    torch.cuda.synchronize()
+    assert torch.allclose(out.float(), torch.matmul(x, w.t()).float(), rtol=1e-2, atol=1e-2)
