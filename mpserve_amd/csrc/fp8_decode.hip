@@ -250,6 +250,7 @@ constexpr uint32_t kAhead = 7;             // request while fewer chunks than th
 constexpr int kQSlots = 8;                 // LDS queue depth (chunks per lane)
 constexpr uint32_t kPast = 0x40000000u;    // offset beyond every fast-path buffer (2*n*m <= 2^30)
 constexpr uint32_t kBsPast = 0x80000000u;  // bitstream offset beyond every bucket's range
+constexpr uint32_t kSlabPast = 0xFFFFFFF0u;  // BF16 byte offset beyond every k = 1024 output (2*n*m < 2^32 - 16)
 
 // LDS: the queue (kQSlots x kBlock u32) at offset 0, then 256 tables x 128 u32
 // entries. During set-up the queue region also holds the fp8 -> table map; the
@@ -451,8 +452,8 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, const 
 // ---------------------------------------------------------------------------
 template <int G, bool kEsc>
 __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
-                                             uint32_t *__restrict__ queue, uint32_t lane, uint32_t rows,
-                                             uint32_t P, uint32_t rowoff_lo, uint32_t rowoff_hi,
+                                             uint32_t *__restrict__ queue, uint32_t lane, uint32_t col,
+                                             uint32_t rows, uint32_t P, uint32_t rowoff_lo, uint32_t rowoff_hi,
                                              uint64_t bucket_bit, const uint2 (&first)[3], uint32_t pos,
                                              uint32_t pos_end, uint32_t *status) {
   constexpr uint32_t K = 1024;
@@ -548,7 +549,7 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
       so[s][b] = walk();
 #pragma unroll
       for (int j = 0; j < G; ++j)
-        qr[s][b * G + j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, lane + (uint32_t)j * K, so[s][b], 0);
+        qr[s][b * G + j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, col + (uint32_t)j * K, so[s][b], 0);
     }
   };
 #pragma unroll
@@ -591,7 +592,7 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
             }
           }
         }
-        dst[lane + (uint32_t)j * K] = (uint16_t)(ent >> 16);
+        dst[col + (uint32_t)j * K] = (uint16_t)(ent >> 16);
       }
     }
   };
@@ -639,6 +640,226 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
   if (pb - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
 }
 
+// ---------------------------------------------------------------------------
+// k = 1024, col_len = P * 1024 with P >= 4, no ESC entry in the bucket's
+// tables (every bucket of a Llama-shaped checkpoint).
+//
+// Element i of a substream lives in slab i: the 1024 columns
+// [c0 + 1024 (i % P), +1024) of the bucket's row i / P. Lane l of wave w,
+// in 16-lane row R = l / 16 at position v = l % 16, decodes substream
+// (column) t = 64w + 4v + R, four elements (one "group", slabs 4g..4g+3) at a
+// time. Per group and wave:
+//  - FP8: lane (R, v) loads the dword of slab 4g+R at columns 64w+4v..+3, so
+//    each 16-lane row reads one contiguous 64-byte segment. A 4x4 byte
+//    transpose between the lanes (0, v), (1, v), (2, v), (3, v) (one
+//    permlane32 swap, one permlane16 swap and two byte permutes) leaves each
+//    lane the four bytes of its own column.
+//  - decode: one 32-bit window cut from the lane's LDS bitstream queue covers
+//    the group's four codes (<= 7 bits each). The window is never shifted: the
+//    7-bit peek of the code that starts o bits in is rotr(window, 23 - o)
+//    bits 8..2, which with the FP8 byte << 9 is the code table entry's byte
+//    address. The running shift s = 23 - o is decremented by whole entries
+//    (their low bits are the length) and only its low 16 bits are kept.
+//  - BF16: the inverse transpose (two permlane32 swaps, one permlane16 swap,
+//    four byte permutes) gives lane (R, v) slab 4g+R's symbols for columns
+//    64w+4v..+3, written with one 8-byte store; each 16-lane row again writes
+//    one contiguous 128-byte segment.
+// A lane requests the next 16 bitstream bytes (four chunks) once it holds
+// fewer than four chunks past its current one, checked every other group;
+// the data land in the queue four groups later. FP8 dwords are loaded DF
+// groups ahead. Every group issues the same vector-memory instructions, so the
+// in-order vmcnt waits stay static.
+//
+// The queue here stores chunk h in slot (~h) & 7 (slot-major, 4 KiB per
+// slot), and positions are kept negated (np = -p, p biased by two chunks as
+// in decode_k1024), so the window's slot addresses and its funnel shift come
+// straight from np.
+// ---------------------------------------------------------------------------
+template <bool kWrap>
+__device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+                                             uint32_t *__restrict__ queue, uint32_t lane, uint32_t rows, uint32_t P,
+                                             uint32_t rowoff_lo, uint32_t rowoff_hi, uint64_t bucket_bit,
+                                             const uint2 (&first)[3], uint32_t pos, uint32_t pos_end,
+                                             uint32_t *status) {
+  constexpr int DF = 4;  // FP8 prefetch distance (groups)
+  rows = uni(rows);
+  P = uni(P);
+  bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
+  const uint32_t count = rows * P;  // elements per lane
+  const uint32_t nfull = count >> 2;
+  const uint32_t tail = count & 3u;  // elements of the last, partial group (only when P % 4 != 0)
+  const uint32_t gall = nfull + (tail ? 1u : 0u);
+  const uint32_t nm = (uint32_t)(T.n * T.m);
+  const __amdgpu_buffer_rsrc_t r_fp8 = make_rsrc(T.fp8, nm);
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(T.out, 2u * nm);
+  const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
+  const uint64_t base_byte = bucket_bit >> 3;
+  const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+  const __amdgpu_buffer_rsrc_t r_bs =
+      make_rsrc(reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+
+  const uint32_t lane4 = lane << 2;
+  const uint32_t R = (lane >> 4) & 3u;
+  const uint32_t colw = (lane & ~63u) | ((lane & 15u) << 2);  // 64w + 4v
+  const char *qbytes = reinterpret_cast<const char *>(queue);
+  const char *lbytes = reinterpret_cast<const char *>(lut);
+  // byte selectors of the FP8 transpose (v_perm: 0-3 pick the second operand's bytes, 4-7 the first's)
+  const uint32_t selA = (R & 2u) ? 0x07060302u : 0x05040100u;
+  const uint32_t selB = (R & 1u) ? 0x07030501u : 0x06020400u;
+
+  // --- bitstream queue -----------------------------------------------------
+  auto chunk_mem = [&](uint32_t h) -> uint32_t {  // biased chunk h from memory (h < 2: out of range, zeros)
+    return __builtin_amdgcn_raw_buffer_load_b32(r_bs, ((h - 2u) ^ 1u) << 2, 0, 0);
+  };
+  // Chunks h (even) and h + 1: slots (~h) & 7 and the one below it.
+  auto put_pair = [&](uint32_t h, uint32_t hi, uint32_t lo) {
+    uint32_t *slot = queue + (((~h << 10) & 0x1800u) | lane);
+    slot[0] = lo;     // chunk h + 1
+    slot[1024] = hi;  // chunk h: the high half of a bitstream word is its first chunk
+  };
+  const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
+  uint32_t wqb = (rq0 + 6u) << 5;  // 32 x (first chunk not yet written)
+  uint32_t rqb = wqb;              // 32 x (first chunk not yet requested)
+  uint32_t np = 0u - (pos + 64u);  // negated biased position
+
+  // 32 stream bits at -npv; from memory for lanes whose queue lacks the two chunks.
+  auto window = [&](uint32_t npv) -> uint32_t {
+    const uint32_t t7 = npv << 7;
+    const uint32_t c0 = *reinterpret_cast<const uint32_t *>(qbytes + ((t7 & 0x7000u) | lane4));
+    const uint32_t c1 = *reinterpret_cast<const uint32_t *>(qbytes + (((t7 - 4096u) & 0x7000u) | lane4));
+    uint32_t w = __builtin_amdgcn_alignbit(c0, c1, npv);
+    const bool dry = (int32_t)(wqb + npv) <= 31;
+    if (__builtin_amdgcn_ballot_w64(dry)) {
+      if (dry) {
+        const uint32_t h = (~npv) >> 5;
+        w = __builtin_amdgcn_alignbit(chunk_mem(h), chunk_mem(h + 1u), npv);
+        __asm__ volatile("" ::"v"(w));  // wait for the loads here, not at a later join
+      }
+    }
+    return w;
+  };
+
+  uint4 infl[2];
+  bool valid[2] = {false, false};
+  infl[0] = infl[1] = make_uint4(0u, 0u, 0u, 0u);
+  // Land the request made four groups ago, then request the next four chunks if needed.
+  auto refill = [&](int rs) {
+    if (valid[rs]) {
+      const uint32_t h = wqb >> 5;
+      put_pair(h, infl[rs].y, infl[rs].x);
+      put_pair(h + 2u, infl[rs].w, infl[rs].z);
+    }
+    wqb += valid[rs] ? 128u : 0u;
+    const bool need = (int32_t)(rqb + np) < 128;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, need ? (rqb >> 3) - 8u : kBsPast, 0, 0);
+    infl[rs] = make_uint4(v[0], v[1], v[2], v[3]);
+    valid[rs] = need;
+    rqb += need ? 128u : 0u;
+  };
+
+  // --- group walker ----------------------------------------------------------
+  auto row_offset = [&](uint32_t r) -> uint32_t {
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_lo, (int)(r & 63u));
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_hi, (int)(r & 63u));
+    return r < 64u ? a : b;
+  };
+  uint32_t w_g = 0, w_row = 0, w_blk = 0;
+  uint32_t w_off = row_offset(0);
+  uint32_t w_next = row_offset(rows > 1u ? 1u : 0u);  // offset of row w_row + 1 (kWrap)
+  const uint32_t vf_al = R * 1024u + colw;           // lane's FP8 byte offset within an aligned group
+  // FP8 load of the walker's group; returns the group's BF16 store offset
+  // (aligned: the uniform element offset of slab 4g; kWrap: the lane's byte offset).
+  auto load_group = [&](uint32_t &F) -> uint32_t {
+    uint32_t ret;
+    if constexpr (!kWrap) {
+      const uint32_t so = uni(w_off + (w_blk << 10));
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, vf_al, so, 0);
+      ret = so;
+    } else {
+      const uint32_t b = w_blk + R;
+      const bool wrap = b >= P;
+      const bool ok = !wrap || w_row + 1u < rows;
+      const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << 10) + colw;
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, ok ? off : 0u, 0, 0);
+      ret = ok ? off << 1 : kSlabPast;
+    }
+    // advance (branch-free; past the last group the walk stays on it)
+    const bool more = w_g + 1u < gall;
+    const uint32_t nb = w_blk + 4u;
+    const bool wr = nb >= P;
+    const uint32_t nrow = w_row + ((more && wr) ? 1u : 0u);
+    const uint32_t noff = row_offset(nrow);
+    const uint32_t nnext = row_offset(nrow + 1u < rows ? nrow + 1u : nrow);
+    // uni(): selects of uniform values may be computed on the VALU, which would
+    // pull the walk (and the loads' soffset) into vector registers.
+    w_blk = uni(more ? (wr ? nb - P : nb) : w_blk);
+    w_off = uni(nrow != w_row ? noff : w_off);
+    w_next = uni(nrow != w_row ? nnext : w_next);
+    w_row = uni(nrow);
+    w_g = uni(w_g + (more ? 1u : 0u));
+    return ret;
+  };
+
+  // --- one group ---------------------------------------------------------------
+  auto group = [&](auto is_tail, uint32_t F, uint32_t so) {
+    constexpr bool kTail = decltype(is_tail)::value;
+    const auto p1 = __builtin_amdgcn_permlane32_swap(F, F, false, false);
+    const uint32_t gq = __builtin_amdgcn_perm(p1[1], p1[0], selA);
+    const auto p2 = __builtin_amdgcn_permlane16_swap(gq, gq, false, false);
+    const uint32_t fq = __builtin_amdgcn_perm(p2[1], p2[0], selB);  // byte j = element j's FP8 byte
+    const uint32_t win = window(np);
+    uint32_t e[4];
+    uint32_t s = 23u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!kTail || (uint32_t)j < tail) {
+        const uint32_t q9 = ((fq >> (8 * j)) & 0xFFu) << 9;
+        const uint32_t x = __builtin_amdgcn_alignbit(win, win, s);
+        e[j] = *reinterpret_cast<const uint32_t *>(lbytes + ((x & 0x1FCu) | q9));
+        s -= e[j];
+      } else {
+        e[j] = 0u;
+      }
+    }
+    np += (uint32_t)((int32_t)(s << 16) >> 16) - 23u;  // minus the bits consumed
+    const auto t0 = __builtin_amdgcn_permlane32_swap(e[0], e[2], false, false);
+    const auto t1 = __builtin_amdgcn_permlane32_swap(e[1], e[3], false, false);
+    const uint32_t a = __builtin_amdgcn_perm(t0[1], t0[0], 0x07060302u);
+    const uint32_t b = __builtin_amdgcn_perm(t1[1], t1[0], 0x07060302u);
+    const auto t2 = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    const v2u o = {__builtin_amdgcn_perm(t2[1], t2[0], 0x05040100u), __builtin_amdgcn_perm(t2[1], t2[0], 0x07060302u)};
+    if constexpr (!kWrap) __builtin_amdgcn_raw_buffer_store_b64(o, r_out, vf_al << 1, uni(so) << 1, 0);
+    else __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, 0);
+  };
+
+  uint32_t Fr[DF], SOr[DF];
+#pragma unroll
+  for (int u = 0; u < DF; ++u) SOr[u] = load_group(Fr[u]);
+  uint32_t g = 0;
+  for (; g + 4u <= nfull; g += 4u) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if ((u & 1) == 0) refill(u >> 1);
+      const uint32_t F = Fr[u], so = SOr[u];
+      SOr[u] = load_group(Fr[u]);
+      group(std::false_type{}, F, so);
+    }
+  }
+  // the last (at most three) full groups and the partial one; their FP8 is already loaded
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (g + (uint32_t)u < gall) {
+      if ((u & 1) == 0) refill(u >> 1);
+      if (g + (uint32_t)u < nfull) group(std::false_type{}, Fr[u], SOr[u]);
+      else group(std::true_type{}, Fr[u], SOr[u]);
+    }
+  }
+  if (0u - np - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
+}
+
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b, uint32_t *lds, uint32_t *status) {
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
@@ -665,10 +886,13 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
   const bool small_stream = (uint64_t)T.bitstream_words < 0x10000000ull;
   // k = 1024 path (any tensor below 2^31 elements) and the general fast path.
-  const bool k1024 = bucket_ok && rows <= 128 && k_eff == 1024 && cl % 1024 == 0 && nm < (1ull << 31) &&
-                     small_stream;
+  const bool k1024 = bucket_ok && rows <= 128 && k_eff == 1024 && cl % 1024 == 0 &&
+                     nm <= (1ull << 31) - 16u && small_stream;
   const bool fast = !k1024 && bucket_ok && rows <= 128 && cl % k_eff == 0 && nm <= (1ull << 29) && small_stream;
   const int lane = tid;
+  // Substream of this work-item: the k = 1024 paths give wave w's 16-lane row
+  // R, position v the column 64w + 4v + R (see decode_slab4); the others, the lane.
+  const int col = k1024 ? ((tid & ~63) | ((tid & 15) << 2) | ((tid >> 4) & 3)) : tid;
   const bool active = bucket_ok && rows > 0 && lane < k_eff;
   const uint32_t *sb = T.bucket_thread_startbit + b * (T.k + 1);
   const uint64_t base = (uint64_t)T.bucket_bit_base[b];
@@ -705,8 +929,8 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   uint32_t pos = 0, pos_end = 0;
   uint2 first[3] = {make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0)};
   if ((k1024 || fast) && active) {
-    pos = sb[lane];
-    pos_end = sb[lane + 1];
+    pos = sb[col];
+    pos_end = sb[col + 1];
     const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
     const uint64_t base_byte = base >> 3;
     const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
@@ -778,14 +1002,23 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   if (!active) return;
   if (k1024) {
     const uint32_t P = (uint32_t)cl / 1024u;
-#define MPS_K1024(GG)                                                                                         \
-  do {                                                                                                        \
-    if (has_esc)                                                                                              \
-      decode_k1024<GG, true>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base,  \
-                             first, pos, pos_end, status);                                                    \
-    else                                                                                                      \
-      decode_k1024<GG, false>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, \
-                              first, pos, pos_end, status);                                                   \
+    if (!has_esc && P >= 4) {
+      if (P % 4 == 0)
+        decode_slab4<false>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
+                            pos, pos_end, status);
+      else
+        decode_slab4<true>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
+                           pos, pos_end, status);
+      return;
+    }
+#define MPS_K1024(GG)                                                                                          \
+  do {                                                                                                         \
+    if (has_esc)                                                                                               \
+      decode_k1024<GG, true>(T, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P, rowoff_lo,     \
+                             rowoff_hi, base, first, pos, pos_end, status);                                    \
+    else                                                                                                       \
+      decode_k1024<GG, false>(T, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P, rowoff_lo,    \
+                              rowoff_hi, base, first, pos, pos_end, status);                                   \
   } while (0)
     if (P % 8 == 0) MPS_K1024(8);
     else if (P % 7 == 0) MPS_K1024(7);
