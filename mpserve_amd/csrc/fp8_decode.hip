@@ -251,6 +251,7 @@ constexpr int kQSlots = 8;                 // LDS queue depth (chunks per lane)
 constexpr uint32_t kPast = 0x40000000u;    // offset beyond every fast-path buffer (2*n*m <= 2^30)
 constexpr uint32_t kBsPast = 0x80000000u;  // bitstream offset beyond every bucket's range
 constexpr uint32_t kSlabPast = 0xFFFFFFF0u;  // BF16 byte offset beyond every k = 1024 output (2*n*m < 2^32 - 16)
+constexpr int kCacheNT = 2;                  // buffer cache-policy bits: non-temporal (gfx950 NT)
 
 // LDS: the queue (kQSlots x kBlock u32) at offset 0, then 256 tables x 128 u32
 // entries. During set-up the queue region also holds the fp8 -> table map; the
@@ -681,7 +682,11 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
                                              uint32_t rowoff_lo, uint32_t rowoff_hi, uint64_t bucket_bit,
                                              const uint2 (&first)[3], uint32_t pos, uint32_t pos_end,
                                              uint32_t *status) {
-  constexpr int DF = 4;  // FP8 prefetch distance (groups)
+#ifndef MPS_SLAB_PREFETCH
+#define MPS_SLAB_PREFETCH 4
+#endif
+  constexpr int DF = MPS_SLAB_PREFETCH;  // FP8 prefetch distance (groups; even)
+  static_assert(DF >= 2 && DF % 2 == 0, "the refill slots alternate every other group");
   rows = uni(rows);
   P = uni(P);
   bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
@@ -831,28 +836,30 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
     const auto t2 = __builtin_amdgcn_permlane16_swap(a, b, false, false);
     typedef unsigned v2u __attribute__((ext_vector_type(2)));
     const v2u o = {__builtin_amdgcn_perm(t2[1], t2[0], 0x05040100u), __builtin_amdgcn_perm(t2[1], t2[0], 0x07060302u)};
-    if constexpr (!kWrap) __builtin_amdgcn_raw_buffer_store_b64(o, r_out, vf_al << 1, uni(so) << 1, 0);
-    else __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, 0);
+    // Non-temporal: the output is written once, and L2 is better spent on the
+    // lanes' bitstream lines and the FP8 lines that wave pairs share.
+    if constexpr (!kWrap) __builtin_amdgcn_raw_buffer_store_b64(o, r_out, vf_al << 1, uni(so) << 1, kCacheNT);
+    else __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, kCacheNT);
   };
 
   uint32_t Fr[DF], SOr[DF];
 #pragma unroll
   for (int u = 0; u < DF; ++u) SOr[u] = load_group(Fr[u]);
   uint32_t g = 0;
-  for (; g + 4u <= nfull; g += 4u) {
+  for (; g + (uint32_t)DF <= nfull; g += (uint32_t)DF) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if ((u & 1) == 0) refill(u >> 1);
+    for (int u = 0; u < DF; ++u) {
+      if ((u & 1) == 0) refill((u >> 1) & 1);
       const uint32_t F = Fr[u], so = SOr[u];
       SOr[u] = load_group(Fr[u]);
       group(std::false_type{}, F, so);
     }
   }
-  // the last (at most three) full groups and the partial one; their FP8 is already loaded
+  // the last (fewer than DF) full groups and the partial one; their FP8 is already loaded
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < DF; ++u) {
     if (g + (uint32_t)u < gall) {
-      if ((u & 1) == 0) refill(u >> 1);
+      if ((u & 1) == 0) refill((u >> 1) & 1);
       if (g + (uint32_t)u < nfull) group(std::false_type{}, Fr[u], SOr[u]);
       else group(std::true_type{}, Fr[u], SOr[u]);
     }
@@ -863,16 +870,11 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b, uint32_t *lds, uint32_t *status) {
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
-  int32_t *s_gid = reinterpret_cast<int32_t *>(qregion) + 7 * kBlock;   // queue slot 7 during set-up
-  int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;  // queue slot 6 (generic path)
-  int32_t *s_flag = reinterpret_cast<int32_t *>(qregion) + 5 * kBlock;  // queue slot 5 during set-up
+  int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
+  uint32_t *s_wflag = qregion + 5 * kBlock;                             // queue slot 5: one word per wave
   const int tid = threadIdx.x;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(T.decode_syms) & 15u) == 0) &&
                       ((reinterpret_cast<uintptr_t>(T.decode_lens) & 3u) == 0);
-  if (tid == 0) {
-    s_flag[0] = 0;  // a row index out of range
-    s_flag[1] = 0;  // some table of the bucket has an ESC entry
-  }
 
   const int32_t ra = T.bucket_row_offsets[b];
   const int32_t rb = T.bucket_row_offsets[b + 1];
@@ -897,15 +899,24 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   const uint32_t *sb = T.bucket_thread_startbit + b * (T.k + 1);
   const uint64_t base = (uint64_t)T.bucket_bit_base[b];
 
-  // fp8 byte -> table id, validated.
+  // Set-up keeps the chains of dependent memory reads short (bucket -> table
+  // ids -> table contents; bucket -> start bits -> first bitstream words): all
+  // loads of a level are issued before any of their results is used.
+  //
+  // Thread tid expands the 16-byte slice tid % 16 of the tables of FP8 bytes
+  // tid / 16 + 64 i (i < 4); their ids are read straight from memory (16
+  // threads share each) and validated.
+  constexpr int kSlices = 256 * (kTable / 8) / kBlock;  // 4
+  int32_t gids[kSlices];
   bool bad_table = false;
-  for (int i = tid; i < 256; i += kBlock) {
-    int32_t g = T.bucket_table[b * 256 + i];
+#pragma unroll
+  for (int i = 0; i < kSlices; ++i) {
+    int32_t g = T.bucket_table[b * 256 + (tid >> 4) + 64 * i];
     if (g < -1 || g >= T.num_tables) {
       bad_table = true;
       g = -1;
     }
-    s_gid[i] = g;
+    gids[i] = g;
   }
   if (bad_table) flag(status, MPS_STATUS_BAD_TABLE);
 
@@ -943,7 +954,6 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
       first[i] = make_uint2(v[0], v[1]);
     }
   }
-  __syncthreads();
   if (!k1024 && !fast) {
     for (int i = tid; i < rows; i += kBlock) {
       const int32_t r = T.row_indices[ra + i];
@@ -951,49 +961,60 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
       s_rows[i] = r;
     }
   }
-  if (bad_row) *s_flag = 1;
 
-  // Expand the 256 tables into 32-bit LDS entries {sym:16 | len:3 << 16 | esc << 20}.
-  uint32_t esc_seen = 0;
-  for (int w = tid; w < 256 * (kTable / 8); w += kBlock) {
-    const int f = w >> 4;
-    const int part = w & 15;
-    const int32_t g = s_gid[f];
-    uint32_t syms[8];
-    uint32_t nibs = 0;
+  // Expand the bucket's 256 tables into 32-bit LDS entries {sym << 16 | esc << 4 | len}:
+  // first every slice's loads, then the expansion.
+  uint4 sv[kSlices];
+  uint32_t nibs[kSlices];
+  const int part = tid & 15;
+#pragma unroll
+  for (int i = 0; i < kSlices; ++i) {
+    const int32_t g = gids[i];
+    sv[i] = make_uint4(0u, 0u, 0u, 0u);
+    nibs[i] = 0;
     if (g >= 0) {
       const uint16_t *sp = T.decode_syms + (int64_t)g * kTable + part * 8;
       const uint8_t *lp = T.decode_lens + (int64_t)g * kPacked + part * 4;
       if (vec_ok) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(sp);
-        syms[0] = v.x & 0xFFFFu; syms[1] = v.x >> 16; syms[2] = v.y & 0xFFFFu; syms[3] = v.y >> 16;
-        syms[4] = v.z & 0xFFFFu; syms[5] = v.z >> 16; syms[6] = v.w & 0xFFFFu; syms[7] = v.w >> 16;
-        nibs = *reinterpret_cast<const uint32_t *>(lp);
+        sv[i] = *reinterpret_cast<const uint4 *>(sp);
+        nibs[i] = *reinterpret_cast<const uint32_t *>(lp);
       } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) syms[j] = sp[j];
-        nibs = (uint32_t)lp[0] | ((uint32_t)lp[1] << 8) | ((uint32_t)lp[2] << 16) | ((uint32_t)lp[3] << 24);
+        sv[i] = make_uint4((uint32_t)sp[0] | ((uint32_t)sp[1] << 16), (uint32_t)sp[2] | ((uint32_t)sp[3] << 16),
+                           (uint32_t)sp[4] | ((uint32_t)sp[5] << 16), (uint32_t)sp[6] | ((uint32_t)sp[7] << 16));
+        nibs[i] = (uint32_t)lp[0] | ((uint32_t)lp[1] << 8) | ((uint32_t)lp[2] << 16) | ((uint32_t)lp[3] << 24);
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) syms[j] = 0;
     }
-    esc_seen |= nibs & 0x88888888u;
+  }
+  uint32_t esc_seen = 0;
+#pragma unroll
+  for (int i = 0; i < kSlices; ++i) {
+    const uint32_t s8[8] = {sv[i].x & 0xFFFFu, sv[i].x >> 16, sv[i].y & 0xFFFFu, sv[i].y >> 16,
+                            sv[i].z & 0xFFFFu, sv[i].z >> 16, sv[i].w & 0xFFFFu, sv[i].w >> 16};
+    esc_seen |= nibs[i] & 0x88888888u;
     uint32_t e[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint32_t nib = (nibs >> (4 * j)) & 0xFu;
-      e[j] = (syms[j] << 16) | (nib & 7u) | ((nib & 8u) ? kEscBit : 0u);
+      const uint32_t nib = (nibs[i] >> (4 * j)) & 0xFu;
+      e[j] = (s8[j] << 16) | (nib & 7u) | ((nib & 8u) ? kEscBit : 0u);
     }
-    uint4 *dst = reinterpret_cast<uint4 *>(lut + f * kTable + part * 8);
+    uint4 *dst = reinterpret_cast<uint4 *>(lut + ((tid >> 4) + 64 * i) * kTable + part * 8);
     dst[0] = make_uint4(e[0], e[1], e[2], e[3]);
     dst[1] = make_uint4(e[4], e[5], e[6], e[7]);
   }
-  if (esc_seen) atomicOr(reinterpret_cast<uint32_t *>(s_flag) + 1, 1u);
+  // Block-wide ORs of "a row index is out of range" (bit 0) and "a table has an
+  // ESC entry" (bit 1): one word per wave, written by its first lane.
+  {
+    const uint32_t wf = (__builtin_amdgcn_ballot_w64(bad_row) ? 1u : 0u) |
+                        (__builtin_amdgcn_ballot_w64(esc_seen != 0) ? 2u : 0u);
+    if ((tid & 63) == 0) s_wflag[tid >> 6] = wf;
+  }
   __syncthreads();
-  const bool has_esc = s_flag[1] != 0;
-  const bool any_bad_row = s_flag[0] != 0;
-  __syncthreads();  // the flag's word belongs to the queue from here on
+  uint32_t bflags = 0;
+#pragma unroll
+  for (int w = 0; w < kBlock / 64; ++w) bflags |= s_wflag[w];
+  const bool has_esc = (bflags & 2u) != 0;
+  const bool any_bad_row = (bflags & 1u) != 0;
+  __syncthreads();  // the flag words belong to the queue from here on
 
   if (!bucket_ok || any_bad_row) {
     if (tid == 0) flag(status, !bucket_ok ? MPS_STATUS_BAD_BUCKET : MPS_STATUS_BAD_ROW);
