@@ -18,6 +18,7 @@
 // plus its ESC payload.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <mutex>
@@ -667,7 +668,7 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
 //    one contiguous 128-byte segment.
 // A lane requests the next 16 bitstream bytes (four chunks) once it holds
 // fewer than four chunks past its current one, checked every other group;
-// the data land in the queue four groups later. FP8 dwords are loaded DF
+// the data land in the queue 2 * RS groups later. FP8 dwords are loaded DF
 // groups ahead. Every group issues the same vector-memory instructions, so the
 // in-order vmcnt waits stay static.
 //
@@ -686,7 +687,11 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
 #define MPS_SLAB_PREFETCH 4
 #endif
   constexpr int DF = MPS_SLAB_PREFETCH;  // FP8 prefetch distance (groups; even)
-  static_assert(DF >= 2 && DF % 2 == 0, "the refill slots alternate every other group");
+#ifndef MPS_SLAB_REFILL_SLOTS
+#define MPS_SLAB_REFILL_SLOTS 1
+#endif
+  constexpr int RS = MPS_SLAB_REFILL_SLOTS;  // bitstream requests in flight per lane (one per two groups)
+  static_assert(DF >= 2 && DF % (2 * RS) == 0, "refills run every other group, round-robin over RS slots");
   rows = uni(rows);
   P = uni(P);
   bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
@@ -746,10 +751,14 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
     return w;
   };
 
-  uint4 infl[2];
-  bool valid[2] = {false, false};
-  infl[0] = infl[1] = make_uint4(0u, 0u, 0u, 0u);
-  // Land the request made four groups ago, then request the next four chunks if needed.
+  uint4 infl[RS];
+  bool valid[RS];
+#pragma unroll
+  for (int i = 0; i < RS; ++i) {
+    infl[i] = make_uint4(0u, 0u, 0u, 0u);
+    valid[i] = false;
+  }
+  // Land the request made 2 * RS groups ago, then request the next four chunks if needed.
   auto refill = [&](int rs) {
     if (valid[rs]) {
       const uint32_t h = wqb >> 5;
@@ -849,7 +858,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   for (; g + (uint32_t)DF <= nfull; g += (uint32_t)DF) {
 #pragma unroll
     for (int u = 0; u < DF; ++u) {
-      if ((u & 1) == 0) refill((u >> 1) & 1);
+      if ((u & 1) == 0) refill((u >> 1) % RS);
       const uint32_t F = Fr[u], so = SOr[u];
       SOr[u] = load_group(Fr[u]);
       group(std::false_type{}, F, so);
@@ -859,7 +868,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
 #pragma unroll
   for (int u = 0; u < DF; ++u) {
     if (g + (uint32_t)u < gall) {
-      if ((u & 1) == 0) refill((u >> 1) & 1);
+      if ((u & 1) == 0) refill((u >> 1) % RS);
       if (g + (uint32_t)u < nfull) group(std::false_type{}, Fr[u], SOr[u]);
       else group(std::true_type{}, Fr[u], SOr[u]);
     }
@@ -1060,16 +1069,37 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   }
 }
 
+// Both kernels are persistent: one workgroup per CU (the LDS holds one
+// bucket's tables) walks its share of the buckets, so a bucket's set-up does
+// not also pay a workgroup launch. Every workgroup runs the same uniform loop
+// to its end.
 __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
-  decode_bucket(T, blockIdx.x, lds, status);
+  for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
+    decode_bucket(T, b, lds, status);
+    __syncthreads();  // the next bucket's set-up overwrites the LDS
+  }
 }
 
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
-                                                          const WorkItem *__restrict__ work, uint32_t *status) {
+                                                          const WorkItem *__restrict__ work, int64_t nwork,
+                                                          uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
-  const WorkItem w = work[blockIdx.x];
-  decode_bucket(tensors[w.tensor], w.bucket, lds, status);
+  for (int64_t i = blockIdx.x; i < nwork; i += gridDim.x) {
+    const WorkItem w = work[i];
+    decode_bucket(tensors[w.tensor], w.bucket, lds, status);
+    __syncthreads();  // the next bucket's set-up overwrites the LDS
+  }
+}
+
+// Workgroups of a persistent launch on the current device: one per CU.
+int persistent_grid(int64_t items, unsigned *grid) {
+  int dev = 0, cus = 0;
+  MPS_HIP_CHECK(hipGetDevice(&dev));
+  MPS_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (cus < 1) cus = 1;
+  *grid = (unsigned)(items < cus ? items : cus);
+  return MPS_OK;
 }
 
 int check_tensor(const mps_fp8_tensor *t) {
@@ -1150,8 +1180,11 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream) 
   uint32_t *status = nullptr;
   rc = status_word(dev, &status);
   if (rc != MPS_OK) return rc;
-  hipLaunchKernelGGL(fp8_decode_one, dim3((unsigned)tensor->num_buckets), dim3(kBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), *tensor, status);
+  unsigned grid = 0;
+  rc = persistent_grid(tensor->num_buckets, &grid);
+  if (rc != MPS_OK) return rc;
+  hipLaunchKernelGGL(fp8_decode_one, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream), *tensor,
+                     status);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
@@ -1161,13 +1194,36 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
   if (!plan_out) return fail(MPS_ERR_INVALID_ARGUMENT, "plan_out is NULL");
   *plan_out = nullptr;
   if (count < 0 || (count > 0 && !tensors)) return fail(MPS_ERR_INVALID_ARGUMENT, "invalid tensor list");
+  // Work items (buckets), largest first: the persistent launch deals them
+  // round-robin to the CUs, which then finish at about the same time. A
+  // bucket's cost is its element count plus a fixed set-up share.
   std::vector<WorkItem> work;
+  std::vector<int64_t> cost;
+  std::vector<int32_t> roff, clen;
   for (int64_t i = 0; i < count; ++i) {
     int rc = check_tensor(&tensors[i]);
     if (rc != MPS_OK) return rc;
-    for (int64_t b = 0; b < tensors[i].num_buckets; ++b) work.push_back({(int32_t)i, (int32_t)b});
+    const int64_t nb = tensors[i].num_buckets;
+    if (nb == 0) continue;
+    roff.resize((size_t)nb + 1);
+    clen.resize((size_t)nb);
+    MPS_HIP_CHECK(hipMemcpy(roff.data(), tensors[i].bucket_row_offsets, sizeof(int32_t) * (nb + 1), hipMemcpyDefault));
+    MPS_HIP_CHECK(hipMemcpy(clen.data(), tensors[i].bucket_col_len, sizeof(int32_t) * nb, hipMemcpyDefault));
+    for (int64_t b = 0; b < nb; ++b) {
+      work.push_back({(int32_t)i, (int32_t)b});
+      const int64_t rows = (int64_t)roff[b + 1] - roff[b];
+      cost.push_back((rows > 0 && clen[b] > 0 ? rows * clen[b] : 0) + 65536);
+    }
   }
   if (work.size() > (size_t)INT32_MAX) return fail(MPS_ERR_INVALID_ARGUMENT, "too many buckets for one plan");
+  {
+    std::vector<size_t> order(work.size());
+    for (size_t j = 0; j < order.size(); ++j) order[j] = j;
+    std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t c) { return cost[a] > cost[c]; });
+    std::vector<WorkItem> sorted(work.size());
+    for (size_t j = 0; j < order.size(); ++j) sorted[j] = work[order[j]];
+    work.swap(sorted);
+  }
   auto *p = new mps_fp8_plan();
   p->count = count;
   p->work_items = (int64_t)work.size();
@@ -1195,8 +1251,11 @@ int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream) {
   uint32_t *status = nullptr;
   int rc = status_word(plan->device, &status);
   if (rc != MPS_OK) return rc;
-  hipLaunchKernelGGL(fp8_decode_plan, dim3((unsigned)plan->work_items), dim3(kBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, status);
+  unsigned grid = 0;
+  rc = persistent_grid(plan->work_items, &grid);
+  if (rc != MPS_OK) return rc;
+  hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
+                     plan->d_tensors, plan->d_work, plan->work_items, status);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
