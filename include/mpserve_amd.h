@@ -71,15 +71,18 @@ int mps_clock_rate_khz(int device, int64_t *khz_out);
 int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
 
 /* Batched decode plan: one launch decodes many tensors (a layer, a model).
- * The plan copies the descriptors to device memory it owns (synchronously, at
- * create time); the pointed-to sidecars must stay alive while the plan is used.
+ * The plan copies the descriptors to device memory it owns and reads each
+ * tensor's bucket row offsets and column lengths to order the buckets largest
+ * first (synchronously, at create time); the pointed-to sidecars must stay
+ * alive while the plan is used. Launches (like mps_fp8_decode's) are
+ * persistent: one workgroup per CU walks its share of the buckets.
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:739); it serves its apply() and model loading paths
  * (scripts/mpserve_vllm_fp8_huffman.py:491-557). */
 typedef struct mps_fp8_plan mps_fp8_plan;
 int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_plan **plan_out);
 int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream);
-/* Launches of the plan's work list (for profiling tools): work items, bytes of LDS per workgroup. */
+/* The plan's work list (for profiling tools): buckets, bytes of LDS per workgroup. */
 int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes);
 int mps_fp8_plan_destroy(mps_fp8_plan *plan);
 

@@ -99,7 +99,7 @@ class DecodePlan:
         wi, lds = ctypes.c_int64(0), ctypes.c_int64(0)
         if self._plan:
             _native.check(_native.lib().mps_fp8_plan_info(self._plan, ctypes.byref(wi), ctypes.byref(lds)))
-        return {"workgroups": int(wi.value), "lds_bytes": int(lds.value)}
+        return {"buckets": int(wi.value), "lds_bytes": int(lds.value)}
 
     def close(self) -> None:
         if getattr(self, "_plan", None):
