@@ -773,6 +773,66 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
     rqb += need ? 128u : 0u;
   };
 
+  // Register reserve: up to four 16-byte blocks that follow the queue's last
+  // chunk. Once per DF groups, a lane whose reserve is down to one block
+  // requests the next 64 bytes (four loads from the same lines, so a 128-byte
+  // line is fetched about twice instead of once per 16 bytes); they land in
+  // the reserve at a later DF boundary, once it is empty. Every other group
+  // the reserve's front block moves into the queue if four slots are free.
+  uint4 rv[4], inb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t rcnt = 0;  // blocks in rv
+  bool ifl = false;   // a 64-byte request is in flight (into inb)
+  auto feed = [&]() {
+    const bool f = rcnt != 0u && (int32_t)(wqb + np) < 128;
+    if (f) {
+      const uint32_t h = wqb >> 5;
+      put_pair(h, rv[0].y, rv[0].x);
+      put_pair(h + 2u, rv[0].w, rv[0].z);
+      rv[0] = rv[1];
+      rv[1] = rv[2];
+      rv[2] = rv[3];
+    }
+    wqb += f ? 128u : 0u;
+    rcnt -= f ? 1u : 0u;
+  };
+  auto reserve = [&]() {
+    const bool land = ifl && rcnt == 0u;
+    if (land) {
+      rv[0] = inb[0];
+      rv[1] = inb[1];
+      rv[2] = inb[2];
+      rv[3] = inb[3];
+    }
+    rcnt = land ? 4u : rcnt;
+    ifl = ifl && !land;
+    // no requests past the substream's end (biased end + the window's reach)
+    const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
+    if (req) {
+      const uint32_t off = (rqb >> 3) - 8u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off + 16u * (uint32_t)i, 0, 0);
+        inb[i] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+    }
+    ifl = ifl || req;
+    rqb += req ? 512u : 0u;
+  };
+#ifndef MPS_SLAB_RESERVE
+#define MPS_SLAB_RESERVE 1
+#endif
+  constexpr bool kReserve = MPS_SLAB_RESERVE != 0;
+  auto bitstream_step = [&](int u) {
+    if constexpr (kReserve) {
+      if (u == 0) reserve();
+      if ((u & 1) == 0) feed();
+    } else {
+      if ((u & 1) == 0) refill((u >> 1) % RS);
+    }
+  };
+
   // --- group walker ----------------------------------------------------------
   auto row_offset = [&](uint32_t r) -> uint32_t {
     const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_lo, (int)(r & 63u));
@@ -858,7 +918,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   for (; g + (uint32_t)DF <= nfull; g += (uint32_t)DF) {
 #pragma unroll
     for (int u = 0; u < DF; ++u) {
-      if ((u & 1) == 0) refill((u >> 1) % RS);
+      bitstream_step(u);
       const uint32_t F = Fr[u], so = SOr[u];
       SOr[u] = load_group(Fr[u]);
       group(std::false_type{}, F, so);
@@ -868,7 +928,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
 #pragma unroll
   for (int u = 0; u < DF; ++u) {
     if (g + (uint32_t)u < gall) {
-      if ((u & 1) == 0) refill((u >> 1) % RS);
+      bitstream_step(u);
       if (g + (uint32_t)u < nfull) group(std::false_type{}, Fr[u], SOr[u]);
       else group(std::true_type{}, Fr[u], SOr[u]);
     }
