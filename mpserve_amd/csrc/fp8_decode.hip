@@ -456,7 +456,7 @@ template <int G, bool kEsc>
 __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
                                              uint32_t *__restrict__ queue, uint32_t lane, uint32_t col,
                                              uint32_t rows, uint32_t P, uint32_t rowoff_lo, uint32_t rowoff_hi,
-                                             uint64_t bucket_bit, const uint2 (&first)[3], uint32_t pos,
+                                             uint64_t bucket_bit, const uint2 (&first)[4], uint32_t pos,
                                              uint32_t pos_end, uint32_t *status) {
   constexpr uint32_t K = 1024;
   constexpr int S = G >= 8 ? 1 : 8 / G;  // blocks per step
@@ -681,10 +681,10 @@ template <bool kWrap>
 __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
                                              uint32_t *__restrict__ queue, uint32_t lane, uint32_t rows, uint32_t P,
                                              uint32_t rowoff_lo, uint32_t rowoff_hi, uint64_t bucket_bit,
-                                             const uint2 (&first)[3], uint32_t pos, uint32_t pos_end,
+                                             const uint2 (&first)[4], uint32_t pos, uint32_t pos_end,
                                              uint32_t *status) {
 #ifndef MPS_SLAB_PREFETCH
-#define MPS_SLAB_PREFETCH 4
+#define MPS_SLAB_PREFETCH 8
 #endif
   constexpr int DF = MPS_SLAB_PREFETCH;  // FP8 prefetch distance (groups; even)
 #ifndef MPS_SLAB_REFILL_SLOTS
@@ -729,8 +729,8 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   };
   const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
 #pragma unroll
-  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
-  uint32_t wqb = (rq0 + 6u) << 5;  // 32 x (first chunk not yet written)
+  for (int i = 0; i < 4; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);  // fills all eight slots
+  uint32_t wqb = (rq0 + 8u) << 5;  // 32 x (first chunk not yet written)
   uint32_t rqb = wqb;              // 32 x (first chunk not yet requested)
   uint32_t np = 0u - (pos + 64u);  // negated biased position
 
@@ -773,26 +773,29 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
     rqb += need ? 128u : 0u;
   };
 
-  // Register reserve: up to four 16-byte blocks that follow the queue's last
-  // chunk. Once per DF groups, a lane whose reserve is down to one block
-  // requests the next 64 bytes (four loads from the same lines, so a 128-byte
+  // Register reserve: up to RB 16-byte blocks that follow the queue's last
+  // chunk. Every fourth group, a lane whose reserve is down to one block
+  // requests the next RB * 16 bytes (loads from the same lines, so a 128-byte
   // line is fetched about twice instead of once per 16 bytes); they land in
-  // the reserve at a later DF boundary, once it is empty. Every other group
+  // the reserve four or more groups later, once it is empty. Every other group
   // the reserve's front block moves into the queue if four slots are free.
-  uint4 rv[4], inb[4];
+#ifndef MPS_SLAB_RESERVE_BLOCKS
+#define MPS_SLAB_RESERVE_BLOCKS 4
+#endif
+  constexpr int RB = MPS_SLAB_RESERVE_BLOCKS;  // 16-byte blocks per request
+  uint4 rv[RB], inb[RB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
+  for (int i = 0; i < RB; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
   uint32_t rcnt = 0;  // blocks in rv
-  bool ifl = false;   // a 64-byte request is in flight (into inb)
+  bool ifl = false;   // a request is in flight (into inb)
   auto feed = [&]() {
     const bool f = rcnt != 0u && (int32_t)(wqb + np) < 128;
     if (f) {
       const uint32_t h = wqb >> 5;
       put_pair(h, rv[0].y, rv[0].x);
       put_pair(h + 2u, rv[0].w, rv[0].z);
-      rv[0] = rv[1];
-      rv[1] = rv[2];
-      rv[2] = rv[3];
+#pragma unroll
+      for (int i = 0; i + 1 < RB; ++i) rv[i] = rv[i + 1];
     }
     wqb += f ? 128u : 0u;
     rcnt -= f ? 1u : 0u;
@@ -800,25 +803,23 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   auto reserve = [&]() {
     const bool land = ifl && rcnt == 0u;
     if (land) {
-      rv[0] = inb[0];
-      rv[1] = inb[1];
-      rv[2] = inb[2];
-      rv[3] = inb[3];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) rv[i] = inb[i];
     }
-    rcnt = land ? 4u : rcnt;
+    rcnt = land ? (uint32_t)RB : rcnt;
     ifl = ifl && !land;
     // no requests past the substream's end (biased end + the window's reach)
     const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
     if (req) {
       const uint32_t off = (rqb >> 3) - 8u;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < RB; ++i) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off + 16u * (uint32_t)i, 0, 0);
         inb[i] = make_uint4(v[0], v[1], v[2], v[3]);
       }
     }
     ifl = ifl || req;
-    rqb += req ? 512u : 0u;
+    rqb += req ? 128u * (uint32_t)RB : 0u;
   };
 #ifndef MPS_SLAB_RESERVE
 #define MPS_SLAB_RESERVE 1
@@ -826,7 +827,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   constexpr bool kReserve = MPS_SLAB_RESERVE != 0;
   auto bitstream_step = [&](int u) {
     if constexpr (kReserve) {
-      if (u == 0) reserve();
+      if (u % 4 == 0) reserve();
       if ((u & 1) == 0) feed();
     } else {
       if ((u & 1) == 0) refill((u >> 1) % RS);
@@ -1005,9 +1006,10 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
       rowoff_hi = (uint32_t)r * (uint32_t)T.m + (uint32_t)c0;
     }
   }
-  // First three bitstream pairs of this lane, loaded before the table set-up.
+  // First four bitstream words of this lane (two 16-byte loads), loaded before
+  // the table set-up; the slab path queues all four, the others three.
   uint32_t pos = 0, pos_end = 0;
-  uint2 first[3] = {make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0)};
+  uint2 first[4] = {make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0)};
   if ((k1024 || fast) && active) {
     pos = sb[col];
     pos_end = sb[col + 1];
@@ -1018,9 +1020,10 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
         reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
     const uint32_t rq0 = (pos >> 5) & ~1u;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r_bs, (rq0 + 2 * i) * 4u, 0, 0);
-      first[i] = make_uint2(v[0], v[1]);
+    for (int i = 0; i < 2; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, (rq0 + 4 * i) * 4u, 0, 0);
+      first[2 * i] = make_uint2(v[0], v[1]);
+      first[2 * i + 1] = make_uint2(v[2], v[3]);
     }
   }
   if (!k1024 && !fast) {
