@@ -727,12 +727,28 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
     slot[0] = lo;     // chunk h + 1
     slot[1024] = hi;  // chunk h: the high half of a bitstream word is its first chunk
   };
+#ifndef MPS_SLAB_ALIGN
+#define MPS_SLAB_ALIGN 1
+#endif
+#ifndef MPS_SLAB_RESERVE_BLOCKS
+#define MPS_SLAB_RESERVE_BLOCKS 4
+#endif
+  constexpr int RB = MPS_SLAB_RESERVE_BLOCKS;  // 16-byte blocks per bitstream request
+  // Byte address of the bucket's bitstream modulo one request (16 * RB bytes):
+  // requests after the first start on that boundary, so each one touches a
+  // single cache-line half (RB = 4) or line (RB = 8).
+  const uint32_t phase =
+      ((uint32_t)reinterpret_cast<uintptr_t>(T.bitstream) + (uint32_t)(bucket_bit >> 3)) & (16u * RB - 1u);
+  // The initial queue: the four words read during set-up, or three when the
+  // fourth would leave the next request off a 16-byte boundary.
   const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
+  const uint32_t nfirst = (MPS_SLAB_ALIGN && ((phase + 4u * (rq0 - 2u)) & 15u)) ? 6u : 8u;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);  // fills all eight slots
-  uint32_t wqb = (rq0 + 8u) << 5;  // 32 x (first chunk not yet written)
-  uint32_t rqb = wqb;              // 32 x (first chunk not yet requested)
-  uint32_t np = 0u - (pos + 64u);  // negated biased position
+  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
+  if (nfirst == 8u) put_pair(rq0 + 6u, first[3].y, first[3].x);
+  uint32_t wqb = (rq0 + nfirst) << 5;  // 32 x (first chunk not yet written)
+  uint32_t rqb = wqb;                  // 32 x (first chunk not yet requested)
+  uint32_t np = 0u - (pos + 64u);      // negated biased position
 
   // 32 stream bits at -npv; from memory for lanes whose queue lacks the two chunks.
   auto window = [&](uint32_t npv) -> uint32_t {
@@ -779,10 +795,6 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   // line is fetched about twice instead of once per 16 bytes); they land in
   // the reserve four or more groups later, once it is empty. Every other group
   // the reserve's front block moves into the queue if four slots are free.
-#ifndef MPS_SLAB_RESERVE_BLOCKS
-#define MPS_SLAB_RESERVE_BLOCKS 4
-#endif
-  constexpr int RB = MPS_SLAB_RESERVE_BLOCKS;  // 16-byte blocks per request
   uint4 rv[RB], inb[RB];
 #pragma unroll
   for (int i = 0; i < RB; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -800,26 +812,31 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
     wqb += f ? 128u : 0u;
     rcnt -= f ? 1u : 0u;
   };
+  uint32_t ninb = 0;  // blocks of the request in flight
   auto reserve = [&]() {
     const bool land = ifl && rcnt == 0u;
     if (land) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) rv[i] = inb[i];
     }
-    rcnt = land ? (uint32_t)RB : rcnt;
+    rcnt = land ? ninb : rcnt;
     ifl = ifl && !land;
     // no requests past the substream's end (biased end + the window's reach)
     const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
+    const uint32_t off = (rqb >> 3) - 8u;
+    // blocks up to the next request boundary (the first request may be short)
+    const uint32_t nreq = MPS_SLAB_ALIGN ? (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4 : (uint32_t)RB;
     if (req) {
-      const uint32_t off = (rqb >> 3) - 8u;
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off + 16u * (uint32_t)i, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, (uint32_t)i < nreq ? off + 16u * (uint32_t)i : kBsPast,
+                                                             0, 0);
         inb[i] = make_uint4(v[0], v[1], v[2], v[3]);
       }
+      ninb = nreq;
     }
     ifl = ifl || req;
-    rqb += req ? 128u * (uint32_t)RB : 0u;
+    rqb += req ? nreq << 7 : 0u;
   };
 #ifndef MPS_SLAB_RESERVE
 #define MPS_SLAB_RESERVE 1
