@@ -793,8 +793,8 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   // chunk. Every fourth group, a lane whose reserve is down to one block
   // requests the next RB * 16 bytes (loads from the same lines, so a 128-byte
   // line is fetched about twice instead of once per 16 bytes); they land in
-  // the reserve four or more groups later, once it is empty. Every other group
-  // the reserve's front block moves into the queue if four slots are free.
+  // the reserve four or more groups later, once it is empty. Every fourth
+  // group the reserve's front block moves into the queue if four slots are free.
   uint4 rv[RB], inb[RB];
 #pragma unroll
   for (int i = 0; i < RB; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -844,8 +844,11 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   constexpr bool kReserve = MPS_SLAB_RESERVE != 0;
   auto bitstream_step = [&](int u) {
     if constexpr (kReserve) {
-      if (u % 4 == 0) reserve();
-      if ((u & 1) == 0) feed();
+      // one 16-byte feed per four groups covers the 4 x 28 bits they can consume
+      if (u % 4 == 0) {
+        reserve();
+        feed();
+      }
     } else {
       if ((u & 1) == 0) refill((u >> 1) % RS);
     }
