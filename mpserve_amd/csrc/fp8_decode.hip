@@ -666,10 +666,12 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
 //    four byte permutes) gives lane (R, v) slab 4g+R's symbols for columns
 //    64w+4v..+3, written with one 8-byte store; each 16-lane row again writes
 //    one contiguous 128-byte segment.
-// A lane requests the next 16 bitstream bytes (four chunks) once it holds
-// fewer than four chunks past its current one, checked every other group;
-// the data land in the queue 2 * RS groups later. FP8 dwords are loaded DF
-// groups ahead. Every group issues the same vector-memory instructions, so the
+// Bitstream: a lane requests up to 64 bytes at a time into a register reserve
+// (aligned so that each request touches one half of a 128-byte line) and,
+// once per four groups, moves 16 bytes from the reserve into its LDS queue.
+// When every lane of the wave then holds enough bits for four windows, the
+// four groups skip the per-window dry check. FP8 dwords are loaded DF groups
+// ahead. Every group issues the same vector-memory instructions, so the
 // in-order vmcnt waits stay static.
 //
 // The queue here stores chunk h in slot (~h) & 7 (slot-major, 4 KiB per
@@ -686,12 +688,8 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
 #ifndef MPS_SLAB_PREFETCH
 #define MPS_SLAB_PREFETCH 8
 #endif
-  constexpr int DF = MPS_SLAB_PREFETCH;  // FP8 prefetch distance (groups; even)
-#ifndef MPS_SLAB_REFILL_SLOTS
-#define MPS_SLAB_REFILL_SLOTS 1
-#endif
-  constexpr int RS = MPS_SLAB_REFILL_SLOTS;  // bitstream requests in flight per lane (one per two groups)
-  static_assert(DF >= 2 && DF % (2 * RS) == 0, "refills run every other group, round-robin over RS slots");
+  constexpr int DF = MPS_SLAB_PREFETCH;  // FP8 prefetch distance (groups)
+  static_assert(DF >= 4 && DF % 4 == 0, "the bitstream is served once per four groups");
   rows = uni(rows);
   P = uni(P);
   bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
@@ -750,7 +748,9 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   uint32_t rqb = wqb;                  // 32 x (first chunk not yet requested)
   uint32_t np = 0u - (pos + 64u);      // negated biased position
 
-  // 32 stream bits at -npv; from memory for lanes whose queue lacks the two chunks.
+  // 32 stream bits at -npv; from memory for lanes whose queue lacks the two
+  // chunks. (Checking once per four groups instead, with an unchecked copy of
+  // the groups, measured slower: the extra branch splits the scheduling region.)
   auto window = [&](uint32_t npv) -> uint32_t {
     const uint32_t t7 = npv << 7;
     const uint32_t c0 = *reinterpret_cast<const uint32_t *>(qbytes + ((t7 & 0x7000u) | lane4));
@@ -765,28 +765,6 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
       }
     }
     return w;
-  };
-
-  uint4 infl[RS];
-  bool valid[RS];
-#pragma unroll
-  for (int i = 0; i < RS; ++i) {
-    infl[i] = make_uint4(0u, 0u, 0u, 0u);
-    valid[i] = false;
-  }
-  // Land the request made 2 * RS groups ago, then request the next four chunks if needed.
-  auto refill = [&](int rs) {
-    if (valid[rs]) {
-      const uint32_t h = wqb >> 5;
-      put_pair(h, infl[rs].y, infl[rs].x);
-      put_pair(h + 2u, infl[rs].w, infl[rs].z);
-    }
-    wqb += valid[rs] ? 128u : 0u;
-    const bool need = (int32_t)(rqb + np) < 128;
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, need ? (rqb >> 3) - 8u : kBsPast, 0, 0);
-    infl[rs] = make_uint4(v[0], v[1], v[2], v[3]);
-    valid[rs] = need;
-    rqb += need ? 128u : 0u;
   };
 
   // Register reserve: up to RB 16-byte blocks that follow the queue's last
@@ -838,20 +816,10 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
     ifl = ifl || req;
     rqb += req ? nreq << 7 : 0u;
   };
-#ifndef MPS_SLAB_RESERVE
-#define MPS_SLAB_RESERVE 1
-#endif
-  constexpr bool kReserve = MPS_SLAB_RESERVE != 0;
-  auto bitstream_step = [&](int u) {
-    if constexpr (kReserve) {
-      // one 16-byte feed per four groups covers the 4 x 28 bits they can consume
-      if (u % 4 == 0) {
-        reserve();
-        feed();
-      }
-    } else {
-      if ((u & 1) == 0) refill((u >> 1) % RS);
-    }
+  // Once per four groups: one 16-byte feed covers the 4 x 28 bits they can consume.
+  auto bitstream_step = [&]() {
+    reserve();
+    feed();
   };
 
   // --- group walker ----------------------------------------------------------
@@ -939,9 +907,9 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   for (; g + (uint32_t)DF <= nfull; g += (uint32_t)DF) {
 #pragma unroll
     for (int u = 0; u < DF; ++u) {
-      bitstream_step(u);
+      if (u % 4 == 0) bitstream_step();
       const uint32_t F = Fr[u], so = SOr[u];
-      SOr[u] = load_group(Fr[u]);
+      SOr[u] = load_group(Fr[u]);  // the group DF ahead
       group(std::false_type{}, F, so);
     }
   }
@@ -949,7 +917,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
 #pragma unroll
   for (int u = 0; u < DF; ++u) {
     if (g + (uint32_t)u < gall) {
-      bitstream_step(u);
+      if (u % 4 == 0) bitstream_step();
       if (g + (uint32_t)u < nfull) group(std::false_type{}, Fr[u], SOr[u]);
       else group(std::true_type{}, Fr[u], SOr[u]);
     }
