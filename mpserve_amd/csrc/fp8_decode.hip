@@ -56,10 +56,52 @@ __device__ __forceinline__ uint32_t chunk_at(const uint32_t *__restrict__ bs32, 
 
 __device__ uint32_t g_zero_chunks[2];
 
-struct WorkItem {
-  int32_t tensor;
-  int32_t bucket;
+// Decode path of a bucket.
+enum : int32_t { kPathBad = 0, kPathGeneric = 1, kPathFast = 2, kPathK1024 = 3 };
+
+struct BucketShape {
+  int32_t rows;   // 0 for a bad bucket
+  int32_t k_eff;  // lanes with elements
+  int32_t path;
 };
+
+// Shape and decode path of the bucket with row range [ra, rb) and column
+// range [c0, c0 + cl) of tensor T. A range outside the tensor (or more rows
+// than the LDS stages) makes the bucket bad. Shared by the plan builder (host)
+// and the single-tensor kernel (device).
+__host__ __device__ inline BucketShape bucket_shape(int32_t ra, int32_t rb, int32_t c0, int32_t cl,
+                                                    const mps_fp8_tensor &T) {
+  const bool ok = ra >= 0 && rb >= ra && (int64_t)rb <= T.num_row_indices && rb - ra <= kRowsLds && cl > 0 &&
+                  c0 >= 0 && (int64_t)c0 + cl <= T.m;
+  BucketShape s;
+  s.rows = ok ? rb - ra : 0;
+  const int64_t total = (int64_t)s.rows * cl;
+  s.k_eff = (int32_t)(T.k < total ? T.k : (total > 0 ? total : 1));
+  const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
+  const bool small_stream = (uint64_t)T.bitstream_words < 0x10000000ull;
+  // k = 1024 path (any tensor below 2^31 elements) and the general fast path.
+  const bool k1024 = ok && s.rows <= 128 && s.k_eff == 1024 && cl % 1024 == 0 && nm <= (1ull << 31) - 16u &&
+                     small_stream;
+  const bool fast = !k1024 && ok && s.rows <= 128 && cl % s.k_eff == 0 && nm <= (1ull << 29) && small_stream;
+  s.path = !ok ? kPathBad : k1024 ? kPathK1024 : fast ? kPathFast : kPathGeneric;
+  return s;
+}
+
+// One bucket to decode: its tensor, ranges, shape and the addresses of its
+// per-bucket arrays. A plan builds these once (64 bytes: one scalar load per
+// bucket, which leaves the table ids, row indices and start bits one
+// dependent load away); the single-tensor kernel builds them on the fly.
+struct WorkItem {
+  int32_t tensor;  // index into the plan's descriptors
+  int32_t bucket;
+  int32_t ra, c0, cl;  // row_offsets[b], col_start[b], col_len[b]
+  int32_t rows, k_eff, path;
+  int64_t bit_base;            // bucket_bit_base[b]
+  const int32_t *table_ids;    // bucket_table + 256 b
+  const uint32_t *startbits;   // bucket_thread_startbit + (k + 1) b
+  const int32_t *row_idx;      // row_indices + ra
+};
+static_assert(sizeof(WorkItem) == 64, "one scalar load per work item");
 
 // One lane: decode its substream.
 //
@@ -668,11 +710,10 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
 //    one contiguous 128-byte segment.
 // Bitstream: a lane requests up to 64 bytes at a time into a register reserve
 // (aligned so that each request touches one half of a 128-byte line) and,
-// once per four groups, moves 16 bytes from the reserve into its LDS queue.
-// When every lane of the wave then holds enough bits for four windows, the
-// four groups skip the per-window dry check. FP8 dwords are loaded DF groups
-// ahead. Every group issues the same vector-memory instructions, so the
-// in-order vmcnt waits stay static.
+// once per four groups, moves 16 bytes from the reserve into its LDS queue;
+// a window whose chunks are not queued is read from memory. FP8 dwords are
+// loaded DF groups ahead. Every group issues the same vector-memory
+// instructions, so the in-order vmcnt waits stay static.
 //
 // The queue here stores chunk h in slot (~h) & 7 (slot-major, 4 KiB per
 // slot), and positions are kept negated (np = -p, p biased by two chunks as
@@ -925,7 +966,28 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   if (0u - np - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
 }
 
-__device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b, uint32_t *lds, uint32_t *status) {
+// The work item of bucket b of tensor T (the single-tensor kernel).
+__device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t b) {
+  WorkItem w;
+  w.tensor = 0;
+  w.bucket = (int32_t)b;
+  w.ra = T.bucket_row_offsets[b];
+  const int32_t rb = T.bucket_row_offsets[b + 1];
+  w.c0 = T.bucket_col_start[b];
+  w.cl = T.bucket_col_len[b];
+  const BucketShape s = bucket_shape(w.ra, rb, w.c0, w.cl, T);
+  w.rows = s.rows;
+  w.k_eff = s.k_eff;
+  w.path = s.path;
+  w.bit_base = T.bucket_bit_base[b];
+  w.table_ids = T.bucket_table + b * 256;
+  w.startbits = T.bucket_thread_startbit + b * (T.k + 1);
+  w.row_idx = T.row_indices + (s.path != kPathBad ? w.ra : 0);
+  return w;
+}
+
+__device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const WorkItem &w, uint32_t *lds,
+                                              uint32_t *status) {
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
@@ -934,28 +996,19 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(T.decode_syms) & 15u) == 0) &&
                       ((reinterpret_cast<uintptr_t>(T.decode_lens) & 3u) == 0);
 
-  const int32_t ra = T.bucket_row_offsets[b];
-  const int32_t rb = T.bucket_row_offsets[b + 1];
-  const int32_t c0 = T.bucket_col_start[b];
-  const int32_t cl = T.bucket_col_len[b];
-  const bool bucket_ok = ra >= 0 && rb >= ra && (int64_t)rb <= T.num_row_indices && rb - ra <= kRowsLds &&
-                         cl > 0 && c0 >= 0 && (int64_t)c0 + cl <= T.m;
-  const int32_t rows = bucket_ok ? rb - ra : 0;
+  const int32_t c0 = w.c0, cl = w.cl, rows = w.rows, k_eff = w.k_eff;
+  const bool bucket_ok = w.path != kPathBad;
   const int64_t total = (int64_t)rows * cl;
-  const int32_t k_eff = (int32_t)(T.k < total ? T.k : (total > 0 ? total : 1));
   const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
-  const bool small_stream = (uint64_t)T.bitstream_words < 0x10000000ull;
-  // k = 1024 path (any tensor below 2^31 elements) and the general fast path.
-  const bool k1024 = bucket_ok && rows <= 128 && k_eff == 1024 && cl % 1024 == 0 &&
-                     nm <= (1ull << 31) - 16u && small_stream;
-  const bool fast = !k1024 && bucket_ok && rows <= 128 && cl % k_eff == 0 && nm <= (1ull << 29) && small_stream;
+  const bool k1024 = w.path == kPathK1024;
+  const bool fast = w.path == kPathFast;
   const int lane = tid;
   // Substream of this work-item: the k = 1024 paths give wave w's 16-lane row
   // R, position v the column 64w + 4v + R (see decode_slab4); the others, the lane.
   const int col = k1024 ? ((tid & ~63) | ((tid & 15) << 2) | ((tid >> 4) & 3)) : tid;
   const bool active = bucket_ok && rows > 0 && lane < k_eff;
-  const uint32_t *sb = T.bucket_thread_startbit + b * (T.k + 1);
-  const uint64_t base = (uint64_t)T.bucket_bit_base[b];
+  const uint32_t *sb = w.startbits;
+  const uint64_t base = (uint64_t)w.bit_base;
 
   // Set-up keeps the chains of dependent memory reads short (bucket -> table
   // ids -> table contents; bucket -> start bits -> first bitstream words): all
@@ -969,7 +1022,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   bool bad_table = false;
 #pragma unroll
   for (int i = 0; i < kSlices; ++i) {
-    int32_t g = T.bucket_table[b * 256 + (tid >> 4) + 64 * i];
+    int32_t g = w.table_ids[(tid >> 4) + 64 * i];
     if (g < -1 || g >= T.num_tables) {
       bad_table = true;
       g = -1;
@@ -984,12 +1037,12 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   if (k1024 || fast) {
     const int wl = lane & 63;
     if (wl < rows) {
-      const int32_t r = T.row_indices[ra + wl];
+      const int32_t r = w.row_idx[wl];
       bad_row |= r < 0 || r >= T.n;
       rowoff_lo = (uint32_t)r * (uint32_t)T.m + (uint32_t)c0;
     }
     if (wl + 64 < rows) {
-      const int32_t r = T.row_indices[ra + wl + 64];
+      const int32_t r = w.row_idx[wl + 64];
       bad_row |= r < 0 || r >= T.n;
       rowoff_hi = (uint32_t)r * (uint32_t)T.m + (uint32_t)c0;
     }
@@ -1016,7 +1069,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
   }
   if (!k1024 && !fast) {
     for (int i = tid; i < rows; i += kBlock) {
-      const int32_t r = T.row_indices[ra + i];
+      const int32_t r = w.row_idx[i];
       bad_row |= r < 0 || r >= T.n;
       s_rows[i] = r;
     }
@@ -1127,7 +1180,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, int64_t b
 __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
-    decode_bucket(T, b, lds, status);
+    decode_bucket(T, bucket_item(T, b), lds, status);
     __syncthreads();  // the next bucket's set-up overwrites the LDS
   }
 }
@@ -1138,7 +1191,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   for (int64_t i = blockIdx.x; i < nwork; i += gridDim.x) {
     const WorkItem w = work[i];
-    decode_bucket(tensors[w.tensor], w.bucket, lds, status);
+    decode_bucket(tensors[w.tensor], w, lds, status);
     __syncthreads();  // the next bucket's set-up overwrites the LDS
   }
 }
@@ -1250,20 +1303,39 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
   // bucket's cost is its element count plus a fixed set-up share.
   std::vector<WorkItem> work;
   std::vector<int64_t> cost;
-  std::vector<int32_t> roff, clen;
+  std::vector<int32_t> roff, cstart, clen;
+  std::vector<int64_t> bbase;
   for (int64_t i = 0; i < count; ++i) {
-    int rc = check_tensor(&tensors[i]);
+    const mps_fp8_tensor &T = tensors[i];
+    int rc = check_tensor(&T);
     if (rc != MPS_OK) return rc;
-    const int64_t nb = tensors[i].num_buckets;
+    const int64_t nb = T.num_buckets;
     if (nb == 0) continue;
     roff.resize((size_t)nb + 1);
+    cstart.resize((size_t)nb);
     clen.resize((size_t)nb);
-    MPS_HIP_CHECK(hipMemcpy(roff.data(), tensors[i].bucket_row_offsets, sizeof(int32_t) * (nb + 1), hipMemcpyDefault));
-    MPS_HIP_CHECK(hipMemcpy(clen.data(), tensors[i].bucket_col_len, sizeof(int32_t) * nb, hipMemcpyDefault));
+    bbase.resize((size_t)nb);
+    MPS_HIP_CHECK(hipMemcpy(roff.data(), T.bucket_row_offsets, sizeof(int32_t) * (nb + 1), hipMemcpyDefault));
+    MPS_HIP_CHECK(hipMemcpy(cstart.data(), T.bucket_col_start, sizeof(int32_t) * nb, hipMemcpyDefault));
+    MPS_HIP_CHECK(hipMemcpy(clen.data(), T.bucket_col_len, sizeof(int32_t) * nb, hipMemcpyDefault));
+    MPS_HIP_CHECK(hipMemcpy(bbase.data(), T.bucket_bit_base, sizeof(int64_t) * nb, hipMemcpyDefault));
     for (int64_t b = 0; b < nb; ++b) {
-      work.push_back({(int32_t)i, (int32_t)b});
-      const int64_t rows = (int64_t)roff[b + 1] - roff[b];
-      cost.push_back((rows > 0 && clen[b] > 0 ? rows * clen[b] : 0) + 65536);
+      const BucketShape s = bucket_shape(roff[b], roff[b + 1], cstart[b], clen[b], T);
+      WorkItem w;
+      w.tensor = (int32_t)i;
+      w.bucket = (int32_t)b;
+      w.ra = roff[b];
+      w.c0 = cstart[b];
+      w.cl = clen[b];
+      w.rows = s.rows;
+      w.k_eff = s.k_eff;
+      w.path = s.path;
+      w.bit_base = bbase[b];
+      w.table_ids = T.bucket_table + b * 256;
+      w.startbits = T.bucket_thread_startbit + b * (T.k + 1);
+      w.row_idx = T.row_indices + (s.path != kPathBad ? w.ra : 0);
+      work.push_back(w);
+      cost.push_back((int64_t)s.rows * (s.path != kPathBad ? clen[b] : 0) + 65536);
     }
   }
   if (work.size() > (size_t)INT32_MAX) return fail(MPS_ERR_INVALID_ARGUMENT, "too many buckets for one plan");
