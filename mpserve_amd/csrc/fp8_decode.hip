@@ -944,8 +944,33 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   uint32_t Fr[DF], SOr[DF];
 #pragma unroll
   for (int u = 0; u < DF; ++u) SOr[u] = load_group(Fr[u]);
+  // Every wave of the workgroup decodes the same number of groups, but the
+  // issue arbiter favours the oldest ready wave (waves 4r..4r+3 are the r-th
+  // oldest on their SIMDs): left alone, the oldest waves finish first and the
+  // bucket ends with a few young waves and little latency hiding. So a wave
+  // lowers its priority by one level per quarter of its groups, counted from
+  // a head start that grows with its age: older waves yield issue slots to
+  // younger ones, and a wave that is ahead to the ones behind.
+#ifndef MPS_PRIO_LEAD
+#define MPS_PRIO_LEAD 8
+#endif
+  const uint32_t quarter = uni(nfull / 4u > 0u ? nfull / 4u : 1u);
+  const uint32_t lead = (3u - (uni(lane) >> 8)) * (quarter * MPS_PRIO_LEAD / 16u);  // head start (groups)
+  uint32_t prio = 3u - (lead / quarter < 3u ? lead / quarter : 3u);
+  uint32_t prio_at = (lead / quarter + 1u) * quarter - lead;  // groups done when the priority next drops
+  if (prio == 3u) __builtin_amdgcn_s_setprio(3);
+  else if (prio == 2u) __builtin_amdgcn_s_setprio(2);
+  else if (prio == 1u) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
   uint32_t g = 0;
   for (; g + (uint32_t)DF <= nfull; g += (uint32_t)DF) {
+    if (g >= prio_at) {
+      prio_at += quarter;
+      --prio;
+      if (prio == 2u) __builtin_amdgcn_s_setprio(2);
+      else if (prio == 1u) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
 #pragma unroll
     for (int u = 0; u < DF; ++u) {
       if (u % 4 == 0) bitstream_step();
@@ -954,6 +979,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
       group(std::false_type{}, F, so);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   // the last (fewer than DF) full groups and the partial one; their FP8 is already loaded
 #pragma unroll
   for (int u = 0; u < DF; ++u) {
