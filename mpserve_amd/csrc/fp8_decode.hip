@@ -1018,9 +1018,11 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
   uint32_t *lut = lds + kQWords;
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
   uint32_t *s_wflag = qregion + 5 * kBlock;                             // queue slot 5: one word per wave
-  const int tid = threadIdx.x;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(T.decode_syms) & 15u) == 0) &&
-                      ((reinterpret_cast<uintptr_t>(T.decode_lens) & 3u) == 0);
+  // The work-item id through an opaque move: the per-lane constants of every
+  // decode path derive from it, and hoisted out of the bucket loop they would
+  // all stay live across the set-up, which then runs out of VGPRs.
+  int tid;
+  __asm__ volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
 
   const int32_t c0 = w.c0, cl = w.cl, rows = w.rows, k_eff = w.k_eff;
   const bool bucket_ok = w.path != kPathBad;
@@ -1036,78 +1038,93 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
   const uint32_t *sb = w.startbits;
   const uint64_t base = (uint64_t)w.bit_base;
 
-  // Set-up keeps the chains of dependent memory reads short (bucket -> table
-  // ids -> table contents; bucket -> start bits -> first bitstream words): all
-  // loads of a level are issued before any of their results is used.
+  // Set-up: two levels of loads, each issued in full before any of its
+  // results is used. (1) From the work record alone: the table ids, the row
+  // indices (fast paths) and the lane's start bits. (2) From those: the
+  // tables' contents and the lane's first bitstream words. They are buffer
+  // loads, whose lanes out of range read zeros, so that none sits behind a
+  // branch: a load under a branch is waited for where the branch joins.
   //
   // Thread tid expands the 16-byte slice tid % 16 of the tables of FP8 bytes
-  // tid / 16 + 64 i (i < 4); their ids are read straight from memory (16
-  // threads share each) and validated.
+  // tid / 16 + 64 i (i < 4); 16 threads read each id.
   constexpr int kSlices = 256 * (kTable / 8) / kBlock;  // 4
+  const bool rows_fast = k1024 || fast;
+  const int wl = lane & 63;
+  const __amdgpu_buffer_rsrc_t r_ids = make_rsrc(w.table_ids, 256u * 4u);
+  const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(w.row_idx, rows_fast ? (uint32_t)rows * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t r_sb = make_rsrc(sb, rows_fast ? ((uint32_t)k_eff + 1u) * 4u : 0u);
   int32_t gids[kSlices];
+#pragma unroll
+  for (int i = 0; i < kSlices; ++i)
+    gids[i] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_ids, (uint32_t)((tid >> 4) + 64 * i) * 4u, 0, 0);
+  const int32_t r_lo = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_rows, (uint32_t)wl * 4u, 0, 0);
+  const int32_t r_hi = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_rows, (uint32_t)(wl + 64) * 4u, 0, 0);
+  const uint32_t sb_off = active ? (uint32_t)col * 4u : kBsPast;
+  uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(r_sb, sb_off, 0, 0);
+  uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_sb, sb_off + 4u, 0, 0);
+
   bool bad_table = false;
 #pragma unroll
   for (int i = 0; i < kSlices; ++i) {
-    int32_t g = w.table_ids[(tid >> 4) + 64 * i];
-    if (g < -1 || g >= T.num_tables) {
+    if (gids[i] < -1 || gids[i] >= T.num_tables) {
       bad_table = true;
-      g = -1;
-    }
-    gids[i] = g;
-  }
-  if (bad_table) flag(status, MPS_STATUS_BAD_TABLE);
-
-  // Row offsets: the fast paths keep rows 0..63 / 64..127 one per lane in VGPRs.
-  bool bad_row = false;
-  uint32_t rowoff_lo = 0, rowoff_hi = 0;
-  if (k1024 || fast) {
-    const int wl = lane & 63;
-    if (wl < rows) {
-      const int32_t r = w.row_idx[wl];
-      bad_row |= r < 0 || r >= T.n;
-      rowoff_lo = (uint32_t)r * (uint32_t)T.m + (uint32_t)c0;
-    }
-    if (wl + 64 < rows) {
-      const int32_t r = w.row_idx[wl + 64];
-      bad_row |= r < 0 || r >= T.n;
-      rowoff_hi = (uint32_t)r * (uint32_t)T.m + (uint32_t)c0;
+      gids[i] = -1;
     }
   }
-  // First four bitstream words of this lane (two 16-byte loads), loaded before
-  // the table set-up; the slab path queues all four, the others three.
-  uint32_t pos = 0, pos_end = 0;
-  uint2 first[4] = {make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0), make_uint2(0, 0)};
-  if ((k1024 || fast) && active) {
-    pos = sb[col];
-    pos_end = sb[col + 1];
+  // Row offsets: the fast paths keep rows 0..63 / 64..127 one per lane in
+  // VGPRs (selects, not a branch, so the loads above are not sunk into one).
+  const bool has_lo = rows_fast && wl < rows, has_hi = rows_fast && wl + 64 < rows;
+  bool bad_row = (has_lo && (r_lo < 0 || r_lo >= T.n)) | (has_hi && (r_hi < 0 || r_hi >= T.n));
+  const uint32_t rowoff_lo = has_lo ? (uint32_t)r_lo * (uint32_t)T.m + (uint32_t)c0 : 0u;
+  const uint32_t rowoff_hi = has_hi ? (uint32_t)r_hi * (uint32_t)T.m + (uint32_t)c0 : 0u;
+  // First four bitstream words of this lane (two 16-byte loads); the slab
+  // path queues all four, the others three.
+  uint2 first[4];
+  {
     const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
     const uint64_t base_byte = base >> 3;
-    const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+    const uint32_t win_bytes = rows_fast && base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
     const __amdgpu_buffer_rsrc_t r_bs = make_rsrc(
         reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
-    const uint32_t rq0 = (pos >> 5) & ~1u;
+    const uint32_t off0 = active ? ((pos >> 5) & ~1u) * 4u : kBsPast;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, (rq0 + 4 * i) * 4u, 0, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off0 + 16u * (uint32_t)i, 0, 0);
       first[2 * i] = make_uint2(v[0], v[1]);
       first[2 * i + 1] = make_uint2(v[2], v[3]);
     }
   }
-  if (!k1024 && !fast) {
+  // The tables' contents (buffer loads when their byte offsets fit 31 bits).
+  uint4 sv[kSlices];
+  uint32_t nibs[kSlices];
+  const int part = tid & 15;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(T.decode_syms) & 15u) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(T.decode_lens) & 3u) == 0);
+  const bool tab_buffer = vec_ok && T.num_tables <= (1 << 22);
+  if (tab_buffer) {
+    const uint32_t ntab = (uint32_t)T.num_tables;
+    const __amdgpu_buffer_rsrc_t r_syms = make_rsrc(T.decode_syms, ntab * (uint32_t)(kTable * 2));
+    const __amdgpu_buffer_rsrc_t r_lens = make_rsrc(T.decode_lens, ntab * (uint32_t)kPacked);
+#pragma unroll
+    for (int i = 0; i < kSlices; ++i) {
+      const bool has = gids[i] >= 0;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+          r_syms, has ? (uint32_t)gids[i] * (uint32_t)(kTable * 2) + (uint32_t)part * 16u : 0x80000000u, 0, 0);
+      sv[i] = make_uint4(v[0], v[1], v[2], v[3]);
+      nibs[i] = __builtin_amdgcn_raw_buffer_load_b32(
+          r_lens, has ? (uint32_t)gids[i] * (uint32_t)kPacked + (uint32_t)part * 4u : 0x80000000u, 0, 0);
+    }
+  }
+  if (bad_table) flag(status, MPS_STATUS_BAD_TABLE);
+  if (!rows_fast) {
     for (int i = tid; i < rows; i += kBlock) {
       const int32_t r = w.row_idx[i];
       bad_row |= r < 0 || r >= T.n;
       s_rows[i] = r;
     }
   }
-
-  // Expand the bucket's 256 tables into 32-bit LDS entries {sym << 16 | esc << 4 | len}:
-  // first every slice's loads, then the expansion.
-  uint4 sv[kSlices];
-  uint32_t nibs[kSlices];
-  const int part = tid & 15;
 #pragma unroll
-  for (int i = 0; i < kSlices; ++i) {
+  for (int i = 0; i < kSlices && !tab_buffer; ++i) {
     const int32_t g = gids[i];
     sv[i] = make_uint4(0u, 0u, 0u, 0u);
     nibs[i] = 0;
@@ -1199,6 +1216,15 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
   }
 }
 
+// End of a bucket: drain the wave's memory counters (its last stores and the
+// FP8 and bitstream prefetches past its substream's end) before the barrier,
+// where the wait overlaps the other waves' last groups. The next set-up then
+// starts with nothing outstanding, and none of its loads waits behind these.
+__device__ __forceinline__ void end_bucket() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // the next bucket's set-up overwrites the LDS
+}
+
 // Both kernels are persistent: one workgroup per CU (the LDS holds one
 // bucket's tables) walks its share of the buckets, so a bucket's set-up does
 // not also pay a workgroup launch. Every workgroup runs the same uniform loop
@@ -1207,7 +1233,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
     decode_bucket(T, bucket_item(T, b), lds, status);
-    __syncthreads();  // the next bucket's set-up overwrites the LDS
+    end_bucket();
   }
 }
 
@@ -1215,10 +1241,16 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
                                                           const WorkItem *__restrict__ work, int64_t nwork,
                                                           uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+  if ((int64_t)blockIdx.x >= nwork) return;
+  // The next bucket's record (scalar registers) is loaded with this bucket's
+  // set-up, so the next set-up starts one round trip shorter.
+  WorkItem w = work[blockIdx.x];
   for (int64_t i = blockIdx.x; i < nwork; i += gridDim.x) {
-    const WorkItem w = work[i];
+    const int64_t inext = i + gridDim.x;
+    const WorkItem wn = work[inext < nwork ? inext : i];
     decode_bucket(tensors[w.tensor], w, lds, status);
-    __syncthreads();  // the next bucket's set-up overwrites the LDS
+    end_bucket();
+    w = wn;
   }
 }
 
