@@ -72,10 +72,12 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
 
 /* Batched decode plan: one launch decodes many tensors (a layer, a model).
  * The plan copies the descriptors to device memory it owns and reads each
- * tensor's bucket row offsets and column lengths to order the buckets largest
- * first (synchronously, at create time); the pointed-to sidecars must stay
- * alive while the plan is used. Launches (like mps_fp8_decode's) are
- * persistent: one workgroup per CU walks its share of the buckets.
+ * tensor's bucket row offsets, column ranges and bit bases (synchronously, at
+ * create time) to order the buckets largest first and to build one work record
+ * per bucket; a sidecar whose bucket metadata is rewritten needs a new plan.
+ * The pointed-to sidecars must stay alive while the plan is used. Launches
+ * (like mps_fp8_decode's) are persistent: one workgroup per CU walks its share
+ * of the buckets.
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:739); it serves its apply() and model loading paths
  * (scripts/mpserve_vllm_fp8_huffman.py:491-557). */
