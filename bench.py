@@ -47,8 +47,10 @@ def parse_args(argv=None):
     # load: with 3 warm-up launches a fresh box measures the model decode ~4%
     # slower than after 1000 (about 6 s).
     p.add_argument("--warmup", type=int, default=1000)
-    p.add_argument("--workload", choices=("model8b", "layer8b"), default="model8b",
-                   help="model8b: full Llama-3-8B-shaped model (the headline); layer8b: one layer")
+    p.add_argument("--workload", choices=("model8b", "layer8b", "layer70b", "gemm8b"), default="model8b",
+                   help="model8b: full Llama-3-8B-shaped model (the headline, config 5); layer8b: one 8B "
+                        "layer (config 2); layer70b: one 70B layer with outliers and ESC codes (config 3); "
+                        "gemm8b: decode share of an 8B layer's latency next to its BF16 GEMMs (config 4)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="time budget of the CPU baseline sample")
     p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: min(16, cpu_count))")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -59,18 +61,164 @@ def parse_args(argv=None):
     return p.parse_args(argv)
 
 
-def weight_list(workload: str):
-    from mpserve_amd.synthetic import LLAMA3_8B_LAYER, LLAMA3_8B_LM_HEAD
+WORKLOADS = {
+    "model8b": "cfg5: Llama-3-8B-shaped full model, 32 layers x 7 linears + lm_head 128256x4096",
+    "layer8b": "cfg2: one Llama-3-8B layer, 7 linears",
+    "layer70b": "cfg3: one Llama-3-70B layer, 7 linears, sigma 0.015 with 0.1% outliers at +-8 sigma",
+    "gemm8b": "cfg4: one Llama-3-8B layer decoded into preallocated scratch + BF16 GEMMs, T in {1,16,128,1024}",
+}
 
+
+def weight_list(workload: str):
+    """(name, n, m, seed, sigma, outlier_p) of every weight of a workload."""
+    from mpserve_amd.synthetic import LLAMA3_8B_LAYER, LLAMA3_8B_LM_HEAD, LLAMA3_70B_LAYER
+
+    if workload == "layer70b":
+        return [(f"layers.0.{name}", n, m, 200 + j, 0.015, 1e-3) for j, (name, n, m) in enumerate(LLAMA3_70B_LAYER)]
     layers = 32 if workload == "model8b" else 1
     out = []
     for layer in range(layers):
         for j, (name, n, m) in enumerate(LLAMA3_8B_LAYER):
-            out.append((f"layers.{layer}.{name}", n, m, 100 + 16 * layer + j))
+            out.append((f"layers.{layer}.{name}", n, m, 100 + 16 * layer + j, 0.02, 0.0))
     if workload == "model8b":
         name, n, m = LLAMA3_8B_LM_HEAD
-        out.append((name, n, m, 99))
+        out.append((name, n, m, 99, 0.02, 0.0))
     return out
+
+
+def data_note(workload: str) -> str:
+    if workload == "layer70b":
+        return ("synthetic: seeded N(0,0.015^2) BF16 with 0.1% outliers at +-8 sigma, per-channel FP8 e4m3, "
+                "sidecar built on the GPU")
+    return "synthetic: seeded N(0,0.02^2) BF16, per-channel FP8 e4m3, sidecar built on the GPU"
+
+
+def time_per_tensor(entries, outs, stream, reps: int = 20):
+    """Each tensor decoded alone through the drop-in op (one launch per tensor, as
+    the reference decodes), timed with events around each launch on its stream."""
+    import torch
+
+    import MPServe_cuda
+    from mpserve_amd.decode import sidecar_decode_args
+
+    rows = []
+    for (name, fp8, sc, src), o in zip(entries, outs):
+        n, m = int(fp8.shape[0]), int(fp8.shape[1])
+        call = sidecar_decode_args(fp8, sc)
+        for _ in range(3):
+            MPServe_cuda.huffman_decode_fp8(*call, out=o)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for s, e in ev:
+            s.record(stream)
+            MPServe_cuda.huffman_decode_fp8(*call, out=o)
+            e.record(stream)
+        torch.cuda.synchronize()
+        if not torch.equal(o.view(torch.uint16), src.view(torch.uint16)):
+            raise RuntimeError(f"per-tensor decode of {name} is not bit-exact")
+        ms = sum(s.elapsed_time(e) for s, e in ev) / reps
+        alg = algorithmic_bytes(n, m, sc)
+        rows.append({"tensor": name, "shape": [n, m], "ms": round(ms, 4),
+                     "out_gbs": round(2 * n * m / ms / 1e6, 1), "rw_gbs": round(alg / ms / 1e6, 1),
+                     "pct_hbm_peak_rw": round(100.0 * alg / ms / 1e6 / HBM_PEAK_GBS, 2),
+                     "buckets": int(sc["bucket_table_i32"].shape[0]),
+                     "esc_tables": int(((sc["decode_lens_u8"] & 0x88) != 0).any(dim=1).sum().item())})
+        log(f"{name} {n}x{m}: {ms:.4f} ms, {rows[-1]['rw_gbs']} GB/s R+W ({rows[-1]['pct_hbm_peak_rw']}%)")
+    return rows
+
+
+def run_gemm(args, entries, outs, plan, dev) -> int:
+    """Config 4: per-layer latency of an 8B layer served from FP8 + sidecar. The
+    layer's 7 weights are decoded (one plan launch) into preallocated BF16
+    scratch, then its 7 BF16 GEMMs y = x W^T run for x [T, K], T in {1, 16, 128,
+    1024}. Sequential: decode, then GEMMs, on one stream. Overlapped: a chain of
+    8 layers in which layer i + 1's weights decode on a side stream (into the
+    second of two scratch sets) while layer i's GEMMs run."""
+    import torch
+    import torch.nn.functional as F
+
+    from mpserve_amd.decode import DecodePlan
+
+    stream = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev)
+    outs2 = [torch.empty_like(o) for o in outs]
+    plan2 = DecodePlan((fp8, sc, o) for (_, fp8, sc, _), o in zip(entries, outs2))
+    plans, bufs = (plan, plan2), (outs, outs2)
+    for _ in range(max(1, args.warmup)):
+        plan.decode(stream)
+    plan2.decode(stream)
+    torch.cuda.synchronize()
+    for (name, _, _, src), o, o2 in zip(entries, outs, outs2):
+        for buf in (o, o2):
+            if not torch.equal(buf.view(torch.uint16), src.view(torch.uint16)):
+                raise RuntimeError(f"decode of {name} is not bit-exact")
+    log("decoded scratch bit-exact")
+    chain = 8
+    g = torch.Generator(device=dev).manual_seed(4)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps
+
+    results = []
+    for T in (1, 16, 128, 1024):
+        xs = [torch.randn((T, o.shape[1]), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+              for o in outs]
+
+        def gemms(ws):
+            for x, w in zip(xs, ws):
+                F.linear(x, w)
+
+        def sequential():
+            plan.decode(stream)
+            gemms(outs)
+
+        def overlapped():
+            dec = [torch.cuda.Event(), torch.cuda.Event()]
+            used = [torch.cuda.Event(), torch.cuda.Event()]
+            side.wait_stream(stream)
+            plans[0].decode(side)
+            dec[0].record(side)
+            for i in range(chain):
+                b = i % 2
+                if i + 1 < chain:
+                    nb = (i + 1) % 2
+                    if i >= 1:
+                        side.wait_event(used[nb])  # layer i - 1's GEMMs are done with that scratch
+                    plans[nb].decode(side)
+                    dec[nb].record(side)
+                stream.wait_event(dec[b])
+                gemms(bufs[b])
+                used[b].record(stream)
+            stream.wait_stream(side)
+
+        t_gemm = timed(lambda: gemms(outs), 50)
+        t_dec = timed(lambda: plan.decode(stream), 50)
+        t_seq = timed(sequential, 50)
+        t_ovl = timed(overlapped, 10) / chain
+        results.append({"T": T, "gemm_ms": round(t_gemm, 4), "decode_ms": round(t_dec, 4),
+                        "sequential_ms": round(t_seq, 4), "overlapped_ms": round(t_ovl, 4),
+                        "decode_share_sequential": round((t_seq - t_gemm) / t_seq, 4),
+                        "decode_share_overlapped": round(max(0.0, t_ovl - t_gemm) / t_ovl, 4)})
+        log(f"T={T}: GEMMs {t_gemm:.4f} ms, decode {t_dec:.4f} ms, sequential {t_seq:.4f} ms, "
+            f"overlapped {t_ovl:.4f} ms per layer")
+    share16 = [r for r in results if r["T"] == 16][0]["decode_share_sequential"]
+    result = {
+        "metric": "cfg4: decode share of an 8B layer's latency (decode + 7 BF16 GEMMs), T=16",
+        "value": round(100.0 * share16, 2), "unit": "%", "n_gpus": 1, "steps": 50, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "u16+bf16",
+        "data": data_note(args.workload),
+        "config": {"workload": WORKLOADS[args.workload], "tensors": len(entries),
+                   "elements": sum(o.numel() for o in outs), "overlap_chain_layers": chain, "results": results},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def algorithmic_bytes(n: int, m: int, sc) -> int:
@@ -161,8 +309,8 @@ def main(argv=None) -> int:
     entries = []  # (name, fp8, sidecar, src)
     total_alg = 0
     total_side = 0
-    for i, (name, n, m, seed) in enumerate(weights):
-        w = make_weight(n, m, sigma=0.02, seed=seed, device=dev)
+    for i, (name, n, m, seed, sigma, outlier_p) in enumerate(weights):
+        w = make_weight(n, m, sigma=sigma, seed=seed, outlier_p=outlier_p, device=dev)
         sc = build_fp8_sidecar(w.bf16, w.fp8_u8, w.scale_u16, max_len=7, threads_per_block=1024)
         entries.append((name, w.fp8_u8, sc, w.bf16))
         total_alg += algorithmic_bytes(n, m, sc)
@@ -178,6 +326,8 @@ def main(argv=None) -> int:
     elems = sum(o.numel() for o in outs)
     bf16_bytes = 2 * elems
     stream = torch.cuda.current_stream(dev)
+    if args.workload == "gemm8b":
+        return run_gemm(args, entries, outs, plan, dev)
 
     for _ in range(max(1, args.warmup)):
         plan.decode(stream)
@@ -206,6 +356,7 @@ def main(argv=None) -> int:
         for (name, _, _, src), o in zip(entries, outs):
             if not torch.equal(o.view(torch.uint16), src.view(torch.uint16)):
                 raise RuntimeError(f"timed decode of {name} is not bit-exact")
+    per_tensor = time_per_tensor(entries, outs, stream) if args.workload != "model8b" else None
 
     if args.copy_calibration > 0:
         n32 = args.copy_calibration * (1 << 20) // 4
@@ -241,10 +392,9 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u16",
-        "data": "synthetic: seeded N(0,0.02^2) BF16, per-channel FP8 e4m3, sidecar built on the GPU",
+        "data": data_note(args.workload),
         "config": {
-            "workload": ("cfg5: Llama-3-8B-shaped full model, 32 layers x 7 linears + lm_head 128256x4096"
-                         if args.workload == "model8b" else "cfg2: one Llama-3-8B layer, 7 linears"),
+            "workload": WORKLOADS[args.workload],
             "tensors": len(entries),
             "elements": elems,
             "max_len": 7,
@@ -256,6 +406,12 @@ def main(argv=None) -> int:
             "sidecar_plus_fp8_over_bf16": round((total_side + fp8_bytes) / bf16_bytes, 4),
             "build_s": round(build_s, 2),
             "plan": plan.info(),
+            # LDS per workgroup (the bucket's 256 expanded tables + the bitstream queues) and waves per CU
+            "lds_occupancy": {"bytes_per_workgroup": plan.info()["lds_bytes"], "of_cu_lds": 163840,
+                              "workgroups_per_cu": 1, "waves_per_cu": 16},
+            "esc_tables": sum(int(((sc["decode_lens_u8"] & 0x88) != 0).any(dim=1).sum().item())
+                              for _, _, sc, _ in entries),
+            "per_tensor": per_tensor,
         },
         "roofline": {
             "bound": "hbm",
