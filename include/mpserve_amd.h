@@ -73,18 +73,24 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
 /* Batched decode plan: one launch decodes many tensors (a layer, a model).
  * The plan copies the descriptors to device memory it owns and reads each
  * tensor's bucket row offsets, column ranges and bit bases (synchronously, at
- * create time) to order the buckets largest first and to build one work record
- * per bucket; a sidecar whose bucket metadata is rewritten needs a new plan.
- * The pointed-to sidecars must stay alive while the plan is used. Launches
- * (like mps_fp8_decode's) are persistent: one workgroup per CU walks its share
- * of the buckets.
+ * create time) to order the work largest first and to build one work record
+ * per bucket. When the buckets are few or uneven for the device's CUs, large
+ * buckets are split into row ranges: a kernel on the legacy default stream
+ * walks their substreams' code lengths once and records each substream's bit
+ * position at every range's first row (the lane checkpoints, owned by the
+ * plan). A sidecar whose bucket metadata, row indices, start bits, tables,
+ * FP8 bytes or bitstream is rewritten needs a new plan in that case. The
+ * pointed-to sidecars must stay alive while the plan is used. Launches (like
+ * mps_fp8_decode's) are persistent: one workgroup per CU walks its share of
+ * the work.
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:739); it serves its apply() and model loading paths
  * (scripts/mpserve_vllm_fp8_huffman.py:491-557). */
 typedef struct mps_fp8_plan mps_fp8_plan;
 int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_plan **plan_out);
 int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream);
-/* The plan's work list (for profiling tools): buckets, bytes of LDS per workgroup. */
+/* The plan's work list (for profiling tools): work items (buckets, and the row
+ * ranges of the buckets it split), bytes of LDS per workgroup. */
 int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes);
 int mps_fp8_plan_destroy(mps_fp8_plan *plan);
 

@@ -87,19 +87,24 @@ __host__ __device__ inline BucketShape bucket_shape(int32_t ra, int32_t rb, int3
   return s;
 }
 
-// One bucket to decode: its tensor, ranges, shape and the addresses of its
-// per-bucket arrays. A plan builds these once (64 bytes: one scalar load per
-// bucket, which leaves the table ids, row indices and start bits one
-// dependent load away); the single-tensor kernel builds them on the fly.
+// One unit of decode work: a bucket, or a range of its rows. Its tensor,
+// column range, shape and the addresses of its per-bucket arrays. Substream
+// (lane) t starts at bit bit_base + startbits[t] and ends at bit_base +
+// endbits[t]: for a whole bucket, its start bits and the next lane's
+// (endbits = startbits + 1); for a row range, the lane checkpoints the plan
+// computed at the range's first and next range's first row. A plan builds
+// these once (64 bytes: one scalar load per item, which leaves the table ids,
+// row indices and start bits one dependent load away); the single-tensor
+// kernel builds them on the fly.
 struct WorkItem {
-  int32_t tensor;  // index into the plan's descriptors
-  int32_t bucket;
-  int32_t ra, c0, cl;  // row_offsets[b], col_start[b], col_len[b]
+  int32_t tensor;       // index into the plan's descriptors
+  int32_t c0, cl;       // col_start[b], col_len[b]
   int32_t rows, k_eff, path;
   int64_t bit_base;            // bucket_bit_base[b]
   const int32_t *table_ids;    // bucket_table + 256 b
-  const uint32_t *startbits;   // bucket_thread_startbit + (k + 1) b
-  const int32_t *row_idx;      // row_indices + ra
+  const uint32_t *startbits;   // per substream: start bit, relative to bit_base
+  const uint32_t *endbits;     // per substream: end bit, relative to bit_base
+  const int32_t *row_idx;      // row_indices + row_offsets[b] (+ the range's first row)
 };
 static_assert(sizeof(WorkItem) == 64, "one scalar load per work item");
 
@@ -996,19 +1001,19 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
 __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t b) {
   WorkItem w;
   w.tensor = 0;
-  w.bucket = (int32_t)b;
-  w.ra = T.bucket_row_offsets[b];
+  const int32_t ra = T.bucket_row_offsets[b];
   const int32_t rb = T.bucket_row_offsets[b + 1];
   w.c0 = T.bucket_col_start[b];
   w.cl = T.bucket_col_len[b];
-  const BucketShape s = bucket_shape(w.ra, rb, w.c0, w.cl, T);
+  const BucketShape s = bucket_shape(ra, rb, w.c0, w.cl, T);
   w.rows = s.rows;
   w.k_eff = s.k_eff;
   w.path = s.path;
   w.bit_base = T.bucket_bit_base[b];
   w.table_ids = T.bucket_table + b * 256;
   w.startbits = T.bucket_thread_startbit + b * (T.k + 1);
-  w.row_idx = T.row_indices + (s.path != kPathBad ? w.ra : 0);
+  w.endbits = w.startbits + 1;
+  w.row_idx = T.row_indices + (s.path != kPathBad ? ra : 0);
   return w;
 }
 
@@ -1052,7 +1057,8 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
   const int wl = lane & 63;
   const __amdgpu_buffer_rsrc_t r_ids = make_rsrc(w.table_ids, 256u * 4u);
   const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(w.row_idx, rows_fast ? (uint32_t)rows * 4u : 0u);
-  const __amdgpu_buffer_rsrc_t r_sb = make_rsrc(sb, rows_fast ? ((uint32_t)k_eff + 1u) * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t r_sb = make_rsrc(sb, rows_fast ? (uint32_t)k_eff * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t r_eb = make_rsrc(w.endbits, rows_fast ? (uint32_t)k_eff * 4u : 0u);
   int32_t gids[kSlices];
 #pragma unroll
   for (int i = 0; i < kSlices; ++i)
@@ -1061,7 +1067,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
   const int32_t r_hi = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_rows, (uint32_t)(wl + 64) * 4u, 0, 0);
   const uint32_t sb_off = active ? (uint32_t)col * 4u : kBsPast;
   uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(r_sb, sb_off, 0, 0);
-  uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_sb, sb_off + 4u, 0, 0);
+  uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_eb, sb_off, 0, 0);
 
   bool bad_table = false;
 #pragma unroll
@@ -1208,7 +1214,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
                      rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
   } else {
     const uint64_t pos0 = base + sb[lane];
-    const uint64_t pend = base + sb[lane + 1];
+    const uint64_t pend = base + w.endbits[lane];
     if (nm <= 0xFFFFFFFFull)
       decode_lane<uint32_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
     else
@@ -1251,6 +1257,97 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
     decode_bucket(tensors[w.tensor], w, lds, status);
     end_bucket();
     w = wn;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Lane checkpoints: where each substream of a bucket stands at the first row
+// of each of its row ranges, so that a plan can decode the ranges as separate
+// work items (more work items than buckets when a plan has few).
+//
+// One workgroup per bucket to split (k = 1024 and fast paths: substream t's
+// i-th element is row i / P, column c0 + t + (i % P) * K). Thread t walks
+// substream t through the code lengths only: the FP8 byte picks the table,
+// the next 7 bits pick the length nibble, an ESC code skips 16 more bits (the
+// lossless decode's semantics). It records its position after each range's
+// last element. Row indices and table ids out of range stop the walk and mark
+// the job failed (the plan then keeps the bucket whole, and its decode
+// reports them).
+// ---------------------------------------------------------------------------
+struct SplitJob {
+  int32_t tensor;
+  int32_t K;           // substreams (k_eff)
+  int32_t P;           // col_len / K
+  int32_t rows;        // rows of the bucket
+  int32_t c0;          // first column
+  int32_t range_rows;  // rows per range (the last range may have fewer)
+  int32_t ranges;
+  int32_t pad;
+  int64_t bit_base;
+  int64_t out;         // first u32 of the job's checkpoints: [ranges - 1][K]
+  const int32_t *table_ids;
+  const uint32_t *startbits;
+  const int32_t *row_idx;
+};
+
+__global__ __launch_bounds__(kBlock) void fp8_checkpoints(const mps_fp8_tensor *__restrict__ tensors,
+                                                          const SplitJob *__restrict__ jobs,
+                                                          uint32_t *__restrict__ ckpt, uint32_t *__restrict__ failed) {
+  __shared__ int32_t s_gid[256];
+  __shared__ uint32_t s_lens[256 * kPacked / 4];  // packed length nibbles of each FP8 byte's table
+  const SplitJob J = jobs[blockIdx.x];
+  const mps_fp8_tensor &T = tensors[J.tensor];
+  const int tid = threadIdx.x;
+  if (tid < 256) {
+    int32_t g = J.table_ids[tid];
+    if (g < -1 || g >= T.num_tables) {
+      failed[blockIdx.x] = 1u;
+      g = -1;
+    }
+    s_gid[tid] = g;
+  }
+  __syncthreads();
+  for (int i = tid; i < 256 * kPacked; i += kBlock) {
+    const int32_t g = s_gid[i / kPacked];
+    reinterpret_cast<uint8_t *>(s_lens)[i] = g >= 0 ? T.decode_lens[(int64_t)g * kPacked + i % kPacked] : 0u;
+  }
+  __syncthreads();
+  if (tid >= J.K) return;
+  const bool empty = T.bitstream_words <= 0;
+  const uint32_t *__restrict__ bs32 = empty ? g_zero_chunks : reinterpret_cast<const uint32_t *>(T.bitstream);
+  const uint64_t nchunks = empty ? 2u : (uint64_t)T.bitstream_words * 2u;
+  const uint8_t *lens = reinterpret_cast<const uint8_t *>(s_lens);
+  uint64_t pos = (uint64_t)J.bit_base + J.startbits[tid];
+  uint64_t cidx = ~0ull;
+  uint32_t ca = 0, cb = 0;
+  const int64_t per_range = (int64_t)J.range_rows * J.P;
+  int64_t next = per_range;
+  int32_t row_idx = 0;
+  int32_t rr = -1, p = 0;  // element's row (within the bucket) and column block
+  for (int j = 1; j < J.ranges; ++j, next += per_range) {
+    for (int64_t i = next - per_range; i < next; ++i) {
+      if (rr != (int32_t)(i / J.P)) {
+        rr = (int32_t)(i / J.P);
+        p = 0;
+        row_idx = J.row_idx[rr];
+        if (row_idx < 0 || row_idx >= T.n) {
+          failed[blockIdx.x] = 1u;
+          return;
+        }
+      }
+      const uint8_t q = T.fp8[(int64_t)row_idx * T.m + J.c0 + tid + (int64_t)p * J.K];
+      ++p;
+      const uint64_t c = pos >> 5;
+      if (c != cidx) {
+        cidx = c;
+        ca = chunk_at(bs32, nchunks, c);
+        cb = chunk_at(bs32, nchunks, c + 1);
+      }
+      const uint32_t peek = (uint32_t)(((((uint64_t)ca << 32) | cb) << (pos & 31u)) >> 57);
+      const uint32_t nib = (lens[q * kPacked + (peek >> 1)] >> ((peek & 1u) * 4u)) & 0xFu;
+      pos += (nib & 7u) + ((nib & 8u) ? 16u : 0u);
+    }
+    ckpt[J.out + (int64_t)(j - 1) * J.K + tid] = (uint32_t)(pos - (uint64_t)J.bit_base);
   }
 }
 
@@ -1314,6 +1411,7 @@ using namespace mps;
 struct mps_fp8_plan {
   mps_fp8_tensor *d_tensors = nullptr;
   WorkItem *d_work = nullptr;
+  uint32_t *d_ckpt = nullptr;  // lane checkpoints of the buckets split into row ranges
   int64_t count = 0;
   int64_t work_items = 0;
   int device = 0;
@@ -1356,11 +1454,9 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
   if (!plan_out) return fail(MPS_ERR_INVALID_ARGUMENT, "plan_out is NULL");
   *plan_out = nullptr;
   if (count < 0 || (count > 0 && !tensors)) return fail(MPS_ERR_INVALID_ARGUMENT, "invalid tensor list");
-  // Work items (buckets), largest first: the persistent launch deals them
-  // round-robin to the CUs, which then finish at about the same time. A
-  // bucket's cost is its element count plus a fixed set-up share.
-  std::vector<WorkItem> work;
-  std::vector<int64_t> cost;
+  // One work record per bucket.
+  std::vector<WorkItem> bucket;
+  std::vector<int64_t> elems;  // elements of each bucket (0: a bad bucket)
   std::vector<int32_t> roff, cstart, clen;
   std::vector<int64_t> bbase;
   for (int64_t i = 0; i < count; ++i) {
@@ -1381,8 +1477,6 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
       const BucketShape s = bucket_shape(roff[b], roff[b + 1], cstart[b], clen[b], T);
       WorkItem w;
       w.tensor = (int32_t)i;
-      w.bucket = (int32_t)b;
-      w.ra = roff[b];
       w.c0 = cstart[b];
       w.cl = clen[b];
       w.rows = s.rows;
@@ -1391,12 +1485,115 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
       w.bit_base = bbase[b];
       w.table_ids = T.bucket_table + b * 256;
       w.startbits = T.bucket_thread_startbit + b * (T.k + 1);
-      w.row_idx = T.row_indices + (s.path != kPathBad ? w.ra : 0);
-      work.push_back(w);
-      cost.push_back((int64_t)s.rows * (s.path != kPathBad ? clen[b] : 0) + 65536);
+      w.endbits = w.startbits + 1;
+      w.row_idx = T.row_indices + (s.path != kPathBad ? roff[b] : 0);
+      bucket.push_back(w);
+      elems.push_back(s.path != kPathBad ? (int64_t)s.rows * clen[b] : 0);
     }
   }
-  if (work.size() > (size_t)INT32_MAX) return fail(MPS_ERR_INVALID_ARGUMENT, "too many buckets for one plan");
+  if (bucket.size() > (size_t)INT32_MAX) return fail(MPS_ERR_INVALID_ARGUMENT, "too many buckets for one plan");
+  auto *p = new mps_fp8_plan();
+  p->count = count;
+  auto cleanup = [&](hipError_t e) {
+    if (p->d_tensors) (void)hipFree(p->d_tensors);
+    if (p->d_work) (void)hipFree(p->d_work);
+    if (p->d_ckpt) (void)hipFree(p->d_ckpt);
+    delete p;
+    return hip_fail(e, "mps_fp8_plan_create");
+  };
+  hipError_t e = hipGetDevice(&p->device);
+  if (e == hipSuccess && count > 0) e = hipMalloc(&p->d_tensors, sizeof(mps_fp8_tensor) * count);
+  if (e == hipSuccess && count > 0)
+    e = hipMemcpy(p->d_tensors, tensors, sizeof(mps_fp8_tensor) * count, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return cleanup(e);
+
+  // Row ranges. A plan whose buckets are few or uneven for the CUs (a layer,
+  // a single tensor) would leave CUs idle behind its largest buckets: buckets
+  // on the k = 1024 and fast paths larger than total / (2 * CUs) elements are
+  // split into row ranges of at most that size (and at least 64 elements per
+  // substream, 16 groups, so that a range's set-up stays small beside its
+  // decode). Each range starts from lane checkpoints (fp8_checkpoints).
+  int cus = 0;
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device);
+  if (e != hipSuccess) return cleanup(e);
+  int64_t total = 0;
+  for (int64_t x : elems) total += x;
+  const int64_t cap = std::max<int64_t>(total / (2 * (int64_t)std::max(cus, 1)), 65536);
+  std::vector<SplitJob> jobs;
+  std::vector<size_t> job_of(bucket.size(), SIZE_MAX);
+  int64_t ck_words = 0;
+  for (size_t i = 0; i < bucket.size(); ++i) {
+    const WorkItem &w = bucket[i];
+    if ((w.path != kPathK1024 && w.path != kPathFast) || elems[i] <= cap || w.rows < 2) continue;
+    const int32_t P = w.cl / w.k_eff;
+    const int32_t min_rows = std::max<int32_t>(1, (64 + P - 1) / P);
+    int64_t ranges = std::min<int64_t>((elems[i] + cap - 1) / cap, w.rows / min_rows);
+    if (ranges < 2) continue;
+    const int32_t range_rows = (int32_t)((w.rows + ranges - 1) / ranges);
+    ranges = (w.rows + range_rows - 1) / range_rows;
+    if (ranges < 2) continue;
+    SplitJob j{};
+    j.tensor = w.tensor;
+    j.K = w.k_eff;
+    j.P = P;
+    j.rows = w.rows;
+    j.c0 = w.c0;
+    j.range_rows = range_rows;
+    j.ranges = (int32_t)ranges;
+    j.bit_base = w.bit_base;
+    j.out = ck_words;
+    j.table_ids = w.table_ids;
+    j.startbits = w.startbits;
+    j.row_idx = w.row_idx;
+    job_of[i] = jobs.size();
+    jobs.push_back(j);
+    ck_words += (ranges - 1) * w.k_eff;
+  }
+  std::vector<uint32_t> failed(jobs.size(), 0u);
+  if (!jobs.empty()) {
+    SplitJob *d_jobs = nullptr;
+    uint32_t *d_failed = nullptr;
+    e = hipMalloc(&p->d_ckpt, sizeof(uint32_t) * (size_t)ck_words);
+    if (e == hipSuccess) e = hipMalloc(&d_jobs, sizeof(SplitJob) * jobs.size());
+    if (e == hipSuccess) e = hipMalloc(&d_failed, sizeof(uint32_t) * jobs.size());
+    if (e == hipSuccess) e = hipMemcpy(d_jobs, jobs.data(), sizeof(SplitJob) * jobs.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d_failed, failed.data(), sizeof(uint32_t) * jobs.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+      // the legacy default stream: ordered after the work that wrote the sidecars
+      hipLaunchKernelGGL(fp8_checkpoints, dim3((unsigned)jobs.size()), dim3(kBlock), 0, 0, p->d_tensors, d_jobs,
+                         p->d_ckpt, d_failed);
+      e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(failed.data(), d_failed, sizeof(uint32_t) * jobs.size(), hipMemcpyDeviceToHost);
+    if (d_jobs) (void)hipFree(d_jobs);
+    if (d_failed) (void)hipFree(d_failed);
+    if (e != hipSuccess) return cleanup(e);
+  }
+
+  // Work items (buckets and ranges), largest first: the persistent launch
+  // deals them round-robin to the CUs, which then finish at about the same
+  // time. An item's cost is its element count plus a fixed set-up share.
+  std::vector<WorkItem> work;
+  std::vector<int64_t> cost;
+  for (size_t i = 0; i < bucket.size(); ++i) {
+    const WorkItem &w = bucket[i];
+    if (job_of[i] == SIZE_MAX || failed[job_of[i]]) {
+      work.push_back(w);
+      cost.push_back(elems[i] + 65536);
+      continue;
+    }
+    const SplitJob &j = jobs[job_of[i]];
+    const uint32_t *ck = p->d_ckpt + j.out;
+    for (int32_t r = 0; r < j.ranges; ++r) {
+      WorkItem x = w;
+      x.rows = std::min(j.range_rows, w.rows - r * j.range_rows);
+      x.row_idx = w.row_idx + (int64_t)r * j.range_rows;
+      x.startbits = r == 0 ? w.startbits : ck + (int64_t)(r - 1) * j.K;
+      x.endbits = r + 1 == j.ranges ? w.endbits : ck + (int64_t)r * j.K;
+      work.push_back(x);
+      cost.push_back((int64_t)x.rows * w.cl + 65536);
+    }
+  }
   {
     std::vector<size_t> order(work.size());
     for (size_t j = 0; j < order.size(); ++j) order[j] = j;
@@ -1405,22 +1602,11 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
     for (size_t j = 0; j < order.size(); ++j) sorted[j] = work[order[j]];
     work.swap(sorted);
   }
-  auto *p = new mps_fp8_plan();
-  p->count = count;
   p->work_items = (int64_t)work.size();
-  hipError_t e = hipGetDevice(&p->device);
-  if (e == hipSuccess && count > 0) e = hipMalloc(&p->d_tensors, sizeof(mps_fp8_tensor) * count);
-  if (e == hipSuccess && !work.empty()) e = hipMalloc(&p->d_work, sizeof(WorkItem) * work.size());
-  if (e == hipSuccess && count > 0)
-    e = hipMemcpy(p->d_tensors, tensors, sizeof(mps_fp8_tensor) * count, hipMemcpyHostToDevice);
+  if (!work.empty()) e = hipMalloc(&p->d_work, sizeof(WorkItem) * work.size());
   if (e == hipSuccess && !work.empty())
     e = hipMemcpy(p->d_work, work.data(), sizeof(WorkItem) * work.size(), hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    if (p->d_tensors) (void)hipFree(p->d_tensors);
-    if (p->d_work) (void)hipFree(p->d_work);
-    delete p;
-    return hip_fail(e, "mps_fp8_plan_create");
-  }
+  if (e != hipSuccess) return cleanup(e);
   *plan_out = p;
   return MPS_OK;
 }
@@ -1452,6 +1638,7 @@ int mps_fp8_plan_destroy(mps_fp8_plan *plan) {
   if (!plan) return MPS_OK;
   if (plan->d_tensors) (void)hipFree(plan->d_tensors);
   if (plan->d_work) (void)hipFree(plan->d_work);
+  if (plan->d_ckpt) (void)hipFree(plan->d_ckpt);
   delete plan;
   return MPS_OK;
 }

@@ -96,10 +96,12 @@ class DecodePlan:
         return self.outputs
 
     def info(self) -> Dict[str, int]:
+        """Work items of a launch (buckets, or row ranges of buckets the plan split)
+        and bytes of LDS per workgroup."""
         wi, lds = ctypes.c_int64(0), ctypes.c_int64(0)
         if self._plan:
             _native.check(_native.lib().mps_fp8_plan_info(self._plan, ctypes.byref(wi), ctypes.byref(lds)))
-        return {"buckets": int(wi.value), "lds_bytes": int(lds.value)}
+        return {"work_items": int(wi.value), "lds_bytes": int(lds.value)}
 
     def close(self) -> None:
         if getattr(self, "_plan", None):

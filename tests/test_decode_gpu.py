@@ -243,3 +243,63 @@ def test_integrity_flags_on_corrupt_sidecar():
     MPServe_cuda.huffman_decode_fp8(*decode_args(to_torch(bad, DEV), q_t))
     assert _status() & 0x4
     assert int(guard.sum().item()) == 0 and out.shape == (n, m)
+
+
+def _plan_decode(items):
+    """Decode [(bf16 ref or None, fp8 u8 numpy, oracle sidecar)] in one plan; (outputs, plan info)."""
+    from mpserve_amd.decode import DecodePlan
+
+    dev_items = []
+    for _, q, sc in items:
+        q_t = torch.from_numpy(np.ascontiguousarray(q)).to(DEV)
+        dev_items.append((q_t, to_torch(sc, DEV), torch.zeros(q.shape, dtype=torch.bfloat16, device=DEV)))
+    plan = DecodePlan(dev_items)
+    plan.decode()
+    torch.cuda.synchronize()
+    return [o.view(torch.uint16).cpu().numpy() for _, _, o in dev_items], plan.info()
+
+
+@pytest.mark.parametrize("case", ["slab_p8", "slab_wrap_p14", "esc_k1024", "fast_k256", "mixed"])
+def test_plan_splits_buckets_into_row_ranges(case):
+    """A plan with few large buckets splits them into row ranges started from lane
+    checkpoints; every range decodes bit-exact and ends where the next begins."""
+    if case == "slab_p8":       # 2 buckets of 128 rows x 8192 columns (one scale key)
+        bf, q, sc = synth(256, 8192, seed=81)
+        items = [(bf, q, oracle.encode(bf, q, sc[:1].copy(), 7, 1024))]
+    elif case == "slab_wrap_p14":  # P = 14: groups straddle rows
+        bf, q, sc = synth(128, 14336, seed=82)
+        items = [(bf, q, oracle.encode(bf, q, sc[:1].copy(), 7, 1024))]
+    elif case == "esc_k1024":
+        bf, q, scales = _esc_inputs(48, 4096, 83)
+        side, stats = oracle.encode(bf, q, scales, 7, 1024, with_stats=True)
+        assert stats["esc_keys"] >= 1
+        items = [(bf, q, side)]
+    elif case == "fast_k256":   # k = 256 substreams, P = 8
+        bf, q, sc = synth(300, 2048, seed=84)
+        items = [(bf, q, oracle.encode(bf, q, sc[:1].copy(), 7, 256))]
+    else:                       # a split tensor next to whole buckets and a generic-path tensor
+        a = synth(256, 8192, seed=85)
+        b = synth(64, 4096, seed=86)
+        c = synth(40, 100, seed=87)
+        items = [(a[0], a[1], oracle.encode(a[0], a[1], a[2][:1].copy(), 7, 1024)),
+                 (b[0], b[1], oracle.encode(b[0], b[1], b[2], 7, 1024)),
+                 (c[0], c[1], oracle.encode(c[0], c[1], c[2], 7, 1024))]
+    buckets = sum(sc["bucket_table_i32"].shape[0] for _, _, sc in items)
+    _status()
+    outs, info = _plan_decode(items)
+    assert info["work_items"] > buckets
+    for (bf, _, _), got in zip(items, outs):
+        assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
+    assert _status() == 0
+
+
+def test_plan_split_with_bad_row_keeps_bucket_whole():
+    """A row index out of range in a bucket the plan would split: the checkpoint
+    walk stops, the bucket stays whole, and its decode reports the bad row."""
+    bf, q, sc = synth(256, 8192, seed=88)
+    side = oracle.encode(bf, q, sc[:1].copy(), 7, 1024)
+    bad = {k: v.copy() for k, v in side.items()}
+    bad["row_indices_i32"][130] = 10 ** 6
+    _status()
+    outs, info = _plan_decode([(None, q, bad)])
+    assert _status() & 0x2
