@@ -94,35 +94,48 @@ def data_note(workload: str) -> str:
 
 
 def time_per_tensor(entries, outs, stream, reps: int = 20):
-    """Each tensor decoded alone through the drop-in op (one launch per tensor, as
-    the reference decodes), timed with events around each launch on its stream."""
+    """Each tensor decoded alone, timed with events around each launch on its
+    stream: through the drop-in op (one launch per tensor over its buckets, as
+    the reference decodes), and through a plan of that tensor alone (which
+    splits large buckets into row ranges when they are few for the CUs)."""
     import torch
 
     import MPServe_cuda
-    from mpserve_amd.decode import sidecar_decode_args
+    from mpserve_amd.decode import DecodePlan, sidecar_decode_args
+
+    def timed(launch):
+        for _ in range(3):
+            launch()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for s, e in ev:
+            s.record(stream)
+            launch()
+            e.record(stream)
+        torch.cuda.synchronize()
+        return sum(s.elapsed_time(e) for s, e in ev) / reps
 
     rows = []
     for (name, fp8, sc, src), o in zip(entries, outs):
         n, m = int(fp8.shape[0]), int(fp8.shape[1])
         call = sidecar_decode_args(fp8, sc)
-        for _ in range(3):
-            MPServe_cuda.huffman_decode_fp8(*call, out=o)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for s, e in ev:
-            s.record(stream)
-            MPServe_cuda.huffman_decode_fp8(*call, out=o)
-            e.record(stream)
-        torch.cuda.synchronize()
-        if not torch.equal(o.view(torch.uint16), src.view(torch.uint16)):
-            raise RuntimeError(f"per-tensor decode of {name} is not bit-exact")
-        ms = sum(s.elapsed_time(e) for s, e in ev) / reps
         alg = algorithmic_bytes(n, m, sc)
-        rows.append({"tensor": name, "shape": [n, m], "ms": round(ms, 4),
-                     "out_gbs": round(2 * n * m / ms / 1e6, 1), "rw_gbs": round(alg / ms / 1e6, 1),
-                     "pct_hbm_peak_rw": round(100.0 * alg / ms / 1e6 / HBM_PEAK_GBS, 2),
-                     "buckets": int(sc["bucket_table_i32"].shape[0]),
-                     "esc_tables": int(((sc["decode_lens_u8"] & 0x88) != 0).any(dim=1).sum().item())})
-        log(f"{name} {n}x{m}: {ms:.4f} ms, {rows[-1]['rw_gbs']} GB/s R+W ({rows[-1]['pct_hbm_peak_rw']}%)")
+        row = {"tensor": name, "shape": [n, m], "buckets": int(sc["bucket_table_i32"].shape[0]),
+               "esc_tables": int(((sc["decode_lens_u8"] & 0x88) != 0).any(dim=1).sum().item())}
+        plan = DecodePlan([(fp8, sc, o)])
+        row["plan_work_items"] = plan.info()["work_items"]
+        for key, launch in (("op", lambda: MPServe_cuda.huffman_decode_fp8(*call, out=o)),
+                            ("plan", lambda: plan.decode(stream))):
+            o.zero_()
+            ms = timed(launch)
+            if not torch.equal(o.view(torch.uint16), src.view(torch.uint16)):
+                raise RuntimeError(f"per-tensor decode ({key}) of {name} is not bit-exact")
+            row[f"{key}_ms"] = round(ms, 4)
+            row[f"{key}_rw_gbs"] = round(alg / ms / 1e6, 1)
+            row[f"{key}_pct_hbm_peak_rw"] = round(100.0 * alg / ms / 1e6 / HBM_PEAK_GBS, 2)
+        plan.close()
+        rows.append(row)
+        log(f"{name} {n}x{m}: op {row['op_ms']:.4f} ms ({row['op_pct_hbm_peak_rw']}%), plan of "
+            f"{row['plan_work_items']} items {row['plan_ms']:.4f} ms ({row['plan_pct_hbm_peak_rw']}%)")
     return rows
 
 
