@@ -121,6 +121,75 @@ typedef struct mps_fp8_encode_in {
  * device memory owned by the returned handle. */
 typedef struct mps_fp8_sidecar mps_fp8_sidecar;
 int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **out);
+/* One AWQ int4 tensor and its sidecar, all device pointers, in either layout
+ * of the reference's AWQ int4 builders (dtype views as for the FP8 tensor). */
+typedef struct mps_awq_tensor {
+  const uint8_t *int4;                   /* [n*m] int4 values, one per byte (low nibble) */
+  const uint64_t *bitstream;             /* [bitstream_words] */
+  int64_t bitstream_words;
+  const uint16_t *decode_syms;           /* [num_tables,2048] */
+  const uint8_t *decode_lens;            /* [num_tables,1024] packed 4-bit, 15 = ESC */
+  int64_t num_tables;
+  const int32_t *bucket_table;           /* [num_buckets,16] int4 value -> table id or -1 */
+  const int32_t *bucket_col_start;       /* row layout: [num_buckets]; by-scale layout: NULL */
+  const int32_t *bucket_col_len;         /* row layout: [num_buckets]; by-scale layout: NULL */
+  const int32_t *bucket_row_offsets;     /* [num_buckets+1] bucket_row_offsets / bucket_group_offsets */
+  const int32_t *row_indices;            /* [num_row_indices] row_indices / group_rows */
+  int64_t num_row_indices;
+  const int32_t *group_col_start;        /* by-scale layout: [num_row_indices]; row layout: NULL */
+  int64_t group_size;                    /* by-scale layout: columns per group */
+  const uint32_t *bucket_thread_startbit;/* [num_buckets, k+1] */
+  const int64_t *bucket_bit_base;        /* [num_buckets+1] */
+  int64_t num_buckets;
+  int64_t k;                             /* 1..1024 */
+  int64_t n, m;                          /* output shape [n, m], n*m < 2^32 - 1 */
+  uint16_t *out;                         /* [n*m] BF16 bit patterns (device) */
+} mps_awq_tensor;
+
+/* Decode one AWQ int4 tensor: out[n,m] = BF16 rebuilt from int4 values + sidecar,
+ * on `stream`. Replaces huffman_cpp::huffman_decode_awq_int4_bucket_entry
+ * (group_col_start == NULL; reference kernel/decode_huffman.cu:877-1018 and
+ * :378-475, bound at kernel/wrapper.cpp:342-386) and
+ * ..._by_scale_entry (group_col_start != NULL; kernel/decode_huffman.cu:760-875
+ * and :477-589, bound at kernel/wrapper.cpp:388-416). The shape/dtype checks
+ * of those entries are done by the caller. max_len must be 11. Columns of a
+ * row bucket are walked as e % col_len, as the builder lays them out.
+ * Asynchronous: returns after the launch. */
+int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream);
+
+/* Inputs of the AWQ int4 sidecar builders, all device pointers: BF16 bit
+ * patterns and int4 values (one per byte, low nibble) of an [n, m] weight, and
+ * the u16 (BF16 bit) scales: one value, [n] (scale_ndim 1) or block-wise
+ * [n/bs0, m/bs1] (scale_ndim 2). by_scale = 0 builds row buckets, 1 builds
+ * buckets of quantisation groups of one exact scale (at most group_cap each). */
+typedef struct mps_awq_encode_in {
+  const uint16_t *bf16;
+  const uint8_t *int4;
+  const uint16_t *scales;
+  int64_t n, m;
+  int32_t scale_ndim;
+  int32_t by_scale;
+  int64_t scale_dims[2];
+  int64_t scale_numel;
+  int64_t max_len;           /* 1..15 (decoding needs 11) */
+  int64_t threads_per_block; /* k: substreams per bucket, 1..1024 */
+  int64_t group_cap;         /* by_scale: groups per bucket, > 0 */
+} mps_awq_encode_in;
+
+/* Build the AWQ int4 sidecar of one weight on the GPU, byte-identical to the
+ * reference builders, which run single-threaded on the host:
+ *   by_scale = 0: huffman_cpp::huffman_build_awq_int4_bucket_decode_tables_entry
+ *     (reference kernel/build_huffman.cu:1583-2126, bound as
+ *     MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables at kernel/wrapper.cpp:275-306);
+ *   by_scale = 1: ..._by_scale_entry (kernel/build_huffman.cu:1075-1580, bound as
+ *     MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables_by_scale at kernel/wrapper.cpp:308-340).
+ * Same argument checks and messages. The result uses the FP8 handle's 17
+ * slots: slots 0-13 in the reference's order of the row-bucket dict (slot 3 is
+ * table_qv_u16, slot 7 bucket_table_i32 [B,16]); by scale, slot 5 holds
+ * bucket_group_offsets_i32, slot 6 group_rows_i32, slot 8 group_col_start_i32
+ * and slot 13 shape_nmkg_i64 (slot 9 is empty). Slots 14-16 are empty. */
+int mps_awq_encode(const mps_awq_encode_in *in, void *stream, mps_fp8_sidecar **out);
+
 /* Element counts of the 17 outputs, in the reference's order (kernel/wrapper.cpp:429-446):
  * decode_syms_u16, decode_lens_u8, table_scale_u16, table_fp8_u16, bucket_scale_u16,
  * bucket_row_offsets_i32, row_indices_i32, bucket_table_i32, bucket_col_start_i32,

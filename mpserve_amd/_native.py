@@ -51,6 +51,31 @@ class MpsFp8EncodeIn(ctypes.Structure):
     ]
 
 
+class MpsAwqTensor(ctypes.Structure):
+    """mps_awq_tensor: one AWQ int4 tensor + sidecar (row or by-scale layout), device pointers."""
+
+    _fields_ = [
+        ("int4", _p), ("bitstream", _p), ("bitstream_words", _i64),
+        ("decode_syms", _p), ("decode_lens", _p), ("num_tables", _i64),
+        ("bucket_table", _p), ("bucket_col_start", _p), ("bucket_col_len", _p),
+        ("bucket_row_offsets", _p), ("row_indices", _p), ("num_row_indices", _i64),
+        ("group_col_start", _p), ("group_size", _i64),
+        ("bucket_thread_startbit", _p), ("bucket_bit_base", _p), ("num_buckets", _i64),
+        ("k", _i64), ("n", _i64), ("m", _i64), ("out", _p),
+    ]
+
+
+class MpsAwqEncodeIn(ctypes.Structure):
+    """mps_awq_encode_in: device inputs of the AWQ int4 sidecar builders."""
+
+    _fields_ = [
+        ("bf16", _p), ("int4", _p), ("scales", _p), ("n", _i64), ("m", _i64),
+        ("scale_ndim", ctypes.c_int32), ("by_scale", ctypes.c_int32),
+        ("scale_dims", _i64 * 2), ("scale_numel", _i64),
+        ("max_len", _i64), ("threads_per_block", _i64), ("group_cap", _i64),
+    ]
+
+
 _lib = None
 
 
@@ -78,8 +103,11 @@ def lib():
         L.mps_fp8_sidecar_copy.argtypes = [_p, ctypes.POINTER(_p), _p]
         L.mps_fp8_sidecar_free.argtypes = [_p]
         L.mps_fp8_sidecar_stats.argtypes = [_p, ctypes.POINTER(_i64)]
+    L.mps_awq_decode.argtypes = [ctypes.POINTER(MpsAwqTensor), _i64, _p]
+    L.mps_awq_encode.argtypes = [ctypes.POINTER(MpsAwqEncodeIn), _p, ctypes.POINTER(_p)]
     for name in ("mps_clock_rate_khz", "mps_fp8_decode", "mps_fp8_plan_create", "mps_fp8_plan_decode",
-                 "mps_fp8_plan_info", "mps_fp8_plan_destroy", "mps_fp8_read_status"):
+                 "mps_fp8_plan_info", "mps_fp8_plan_destroy", "mps_fp8_read_status", "mps_awq_decode",
+                 "mps_awq_encode"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

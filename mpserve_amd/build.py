@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmpserve_amd.so")
 ARCH = os.environ.get("MPS_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["fp8_decode.hip", "fp8_encode.hip"]
+SOURCES = ["fp8_decode.hip", "fp8_encode.hip", "awq_decode.hip"]
 
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",

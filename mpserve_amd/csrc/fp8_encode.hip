@@ -90,9 +90,9 @@ __device__ bool global_insert(uint64_t *keys, uint32_t *counts, uint64_t cap_mas
 }
 
 __global__ __launch_bounds__(kHistBlock) void hist_kernel(const uint16_t *__restrict__ bf16, const uint8_t *__restrict__ fp8,
-                                                          int64_t n, int64_t m, ScaleMap S, int64_t elems_per_block,
-                                                          uint64_t *keys, uint32_t *counts, uint64_t cap_mask,
-                                                          uint32_t *overflow) {
+                                                          int64_t n, int64_t m, ScaleMap S, uint32_t qmask,
+                                                          int64_t elems_per_block, uint64_t *keys, uint32_t *counts,
+                                                          uint64_t cap_mask, uint32_t *overflow) {
   __shared__ unsigned long long s_keys[kLdsSlots];
   __shared__ uint32_t s_cnt[kLdsSlots];
   for (int i = threadIdx.x; i < kLdsSlots; i += kHistBlock) {
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kHistBlock) void hist_kernel(const uint16_t *__rest
   const int64_t e1 = e0 + elems_per_block < numel ? e0 + elems_per_block : numel;
   for (int64_t e = e0 + threadIdx.x; e < e1; e += kHistBlock) {
     const int64_t row = e / m, col = e - row * m;
-    const uint64_t k = key40(sidx_of(S, row, col), fp8[e], bf16[e]);
+    const uint64_t k = key40(sidx_of(S, row, col), fp8[e] & qmask, bf16[e]);
     // LDS first: a short probe, then the global table.
     uint32_t h = (uint32_t)(hash64(k) & (kLdsSlots - 1));
     bool done = false;
@@ -308,6 +308,17 @@ __device__ void package_merge_lengths(const int32_t *w, int n, int L, int32_t *A
   }
 }
 
+// ESC rules of the three builders:
+//  kEscFp8        build_huffman.cu:485-535 and :205-228: esc_sym = smallest u16 not kept, list re-sorted
+//                 (count asc, sym asc), the ESC entries' nibble is len | 8.
+//  kEscAwqBucket  build_huffman.cu:1775-1836: as kEscFp8 (ESC weight at least 1), but the ESC code
+//                 has length L and its one LUT entry has nibble 15.
+//  kEscAwqByScale build_huffman.cu:1251-1316: esc_sym = smallest u16 absent from all of the key's
+//                 symbols (0xFFFF if none is); the list stays (count desc, sym asc) with ESC last, and
+//                 the lengths package-merge returns for the sorted weights apply to it by position;
+//                 ESC length L, nibble 15.
+enum : int { kEscFp8 = 0, kEscAwqBucket = 1, kEscAwqByScale = 2 };
+
 struct CodebookArgs {
   const uint32_t *gid_tkey;
   const uint32_t *toff;
@@ -325,6 +336,7 @@ struct CodebookArgs {
   uint16_t *table_fp8;
   uint32_t G;
   int L;
+  int esc_mode;  // kEscFp8, kEscAwqBucket or kEscAwqByScale
   uint32_t *err;
   uint32_t *esc_stats;  // [0] keys with ESC, [1] collisions (elements)
 };
@@ -376,6 +388,7 @@ __global__ void codebook_kernel(CodebookArgs a) {
   int32_t *Bv = A + 4 * nmax;
   uint8_t *Al = reinterpret_cast<uint8_t *>(Bv + 4 * nmax);
   uint8_t *Bl = Al + 4 * nmax;
+  int32_t *sw = reinterpret_cast<int32_t *>(Bl + 4 * nmax);  // sorted weights (kEscAwqByScale)
   uint32_t nl = 0;
   bool use_esc = false;
   uint32_t esc_sym = 0;
@@ -413,6 +426,24 @@ __global__ void codebook_kernel(CodebookArgs a) {
     uint32_t kept_sum = 0;
     for (uint32_t t = 0; t < nl; ++t) kept_sum += (uint32_t)lw[t];
     const uint32_t esc_w = total - kept_sum;
+    if (a.esc_mode == kEscAwqByScale) {
+      // Smallest u16 absent from all ni (distinct) symbols: the largest c with
+      // #{sym < c} == c, found by bisection over c in [0, 65536].
+      uint32_t lo = 0, hi = 65536;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        uint32_t below = 0;
+        for (uint32_t t = 0; t < ni; ++t) below += sym[t] < mid;
+        if (below == mid) lo = mid;
+        else hi = mid - 1;
+      }
+      esc_sym = lo > 0xFFFFu ? 0xFFFFu : lo;
+      lw[nl] = (int32_t)esc_w;  // last; the list keeps its (count desc, sym asc) order
+      ls[nl] = (int32_t)esc_sym;
+      ++nl;
+      atomicAdd(&a.esc_stats[0], 1u);
+      goto lengths;
+    }
     // smallest u16 not among the kept: sort kept syms (insertion, <= 2^15 items)
     for (uint32_t p = 1; p < nl; ++p) {
       const int32_t v = ls[p], vw = lw[p];
@@ -431,7 +462,7 @@ __global__ void codebook_kernel(CodebookArgs a) {
       else if ((uint32_t)ls[p] > cand) break;
     }
     esc_sym = cand & 0xFFFF;
-    lw[nl] = (int32_t)esc_w;
+    lw[nl] = (a.esc_mode == kEscAwqBucket && (int32_t)esc_w <= 0) ? 1 : (int32_t)esc_w;
     ls[nl] = (int32_t)esc_sym;
     ++nl;
     // back to (count asc, sym asc)
@@ -454,8 +485,24 @@ __global__ void codebook_kernel(CodebookArgs a) {
     }
     nl = ni;
   }
-  // weights are ascending (as int); package-merge expects that order
-  package_merge_lengths(lw, (int)nl, L, A, Bv, Al, Bl, lens);
+lengths:
+  if (a.esc_mode == kEscAwqByScale && use_esc) {
+    // package-merge sorts the weights and returns lengths by sorted position;
+    // the reference applies them to its (unsorted) list position by position
+    for (uint32_t t = 0; t < nl; ++t) {
+      const int32_t v = lw[t];
+      int64_t q = (int64_t)t - 1;
+      while (q >= 0 && sw[q] > v) {
+        sw[q + 1] = sw[q];
+        --q;
+      }
+      sw[q + 1] = v;
+    }
+    package_merge_lengths(sw, (int)nl, L, A, Bv, Al, Bl, lens);
+  } else {
+    // weights are ascending (as int); package-merge expects that order
+    package_merge_lengths(lw, (int)nl, L, A, Bv, Al, Bl, lens);
+  }
   // canonical codes (build_huffman.cu:171-203), handed out in list order
   uint32_t bl_count[16], next_code[16];
   for (int b = 0; b < 16; ++b) bl_count[b] = 0;
@@ -464,6 +511,7 @@ __global__ void codebook_kernel(CodebookArgs a) {
       atomicOr(a.err, 2u);
       return;
     }
+    if (use_esc && a.esc_mode != kEscFp8 && (uint32_t)ls[t] == esc_sym) lens[t] = L;  // AWQ: ESC code has length L
     bl_count[lens[t]]++;
   }
   uint32_t code = 0;
@@ -481,7 +529,7 @@ __global__ void codebook_kernel(CodebookArgs a) {
     const uint32_t fill = 1u << (L - len);
     const uint32_t base = c << (L - len);
     const bool is_esc = use_esc && (uint32_t)ls[t] == esc_sym;
-    const uint32_t nib = is_esc ? ((uint32_t)len | 0x8u) : (uint32_t)len;
+    const uint32_t nib = is_esc ? (a.esc_mode == kEscFp8 ? ((uint32_t)len | 0x8u) : 15u) : (uint32_t)len;
     for (uint32_t f = 0; f < fill; ++f) {
       const uint32_t e = base + f;
       dsyms[e] = (uint16_t)ls[t];
@@ -524,7 +572,7 @@ __global__ void codebook_kernel(CodebookArgs a) {
   }
 }
 
-constexpr uint32_t kWsPerItem = 13;  // 3 list arrays + 2 x 4 merge ints + 2 x 4 merge bytes
+constexpr uint32_t kWsPerItem = 14;  // 3 list arrays + 2 x 4 merge ints + 2 x 4 merge bytes + sorted weights
 
 __global__ void ws_size_kernel(const uint32_t *gid_tkey, const uint32_t *tcount, uint32_t G, uint32_t T,
                                uint32_t *sz) {
@@ -537,11 +585,16 @@ __global__ void ws_size_kernel(const uint32_t *gid_tkey, const uint32_t *tcount,
 // ---------------------------------------------------------------------------
 // 4. bucket_table, U / unique gids / fp8 -> uidx (one work-item per bucket)
 // ---------------------------------------------------------------------------
-__global__ void bucket_table_kernel(const uint16_t *bucket_sidx, uint32_t B, const uint32_t *tcount,
+// qvals = 256 (FP8 bytes; also U/uniq/uidx) or 16 (AWQ int4 values, build_huffman.cu:1973-1982).
+__global__ void bucket_table_kernel(const uint16_t *bucket_sidx, uint32_t B, int qvals, const uint32_t *tcount,
                                     const uint32_t *tgid, int32_t *btab, int32_t *bU, int32_t *uniq, int16_t *uidx) {
   const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const uint64_t t0 = (uint64_t)bucket_sidx[b] * 256;
+  if (qvals != 256) {
+    for (int c = 0; c < qvals; ++c) btab[b * qvals + c] = tcount[t0 + c] ? (int32_t)tgid[t0 + c] : -1;
+    return;
+  }
   int32_t U = 0;
   for (int c = 0; c < 256; ++c) {
     const int32_t gid = tcount[t0 + c] ? (int32_t)tgid[t0 + c] : -1;
@@ -572,6 +625,8 @@ struct LaneArgs {
   const int32_t *row_indices;
   const int32_t *col_start;
   const int32_t *col_len;
+  const int32_t *row_col;     // per-row column start (groups of the by-scale layout) or null
+  uint32_t qmask;
   const uint32_t *lane_base;  // [B+1] cumulative k_eff
   uint32_t B;
   int64_t k;
@@ -599,16 +654,16 @@ __global__ void lane_bits_kernel(LaneArgs a) {
   const uint32_t b = find_bucket(a.lane_base, a.B, g);
   const uint32_t t = g - a.lane_base[b];
   const int32_t ra = a.row_offsets[b], rows = a.row_offsets[b + 1] - ra;
-  const int32_t c0 = a.col_start[b], cl = a.col_len[b];
+  const int32_t c0 = a.row_col ? 0 : a.col_start[b], cl = a.col_len[b];
   const int64_t total = (int64_t)rows * cl;
   const int64_t k_eff = a.lane_base[b + 1] - a.lane_base[b];
   uint64_t bits = 0;
   for (int64_t e = t; e < total; e += k_eff) {
     const int64_t rr = e / cl, cc = e - rr * cl;
     const int64_t row = a.row_indices[ra + rr];
-    const int64_t col = c0 + cc;
+    const int64_t col = (a.row_col ? a.row_col[ra + rr] : c0) + cc;
     const int64_t idx = row * a.m + col;
-    const uint64_t k = key40(sidx_of(a.S, row, col), a.fp8[idx], a.bf16[idx]);
+    const uint64_t k = key40(sidx_of(a.S, row, col), a.fp8[idx] & a.qmask, a.bf16[idx]);
     uint64_t h = hash64(k) & a.cap_mask;
     while (a.keys[h] != k) {
       if (a.keys[h] == kEmpty) {
@@ -648,6 +703,7 @@ struct PackArgs {
   const int32_t *row_indices;
   const int32_t *col_start;
   const int32_t *col_len;
+  const int32_t *row_col;  // as LaneArgs::row_col
   const uint32_t *lane_base;
   uint32_t B;
   int64_t k;
@@ -670,7 +726,7 @@ __global__ void pack_kernel(PackArgs a) {
   const uint32_t b = find_bucket(a.lane_base, a.B, g);
   const uint32_t t = g - a.lane_base[b];
   const int32_t ra = a.row_offsets[b], rows = a.row_offsets[b + 1] - ra;
-  const int32_t c0 = a.col_start[b], cl = a.col_len[b];
+  const int32_t c0 = a.row_col ? 0 : a.col_start[b], cl = a.col_len[b];
   const int64_t total = (int64_t)rows * cl;
   const int64_t k_eff = a.lane_base[b + 1] - a.lane_base[b];
   const uint32_t *sb = a.startbit + (uint64_t)b * (a.k + 1);
@@ -699,7 +755,7 @@ __global__ void pack_kernel(PackArgs a) {
   };
   for (int64_t e = t; e < total; e += k_eff) {
     const int64_t rr = e / cl, cc = e - rr * cl;
-    const int64_t idx = (int64_t)a.row_indices[ra + rr] * a.m + c0 + cc;
+    const int64_t idx = (int64_t)a.row_indices[ra + rr] * a.m + (a.row_col ? a.row_col[ra + rr] : c0) + cc;
     const uint32_t cw = a.cw_elem[idx];
     put(cw & 0xFFFF, cw_len(cw));
     if (cw & kRaw) put(a.bf16[idx], 16);
@@ -773,54 +829,29 @@ struct mps_fp8_sidecar {
   int64_t stats[4] = {};  // esc keys, esc collision elements, distinct (key, symbol) pairs, hash capacity
 };
 
-extern "C" {
+namespace mps {
+namespace {
 
-int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **out) {
-  last_error().clear();
-  if (!in || !out) return fail(MPS_ERR_INVALID_ARGUMENT, "inputs must be defined");
-  *out = nullptr;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t L = in->max_len, kth = in->threads_per_block;
-  if (L <= 0 || L > 15) return fail(MPS_ERR_INVALID_ARGUMENT, "max_len must be in [1, 15]");
-  if (kth <= 0 || kth > 1024) return fail(MPS_ERR_INVALID_ARGUMENT, "threads_per_block must be in [1, 1024]");
-  const int64_t numel = in->numel;
-  if (in->ndim < 0 || in->ndim > 8 || in->scale_ndim < 0 || in->scale_ndim > 8)
-    return fail(MPS_ERR_INVALID_ARGUMENT, "too many dimensions");
-  // scale modes (build_huffman.cu:325-366)
-  const int64_t scale_numel = in->scale_numel;
-  const bool scale_scalar = scale_numel == 1;
-  const bool scale_per_elem = scale_numel == numel;
-  bool scale_per_row = false, scale_block2d = false;
-  int64_t n_rows = -1, n_cols = -1, sb0 = -1, sb1 = -1, nb0 = -1, nb1 = -1;
-  if (!scale_scalar && !scale_per_elem && in->ndim == 2) {
-    n_rows = in->dims[0];
-    n_cols = in->dims[1];
-    scale_per_row = scale_numel == n_rows;
-    if (!scale_per_row && in->scale_ndim == 2) {
-      nb0 = in->scale_dims[0];
-      nb1 = in->scale_dims[1];
-      if (nb0 > 0 && nb1 > 0 && n_rows % nb0 == 0 && n_cols % nb1 == 0) {
-        sb0 = n_rows / nb0;
-        sb1 = n_cols / nb1;
-        if (sb0 > 0 && sb1 > 0) scale_block2d = true;
-      }
-    }
-  }
-  if (!scale_scalar && !scale_per_elem && !scale_per_row && !scale_block2d)
-    return fail(MPS_ERR_INVALID_ARGUMENT,
-                "unsupported scales shape: use scalar, per-row (n,), per-element (numel), or 2D block-wise "
-                "[n/bs0,m/bs1]");
-  // The reference builds the tables before it checks the bucket layout; the
-  // checks below raise the same errors without the wasted work.
-  if (in->ndim != 2) return fail(MPS_ERR_INVALID_ARGUMENT, "bucket packing requires bf16_params to be 2D [n,m]");
-  const int64_t n = in->dims[0], m = in->dims[1];
-  if (n <= 0 || m <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "bf16_params shape must be non-empty");
-  if (!scale_block2d && !(scale_scalar || (!scale_per_elem && scale_per_row)))
-    return fail(MPS_ERR_INVALID_ARGUMENT,
-                "bucket packing requires scales to be scalar, per-row (n,), or 2D block-wise");
-  if (numel != n * m) return fail(MPS_ERR_INVALID_ARGUMENT, "bf16_params and fp8_params must have same numel");
-  if (numel >= (int64_t)1 << 32) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor too large for the GPU builder");
+enum : int { kFmtFp8 = kEscFp8, kFmtAwqBucket = kEscAwqBucket, kFmtAwqByScale = kEscAwqByScale };
 
+// One builder run, after the entry point's own argument checks.
+struct EncodeSpec {
+  const uint16_t *bf16;
+  const uint8_t *q;  // FP8 bytes, or AWQ int4 values (low nibble)
+  const uint16_t *scales;
+  int64_t n, m, scale_numel;
+  bool scalar, per_row, block2d;
+  int64_t nb0, nb1, sb0, sb1;
+  int64_t L, k, group_cap;
+  int format;
+};
+
+int encode_impl(const EncodeSpec &sp, hipStream_t s, mps_fp8_sidecar **out) {
+  const int64_t n = sp.n, m = sp.m, numel = n * m, L = sp.L, kth = sp.k, scale_numel = sp.scale_numel;
+  const bool scale_scalar = sp.scalar, scale_block2d = sp.block2d;
+  const int64_t nb0 = sp.nb0, nb1 = sp.nb1, sb0 = sp.sb0, sb1 = sp.sb1;
+  const uint32_t qmask = sp.format == kFmtFp8 ? 0xFFu : 0x0Fu;
+  const int qvals = sp.format == kFmtFp8 ? 256 : 16;
   hipError_t e;
 #define HC(x)                                                   \
   do {                                                          \
@@ -829,7 +860,7 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
 
   // --- scales to host, dense scale index (sorted unique values) ---
   std::vector<uint16_t> hsc((size_t)scale_numel);
-  HC(hipMemcpyAsync(hsc.data(), in->scales, sizeof(uint16_t) * scale_numel, hipMemcpyDeviceToHost, s));
+  HC(hipMemcpyAsync(hsc.data(), sp.scales, sizeof(uint16_t) * scale_numel, hipMemcpyDeviceToHost, s));
   HC(hipStreamSynchronize(s));
   std::vector<uint16_t> uniq_sc(hsc);
   std::sort(uniq_sc.begin(), uniq_sc.end());
@@ -843,7 +874,47 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   std::vector<int32_t> row_indices, row_offsets{0}, col_start, col_len;
   std::vector<uint16_t> bucket_scale;
   std::vector<uint16_t> row_sidx, block_sidx;
-  if (!scale_block2d) {
+  std::vector<int32_t> group_col;  // by scale: column start of each group
+  const bool by_scale = sp.format == kFmtAwqByScale;
+  if (by_scale) {
+    // quantisation groups (row, column start) bucketed by exact scale, scales
+    // ascending, groups in (row, column) order, <= group_cap a bucket
+    // (build_huffman.cu:1350-1385)
+    const int64_t gsz = scale_block2d ? sb1 : m;
+    const int64_t gpr = scale_block2d ? nb1 : 1;
+    if (!scale_block2d) {
+      row_sidx.resize((size_t)n);
+      for (int64_t r = 0; r < n; ++r) row_sidx[(size_t)r] = sidx_of_value(scale_scalar ? hsc[0] : hsc[(size_t)r]);
+    } else {
+      block_sidx.resize((size_t)(nb0 * nb1));
+      for (int64_t i = 0; i < nb0 * nb1; ++i) block_sidx[(size_t)i] = sidx_of_value(hsc[(size_t)i]);
+    }
+    std::vector<uint64_t> gk((size_t)(n * gpr));
+    for (int64_t r = 0; r < n; ++r)
+      for (int64_t bc = 0; bc < gpr; ++bc) {
+        const uint16_t v = scale_scalar ? hsc[0] : !scale_block2d ? hsc[(size_t)r] : hsc[(size_t)((r / sb0) * nb1 + bc)];
+        gk[(size_t)(r * gpr + bc)] = ((uint64_t)v << 40) | (uint64_t)(r * gpr + bc);
+      }
+    std::sort(gk.begin(), gk.end());
+    size_t i = 0;
+    while (i < gk.size()) {
+      size_t j = i;
+      while (j < gk.size() && (gk[j] >> 40) == (gk[i] >> 40)) ++j;
+      for (size_t off = i; off < j; off += (size_t)sp.group_cap) {
+        const size_t take = std::min<size_t>((size_t)sp.group_cap, j - off);
+        for (size_t q = 0; q < take; ++q) {
+          const int64_t gi = (int64_t)(gk[off + q] & 0xFFFFFFFFFFull);
+          row_indices.push_back((int32_t)(gi / gpr));
+          group_col.push_back((int32_t)((gi % gpr) * gsz));
+        }
+        bucket_scale.push_back((uint16_t)(gk[i] >> 40));
+        col_start.push_back(0);
+        col_len.push_back((int32_t)gsz);
+        row_offsets.push_back((int32_t)row_indices.size());
+      }
+      i = j;
+    }
+  } else if (!scale_block2d) {
     row_sidx.resize((size_t)n);
     std::vector<std::pair<uint16_t, int32_t>> order((size_t)n);
     for (int64_t r = 0; r < n; ++r) {
@@ -915,13 +986,18 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   HC(sc->bucket_scale.alloc(B));
   HC(sc->bucket_row_offsets.alloc(B + 1));
   HC(sc->row_indices.alloc(row_indices.size()));
-  HC(sc->bucket_col_start.alloc(B));
+  HC(sc->bucket_col_start.alloc(by_scale ? group_col.size() : (size_t)B));
   HC(sc->bucket_col_len.alloc(B));
   HC(hipMemcpyAsync(sc->bucket_scale.p, bucket_scale.data(), 2 * (size_t)B, hipMemcpyHostToDevice, s));
   HC(hipMemcpyAsync(sc->bucket_row_offsets.p, row_offsets.data(), 4 * (size_t)(B + 1), hipMemcpyHostToDevice, s));
   if (!row_indices.empty())
     HC(hipMemcpyAsync(sc->row_indices.p, row_indices.data(), 4 * row_indices.size(), hipMemcpyHostToDevice, s));
-  HC(hipMemcpyAsync(sc->bucket_col_start.p, col_start.data(), 4 * (size_t)B, hipMemcpyHostToDevice, s));
+  if (by_scale) {
+    if (!group_col.empty())
+      HC(hipMemcpyAsync(sc->bucket_col_start.p, group_col.data(), 4 * group_col.size(), hipMemcpyHostToDevice, s));
+  } else {
+    HC(hipMemcpyAsync(sc->bucket_col_start.p, col_start.data(), 4 * (size_t)B, hipMemcpyHostToDevice, s));
+  }
   HC(hipMemcpyAsync(sc->bucket_col_len.p, col_len.data(), 4 * (size_t)B, hipMemcpyHostToDevice, s));
 
   ScaleMap smap;
@@ -947,8 +1023,8 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
     HC(hipMemsetAsync(keys.p, 0xFF, sizeof(uint64_t) * cap, s));
     HC(hipMemsetAsync(counts.p, 0, sizeof(uint32_t) * cap, s));
     HC(hipMemsetAsync(flags.p, 0, sizeof(uint32_t) * 8, s));
-    hipLaunchKernelGGL(hist_kernel, dim3(hist_blocks), dim3(kHistBlock), 0, s, in->bf16, in->fp8, n, m, smap,
-                       per_block, keys.p, counts.p, cap - 1, flags.p);
+    hipLaunchKernelGGL(hist_kernel, dim3(hist_blocks), dim3(kHistBlock), 0, s, sp.bf16, sp.q, n, m, smap,
+                       qmask, per_block, keys.p, counts.p, cap - 1, flags.p);
     HC(hipGetLastError());
     HC(hipMemcpyAsync(hflags, flags.p, sizeof(hflags), hipMemcpyDeviceToHost, s));
     HC(hipStreamSynchronize(s));
@@ -1039,18 +1115,20 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   cba.table_fp8 = sc->table_fp8.p;
   cba.G = G;
   cba.L = (int)L;
+  cba.esc_mode = sp.format;
   cba.err = flags.p + 1;
   cba.esc_stats = flags.p + 2;
   if (G) hipLaunchKernelGGL(codebook_kernel, dim3((G + 63) / 64), dim3(64), 0, s, cba);
   HC(hipGetLastError());
 
   // --- 4. bucket tables ---
-  HC(sc->bucket_table.alloc((size_t)B * 256));
-  HC(sc->bucket_U.alloc(B));
-  HC(sc->bucket_unique_gid.alloc((size_t)B * 256));
-  HC(sc->bucket_fp8_uidx.alloc((size_t)B * 256));
+  const bool fp8 = sp.format == kFmtFp8;
+  HC(sc->bucket_table.alloc((size_t)B * qvals));
+  HC(sc->bucket_U.alloc(fp8 ? B : 0));
+  HC(sc->bucket_unique_gid.alloc(fp8 ? (size_t)B * 256 : 0));
+  HC(sc->bucket_fp8_uidx.alloc(fp8 ? (size_t)B * 256 : 0));
   if (B)
-    hipLaunchKernelGGL(bucket_table_kernel, dim3((B + 63) / 64), dim3(64), 0, s, d_bucket_sidx.p, B, tcount.p,
+    hipLaunchKernelGGL(bucket_table_kernel, dim3((B + 63) / 64), dim3(64), 0, s, d_bucket_sidx.p, B, qvals, tcount.p,
                        tgid.p, sc->bucket_table.p, sc->bucket_U.p, sc->bucket_unique_gid.p, sc->bucket_fp8_uidx.p);
   HC(hipGetLastError());
 
@@ -1062,8 +1140,10 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   HC(bucket_bits.alloc(B));
   const uint32_t lanes = lane_base[B];
   LaneArgs la;
-  la.bf16 = in->bf16;
-  la.fp8 = in->fp8;
+  la.bf16 = sp.bf16;
+  la.fp8 = sp.q;
+  la.qmask = qmask;
+  la.row_col = by_scale ? sc->bucket_col_start.p : nullptr;
   la.S = smap;
   la.m = m;
   la.row_offsets = sc->bucket_row_offsets.p;
@@ -1089,7 +1169,8 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   HC(hipMemcpyAsync(hflags, flags.p, sizeof(hflags), hipMemcpyDeviceToHost, s));
   HC(hipStreamSynchronize(s));
   if (hflags[1] & 2u) return fail(MPS_ERR_RUNTIME, "invalid code length");
-  if (hflags[1] & 4u) return fail(MPS_ERR_RUNTIME, "missing enc table for (scale,fp8) key");
+  if (hflags[1] & 4u)
+    return fail(MPS_ERR_RUNTIME, fp8 ? "missing enc table for (scale,fp8) key" : "missing enc table for (scale,qv) key");
   // 64-bit aligned bucket bases (build_huffman.cu:813-818), final cursor unaligned
   std::vector<int64_t> bit_base(B + 1, 0);
   int64_t pos = 0;
@@ -1105,7 +1186,8 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   HC(sc->bitstream.alloc((size_t)W));
   if (W) HC(hipMemsetAsync(sc->bitstream.p, 0, 8 * (size_t)W, s));
   PackArgs pa;
-  pa.bf16 = in->bf16;
+  pa.bf16 = sp.bf16;
+  pa.row_col = by_scale ? sc->bucket_col_start.p : nullptr;
   pa.m = m;
   pa.row_offsets = sc->bucket_row_offsets.p;
   pa.row_indices = sc->row_indices.p;
@@ -1120,15 +1202,18 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   pa.bits = reinterpret_cast<unsigned long long *>(sc->bitstream.p);
   if (lanes && W) hipLaunchKernelGGL(pack_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, pa);
   HC(hipGetLastError());
-  const int64_t shape[3] = {n, m, kth};
-  HC(sc->shape_nmk.alloc(3));
-  HC(hipMemcpyAsync(sc->shape_nmk.p, shape, sizeof(shape), hipMemcpyHostToDevice, s));
+  const int64_t shape[4] = {n, m, kth, by_scale ? (int64_t)col_len.front() : 0};
+  const int nshape = by_scale ? 4 : 3;
+  HC(sc->shape_nmk.alloc(nshape));
+  HC(hipMemcpyAsync(sc->shape_nmk.p, shape, 8 * nshape, hipMemcpyHostToDevice, s));
   HC(hipMemcpyAsync(hflags, flags.p, sizeof(hflags), hipMemcpyDeviceToHost, s));
   HC(hipStreamSynchronize(s));
 
+  // by scale, slots 5, 6 and 8 hold the group offsets, group rows and group column starts
   const int64_t sizes[17] = {(int64_t)G * Tsz, (int64_t)G * packed, G, G, B, B + 1, (int64_t)row_indices.size(),
-                             (int64_t)B * 256, B, B, (int64_t)B * (kth + 1), B + 1, W, 3, B, (int64_t)B * 256,
-                             (int64_t)B * 256};
+                             (int64_t)B * qvals, by_scale ? (int64_t)group_col.size() : B, by_scale ? 0 : B,
+                             (int64_t)B * (kth + 1), B + 1, W, nshape, fp8 ? B : 0, fp8 ? (int64_t)B * 256 : 0,
+                             fp8 ? (int64_t)B * 256 : 0};
   std::memcpy(sc->sizes, sizes, sizeof(sizes));
   sc->stats[0] = hflags[2];
   sc->stats[1] = hflags[3];
@@ -1137,6 +1222,99 @@ int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **
   *out = sc.release();
   return MPS_OK;
 #undef HC
+}
+
+}  // namespace
+}  // namespace mps
+
+extern "C" {
+
+int mps_fp8_encode(const mps_fp8_encode_in *in, void *stream, mps_fp8_sidecar **out) {
+  last_error().clear();
+  if (!in || !out) return fail(MPS_ERR_INVALID_ARGUMENT, "inputs must be defined");
+  *out = nullptr;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t L = in->max_len, kth = in->threads_per_block;
+  if (L <= 0 || L > 15) return fail(MPS_ERR_INVALID_ARGUMENT, "max_len must be in [1, 15]");
+  if (kth <= 0 || kth > 1024) return fail(MPS_ERR_INVALID_ARGUMENT, "threads_per_block must be in [1, 1024]");
+  const int64_t numel = in->numel;
+  if (in->ndim < 0 || in->ndim > 8 || in->scale_ndim < 0 || in->scale_ndim > 8)
+    return fail(MPS_ERR_INVALID_ARGUMENT, "too many dimensions");
+  // scale modes (build_huffman.cu:325-366)
+  const int64_t scale_numel = in->scale_numel;
+  const bool scale_scalar = scale_numel == 1;
+  const bool scale_per_elem = scale_numel == numel;
+  bool scale_per_row = false, scale_block2d = false;
+  int64_t n_rows = -1, n_cols = -1, sb0 = -1, sb1 = -1, nb0 = -1, nb1 = -1;
+  if (!scale_scalar && !scale_per_elem && in->ndim == 2) {
+    n_rows = in->dims[0];
+    n_cols = in->dims[1];
+    scale_per_row = scale_numel == n_rows;
+    if (!scale_per_row && in->scale_ndim == 2) {
+      nb0 = in->scale_dims[0];
+      nb1 = in->scale_dims[1];
+      if (nb0 > 0 && nb1 > 0 && n_rows % nb0 == 0 && n_cols % nb1 == 0) {
+        sb0 = n_rows / nb0;
+        sb1 = n_cols / nb1;
+        if (sb0 > 0 && sb1 > 0) scale_block2d = true;
+      }
+    }
+  }
+  if (!scale_scalar && !scale_per_elem && !scale_per_row && !scale_block2d)
+    return fail(MPS_ERR_INVALID_ARGUMENT,
+                "unsupported scales shape: use scalar, per-row (n,), per-element (numel), or 2D block-wise "
+                "[n/bs0,m/bs1]");
+  // The reference builds the tables before it checks the bucket layout; the
+  // checks below raise the same errors without the wasted work.
+  if (in->ndim != 2) return fail(MPS_ERR_INVALID_ARGUMENT, "bucket packing requires bf16_params to be 2D [n,m]");
+  const int64_t n = in->dims[0], m = in->dims[1];
+  if (n <= 0 || m <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "bf16_params shape must be non-empty");
+  if (!scale_block2d && !(scale_scalar || (!scale_per_elem && scale_per_row)))
+    return fail(MPS_ERR_INVALID_ARGUMENT,
+                "bucket packing requires scales to be scalar, per-row (n,), or 2D block-wise");
+  if (numel != n * m) return fail(MPS_ERR_INVALID_ARGUMENT, "bf16_params and fp8_params must have same numel");
+  if (numel >= (int64_t)1 << 32) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor too large for the GPU builder");
+  EncodeSpec sp{in->bf16, in->fp8, in->scales, n, m, scale_numel, scale_scalar, scale_per_row, scale_block2d,
+                nb0, nb1, sb0, sb1, L, kth, 0, kFmtFp8};
+  return encode_impl(sp, s, out);
+}
+
+
+int mps_awq_encode(const mps_awq_encode_in *in, void *stream, mps_fp8_sidecar **out) {
+  last_error().clear();
+  if (!in || !out) return fail(MPS_ERR_INVALID_ARGUMENT, "inputs must be defined");
+  *out = nullptr;
+  // checks of build_huffman.cu:1097-1153 (by scale) and :1605-1650, in order
+  const int64_t L = in->max_len, kth = in->threads_per_block, n = in->n, m = in->m;
+  if (L <= 0 || L > 15) return fail(MPS_ERR_INVALID_ARGUMENT, "max_len must be in (0,15]");
+  if (kth <= 0 || kth > 1024) return fail(MPS_ERR_INVALID_ARGUMENT, "threads_per_block must be in [1,1024]");
+  if (in->by_scale && in->group_cap <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "group_cap must be > 0");
+  if (n <= 0 || m <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "bf16_params shape must be non-empty");
+  if (in->scale_ndim < 0 || in->scale_ndim > 2) return fail(MPS_ERR_INVALID_ARGUMENT,
+      "unsupported scales_u16 shape: use scalar, per-row (n,), or 2D block-wise [n/bs0,m/bs1]");
+  const int64_t scale_numel = in->scale_numel;
+  const bool scalar = scale_numel == 1;
+  const bool per_row = !scalar && in->scale_ndim == 1 && scale_numel == n;
+  bool block2d = false;
+  int64_t nb0 = -1, nb1 = -1, sb0 = -1, sb1 = -1;
+  if (!scalar && !per_row && in->scale_ndim == 2) {
+    nb0 = in->scale_dims[0];
+    nb1 = in->scale_dims[1];
+    if (nb0 > 0 && nb1 > 0 && n % nb0 == 0 && m % nb1 == 0) {
+      sb0 = n / nb0;
+      sb1 = m / nb1;
+      block2d = sb0 > 0 && sb1 > 0;
+    }
+  }
+  if (!scalar && !per_row && !block2d)
+    return fail(MPS_ERR_INVALID_ARGUMENT,
+                "unsupported scales_u16 shape: use scalar, per-row (n,), or 2D block-wise [n/bs0,m/bs1]");
+  if (n * m >= (int64_t)1 << 32) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor too large for the GPU builder");
+  if (in->by_scale && n * (block2d ? nb1 : 1) >= (int64_t)1 << 31)
+    return fail(MPS_ERR_INVALID_ARGUMENT, "too many quantisation groups for the GPU builder");
+  EncodeSpec sp{in->bf16, in->int4, in->scales, n, m, scale_numel, scalar, per_row, block2d, nb0, nb1, sb0, sb1,
+                L, kth, in->group_cap, in->by_scale ? kFmtAwqByScale : kFmtAwqBucket};
+  return encode_impl(sp, reinterpret_cast<hipStream_t>(stream), out);
 }
 
 int mps_fp8_sidecar_sizes(const mps_fp8_sidecar *sc, int64_t *sizes17) {

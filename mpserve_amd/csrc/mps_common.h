@@ -28,6 +28,10 @@ inline int hip_fail(hipError_t e, const char *what) {
   return fail(MPS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// The per-device word the decode kernels OR their MPS_STATUS_* flags into
+// (allocated on first use, kept for the life of the process).
+int status_word(int device, uint32_t **out);
+
 }  // namespace mps
 
 #define MPS_HIP_CHECK(expr)                                        \

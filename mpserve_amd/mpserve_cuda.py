@@ -229,7 +229,13 @@ for _name in ("init_cuda", "cleanup_cuda", "build_trie_AWQ", "build_trie", "quer
               "get_trie_count", "get_tot_path_length", "save_trie_collection", "load_trie_collection",
               "save_trie_collection_awq", "load_trie_collection_awq", "load_bf16_from_int8", "dequantize_awq",
               "build_trie_AWQ_to_FP8", "save_trie_collection_awq_to_fp8", "load_trie_collection_awq_to_fp8",
-              "huffman_build_awq_decode_tables", "huffman_decode_awq_shared_table",
-              "huffman_build_awq_int4_bucket_decode_tables", "huffman_build_awq_int4_bucket_decode_tables_by_scale",
-              "huffman_decode_awq_int4_bucket", "huffman_decode_awq_int4_bucket_by_scale"):
+              "huffman_build_awq_decode_tables", "huffman_decode_awq_shared_table"):
     globals()[_name] = _not_in_scope(_name)
+
+# AWQ int4 bucket builders and decoders (wrapper.cpp:275-416).
+from .awq import (huffman_build_awq_int4_bucket_decode_tables,  # noqa: E402
+                  huffman_build_awq_int4_bucket_decode_tables_by_scale, huffman_decode_awq_int4_bucket,
+                  huffman_decode_awq_int4_bucket_by_scale)
+
+__all__ += ["huffman_build_awq_int4_bucket_decode_tables", "huffman_build_awq_int4_bucket_decode_tables_by_scale",
+            "huffman_decode_awq_int4_bucket", "huffman_decode_awq_int4_bucket_by_scale"]

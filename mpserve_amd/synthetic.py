@@ -58,3 +58,35 @@ def make_weight(n: int, m: int, sigma: float = 0.02, seed: int = 0, outlier_p: f
     w = w.to(torch.bfloat16)
     q, s, key = quantize_per_row(w)
     return SyntheticWeight(w.contiguous(), q, s, key)
+
+
+@dataclass
+class SyntheticAwqWeight:
+    bf16: torch.Tensor       # [n, m] bfloat16
+    int4_u8: torch.Tensor    # [n, m] uint8, int4 values 0..15
+    scale_u16: torch.Tensor  # [n, m // group] (or [n] when group is None) uint16: BF16 bits of the scale
+
+
+def make_awq_weight(n: int, m: int, group: int | None = 128, sigma: float = 0.02, seed: int = 0,
+                    device: str | torch.device = "cpu") -> SyntheticAwqWeight:
+    """Seeded BF16 weight and an AWQ-style int4 quantisation of it.
+
+    The scale of each group of ``group`` columns of a row (of a whole row when
+    ``group`` is None) is ``absmax / 7`` rounded to BF16, and the int4 value is
+    ``clamp(round(w / s) + 8, 0, 15)`` (zero point 8). The sidecar the AWQ
+    builders write depends only on these three tensors, not on how the int4
+    values were chosen.
+    """
+    g = torch.Generator(device=device).manual_seed(int(seed))
+    w = (torch.randn((n, m), generator=g, device=device, dtype=torch.float32) * sigma).to(torch.bfloat16)
+    wf = w.float()
+    gs = m if group is None else int(group)
+    amax = wf.reshape(n, m // gs, gs).abs().amax(dim=2)
+    s = (amax / 7.0).to(torch.bfloat16)
+    s = torch.where(s.float() > 0, s, torch.ones_like(s))
+    sf = s.float().repeat_interleave(gs, dim=1)
+    q = (torch.round(wf / sf) + 8).clamp(0, 15).to(torch.uint8)
+    key = s.view(torch.uint16)
+    if group is None:
+        key = key.reshape(n)
+    return SyntheticAwqWeight(w.contiguous(), q.contiguous(), key.contiguous())

@@ -1,0 +1,155 @@
+"""AWQ int4 path on the GPU: builders byte for byte against the oracle, decoders
+bit for bit against the input (and the oracle's decode), through MPServe_cuda.
+
+Integer work: the bar is equality.
+"""
+import numpy as np
+import pytest
+import torch
+
+import MPServe_cuda
+import oracle
+from mpserve_amd import awq
+from mpserve_amd.mpserve_cuda import read_status
+from mpserve_amd.synthetic import make_awq_weight
+from tests.test_awq_oracle import esc_inputs
+
+DEV = "cuda:0"
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # name, n, m, group (None: per row), k, by_scale, group_cap
+    ("row_per_row_k256", 192, 512, None, 256, False, 1024),
+    ("row_block2d_g128_k256", 64, 512, 128, 256, False, 1024),
+    ("row_block2d_g64_k1024", 96, 256, 64, 1024, False, 1024),
+    ("row_per_row_k1", 8, 64, None, 1, False, 1024),
+    ("by_scale_g128_k256", 128, 512, 128, 256, True, 1024),
+    ("by_scale_g128_k1024_cap16", 128, 512, 128, 1024, True, 16),
+    ("by_scale_per_row_k100", 96, 384, None, 100, True, 1024),
+    ("by_scale_g32_k7", 32, 256, 32, 7, True, 5),
+]
+
+
+def _inputs(name, n, m, group):
+    w = make_awq_weight(n, m, group, seed=sum(map(ord, name)))
+    return w.bf16, w.int4_u8, w.scale_u16
+
+
+def _build(bf16, q, sc, k, by_scale, cap):
+    if by_scale:
+        return MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables_by_scale(bf16, q, sc, 11, k, cap)
+    return MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables(bf16, q, sc, 11, k)
+
+
+def _same(got, want):
+    assert list(got) == list(want)
+    for key, v in want.items():
+        g = got[key].numpy()
+        assert g.shape == v.shape, (key, g.shape, v.shape)
+        assert np.array_equal(g.view(v.dtype) if g.dtype != v.dtype else g, v), \
+            f"{key}: {(g != v).sum()} entries differ"
+
+
+def _decode(d, q, n, m, by_scale):
+    t = {k: v.to(DEV) for k, v in d.items()}
+    qd = q.to(DEV)
+    if by_scale:
+        out = MPServe_cuda.huffman_decode_awq_int4_bucket_by_scale(
+            qd, t["bitstream_u64"], t["decode_syms_u16"], t["decode_lens_u8"], t["bucket_table_i32"],
+            t["bucket_group_offsets_i32"], t["group_rows_i32"], t["group_col_start_i32"],
+            t["bucket_thread_startbit_u32"], t["bucket_bit_base_i64"], n, m, 11, int(d["shape_nmkg_i64"][3]))
+    else:
+        out = MPServe_cuda.huffman_decode_awq_int4_bucket(
+            qd, t["bitstream_u64"], t["decode_syms_u16"], t["decode_lens_u8"], t["bucket_table_i32"],
+            t["bucket_col_start_i32"], t["bucket_col_len_i32"], t["bucket_row_offsets_i32"], t["row_indices_i32"],
+            t["bucket_thread_startbit_u32"], t["bucket_bit_base_i64"], n, m, 11)
+    torch.cuda.synchronize()
+    return out.view(torch.uint16).cpu().numpy()
+
+
+@pytest.mark.parametrize("name,n,m,group,k,by_scale,cap", CASES, ids=[c[0] for c in CASES])
+def test_build_matches_oracle_and_decode_round_trips(name, n, m, group, k, by_scale, cap):
+    print(f"[awq] {name}", flush=True)
+    bf16, q, sc = _inputs(name, n, m, group)
+    bits = bf16.view(torch.uint16).numpy()
+    got = _build(bf16, q, sc, k, by_scale, cap)
+    want = oracle.awq_encode(bits, q.numpy(), sc.numpy(), 11, k, cap, by_scale)
+    _same(got, want)
+    read_status(torch.device(DEV))
+    out = _decode(got, q, n, m, by_scale)
+    assert np.array_equal(out, bits)
+    assert np.array_equal(out, oracle.awq_decode(want, q.numpy(), n, m))
+    assert read_status(torch.device(DEV)) == 0
+
+
+@pytest.mark.parametrize("by_scale", [False, True])
+def test_esc_keys(by_scale):
+    print(f"[awq] esc by_scale={by_scale}", flush=True)
+    bits, q, sc = esc_inputs(with_zero=not by_scale)
+    bf16 = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    qt, st = torch.from_numpy(q), torch.from_numpy(sc.view(np.int16)).view(torch.uint16)
+    got = _build(bf16, qt, st, 256, by_scale, 1024)
+    want, stats = oracle.awq_encode(bits, q, sc, 11, 256, 1024, by_scale, with_stats=True)
+    assert stats["esc_keys"] == 1
+    _same(got, want)  # row buckets: includes the reference's ESC collisions (bare ESC codes)
+    if by_scale:
+        read_status(torch.device(DEV))
+        assert np.array_equal(_decode(got, qt, 64, 1024, True), bits)
+        assert read_status(torch.device(DEV)) == 0
+
+
+def test_esc_round_trip_row_buckets():
+    print("[awq] esc row buckets, no collision", flush=True)
+    bits, q, sc = esc_inputs(with_zero=False)
+    bf16 = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    qt, st = torch.from_numpy(q), torch.from_numpy(sc.view(np.int16)).view(torch.uint16)
+    got = _build(bf16, qt, st, 1024, False, 1024)
+    assert np.array_equal(_decode(got, qt, 64, 1024, False), bits)
+
+
+def test_cuda_inputs_give_cuda_outputs_and_same_bytes():
+    bf16, q, sc = _inputs("cuda_in", 64, 256, 64)
+    host = _build(bf16, q, sc, 256, True, 1024)
+    dev = _build(bf16.to(DEV), q.to(DEV), sc.to(DEV), 256, True, 1024)
+    for key in host:
+        assert dev[key].is_cuda
+        assert torch.equal(dev[key].cpu(), host[key])
+
+
+@pytest.mark.parametrize("by_scale", [False, True])
+def test_full_size_round_trip(by_scale):
+    """Llama-3-8B q_proj, group 128: GPU build, GPU decode, equality with the input."""
+    print(f"[awq] 4096x4096 by_scale={by_scale}", flush=True)
+    w = make_awq_weight(4096, 4096, 128 if by_scale else None, seed=21, device=DEV)
+    d = _build(w.bf16, w.int4_u8, w.scale_u16, 1024, by_scale, 1024)
+    read_status(torch.device(DEV))
+    t = {k: v for k, v in d.items()}
+    if by_scale:
+        out = awq.huffman_decode_awq_int4_bucket_by_scale(
+            w.int4_u8, t["bitstream_u64"], t["decode_syms_u16"], t["decode_lens_u8"], t["bucket_table_i32"],
+            t["bucket_group_offsets_i32"], t["group_rows_i32"], t["group_col_start_i32"],
+            t["bucket_thread_startbit_u32"], t["bucket_bit_base_i64"], 4096, 4096, 11, 128)
+    else:
+        out = awq.huffman_decode_awq_int4_bucket(
+            w.int4_u8, t["bitstream_u64"], t["decode_syms_u16"], t["decode_lens_u8"], t["bucket_table_i32"],
+            t["bucket_col_start_i32"], t["bucket_col_len_i32"], t["bucket_row_offsets_i32"], t["row_indices_i32"],
+            t["bucket_thread_startbit_u32"], t["bucket_bit_base_i64"], 4096, 4096, 11)
+    assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16))
+    assert read_status(torch.device(DEV)) == 0
+
+
+def test_decode_argument_checks():
+    bf16, q, sc = _inputs("checks", 32, 256, 128)
+    d = {k: v.to(DEV) for k, v in _build(bf16, q, sc, 256, False, 1024).items()}
+    qd = q.to(DEV)
+    args = [qd, d["bitstream_u64"], d["decode_syms_u16"], d["decode_lens_u8"], d["bucket_table_i32"],
+            d["bucket_col_start_i32"], d["bucket_col_len_i32"], d["bucket_row_offsets_i32"], d["row_indices_i32"],
+            d["bucket_thread_startbit_u32"], d["bucket_bit_base_i64"], 32, 256]
+    with pytest.raises(ValueError, match="max_len must be 11"):
+        MPServe_cuda.huffman_decode_awq_int4_bucket(*args, 7)
+    with pytest.raises(ValueError, match="int4_values_u8 numel must equal n\\*m"):
+        MPServe_cuda.huffman_decode_awq_int4_bucket(*args[:-2], 31, 256)
+    bad = list(args)
+    bad[4] = d["bucket_table_i32"][:, :8].contiguous()
+    with pytest.raises(ValueError, match=r"bucket_table_i32 must be int32 CUDA \[B,16\]"):
+        MPServe_cuda.huffman_decode_awq_int4_bucket(*bad)

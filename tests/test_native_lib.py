@@ -20,7 +20,7 @@ def _declared():
 def test_header_declares_entry_points():
     names = _declared()
     for required in ("mps_fp8_decode", "mps_fp8_plan_create", "mps_fp8_plan_decode", "mps_last_error",
-                     "mps_clock_rate_khz", "mps_fp8_encode"):
+                     "mps_clock_rate_khz", "mps_fp8_encode", "mps_awq_decode", "mps_awq_encode"):
         assert required in names
 
 

@@ -1,5 +1,7 @@
 """Argument checks of the drop-in ops: same exception types and messages as the
 reference's entry points (decode_huffman.cu:606-697, build_huffman.cu:298-366)."""
+import inspect
+
 import numpy as np
 import pytest
 import torch
@@ -39,9 +41,52 @@ def test_sidecar_keys_match_reference_order():
 
 
 def test_out_of_scope_ops_raise_not_implemented():
-    for name in ("dequantize_awq", "huffman_decode_awq_int4_bucket", "build_trie"):
+    for name in ("dequantize_awq", "huffman_decode_awq_shared_table", "build_trie"):
         with pytest.raises(NotImplementedError):
             getattr(MPServe_cuda, name)()
+
+
+def test_awq_int4_op_signatures_match_reference():
+    """Argument names and defaults of wrapper.cpp:275-416."""
+    sig = inspect.signature
+    p = sig(MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables).parameters
+    assert list(p)[:5] == ["bf16_params", "int4_values_u8", "scales_u16", "max_len", "threads_per_block"]
+    assert (p["max_len"].default, p["threads_per_block"].default) == (11, 256)
+    p = sig(MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables_by_scale).parameters
+    assert list(p)[:6] == ["bf16_values", "int4_values", "scales_u16", "max_len", "threads", "group_cap"]
+    assert (p["max_len"].default, p["threads"].default, p["group_cap"].default) == (11, 256, 1024)
+    p = sig(MPServe_cuda.huffman_decode_awq_int4_bucket).parameters
+    assert list(p)[:14] == ["int4_values_u8", "bitstream_u64", "decode_syms_u16", "decode_lens_u8",
+                            "bucket_table_i32", "bucket_col_start_i32", "bucket_col_len_i32",
+                            "bucket_row_offsets_i32", "row_indices_i32", "bucket_thread_startbit_u32",
+                            "bucket_bit_base_i64", "n", "m", "max_len"]
+    assert p["max_len"].default == 11
+    p = sig(MPServe_cuda.huffman_decode_awq_int4_bucket_by_scale).parameters
+    assert list(p)[:14] == ["int4_values_u8", "bitstream_u64", "decode_syms_u16", "decode_lens_u8",
+                            "bucket_table_i32", "bucket_group_offsets_i32", "group_rows_i32",
+                            "group_col_start_i32", "bucket_thread_startbit_u32", "bucket_bit_base_i64", "n", "m",
+                            "max_len", "group_size"]
+    assert p["max_len"].default is inspect.Parameter.empty and p["group_size"].default is inspect.Parameter.empty
+
+
+def test_awq_build_argument_messages():
+    """build_huffman.cu:1082-1123 / :1589-1623, checked before any GPU work."""
+    bf = torch.zeros(4, 8, dtype=torch.bfloat16)
+    q = torch.zeros(4, 8, dtype=torch.uint8)
+    sc = torch.zeros(4, dtype=torch.uint16)
+    b, bs = MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables, \
+        MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables_by_scale
+    for args, msg in (((bf.float(), q, sc), "bf16_params must be torch.bfloat16"),
+                      ((bf, q.int(), sc), "int4_values_u8 must be torch.uint8"),
+                      ((bf, q, sc.int()), r"scales_u16 must be torch.uint16 \(bf16 raw bits\)"),
+                      ((bf, q, sc, 0), r"max_len must be in \(0,15\]"),
+                      ((bf, q, sc, 11, 1025), r"threads_per_block must be in \[1,1024\]"),
+                      ((bf.reshape(-1), q.reshape(-1), sc), r"bf16_params must be 2D \[n,m\]"),
+                      ((bf, q[:, :4], sc), "int4_values_u8 shape must match bf16_params")):
+        with pytest.raises(ValueError, match=msg):
+            b(*args)
+    with pytest.raises(ValueError, match="group_cap must be > 0"):
+        bs(bf, q, sc, 11, 256, 0)
 
 
 def test_decode_validation_messages_via_meta_checks(monkeypatch):
