@@ -47,10 +47,11 @@ def parse_args(argv=None):
     # load: with 3 warm-up launches a fresh box measures the model decode ~4%
     # slower than after 1000 (about 6 s).
     p.add_argument("--warmup", type=int, default=1000)
-    p.add_argument("--workload", choices=("model8b", "layer8b", "layer70b", "gemm8b"), default="model8b",
+    p.add_argument("--workload", choices=("model8b", "layer8b", "layer70b", "gemm8b", "awq8b"), default="model8b",
                    help="model8b: full Llama-3-8B-shaped model (the headline, config 5); layer8b: one 8B "
                         "layer (config 2); layer70b: one 70B layer with outliers and ESC codes (config 3); "
-                        "gemm8b: decode share of an 8B layer's latency next to its BF16 GEMMs (config 4)")
+                        "gemm8b: decode share of an 8B layer's latency next to its BF16 GEMMs (config 4); "
+                        "awq8b: AWQ int4 decode of one 8B layer, by-scale and row-bucket sidecars")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="time budget of the CPU baseline sample")
     p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: min(16, cpu_count))")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -66,7 +67,136 @@ WORKLOADS = {
     "layer8b": "cfg2: one Llama-3-8B layer, 7 linears",
     "layer70b": "cfg3: one Llama-3-70B layer, 7 linears, sigma 0.015 with 0.1% outliers at +-8 sigma",
     "gemm8b": "cfg4: one Llama-3-8B layer decoded into preallocated scratch + BF16 GEMMs, T in {1,16,128,1024}",
+    "awq8b": "AWQ int4 (group 128, zero point 8) one Llama-3-8B layer, max_len 11, k 1024: by-scale sidecar "
+             "(group buckets) and row-bucket sidecar (per-row scales)",
 }
+
+
+def awq_algorithmic_bytes(n: int, m: int, sc) -> int:
+    """Bytes one AWQ int4 decode must move: int4 bytes + bitstream + each table
+    once (2048 u16 symbols + 1024 length bytes) + bucket and row/group metadata
+    read, BF16 written."""
+    N = n * m
+    B = sc["bucket_table_i32"].shape[0]
+    k = sc["bucket_thread_startbit_u32"].shape[1] - 1
+    meta = B * (16 * 4 + 4 * (k + 1) + 8 + 4)
+    if "group_rows_i32" in sc:
+        meta += 8 * sc["group_rows_i32"].numel()
+    else:
+        meta += B * 8 + 4 * sc["row_indices_i32"].numel()
+    return N + 8 * sc["bitstream_u64"].numel() + 5120 * sc["decode_syms_u16"].shape[0] + meta + 2 * N
+
+
+def run_awq(args, dev) -> int:
+    """AWQ int4 decode: each weight of one 8B layer through the drop-in ops, per layout."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from mpserve_amd import awq
+    from mpserve_amd.synthetic import LLAMA3_8B_LAYER, make_awq_weight
+
+    stream = torch.cuda.current_stream(dev)
+    layouts = {}
+    for layout, group in (("by_scale", 128), ("row_buckets", None)):
+        items = []
+        for j, (name, n, m) in enumerate(LLAMA3_8B_LAYER):
+            w = make_awq_weight(n, m, group, seed=300 + j, device=dev)
+            scales = w.scale_u16
+            sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, scales, 11, 1024, 1024, bool(group), with_stats=True)
+            if group:
+                call = lambda sc=sc, w=w, n=n, m=m, o=None: awq.huffman_decode_awq_int4_bucket_by_scale(  # noqa: E731
+                    w.int4_u8, sc["bitstream_u64"], sc["decode_syms_u16"], sc["decode_lens_u8"],
+                    sc["bucket_table_i32"], sc["bucket_group_offsets_i32"], sc["group_rows_i32"],
+                    sc["group_col_start_i32"], sc["bucket_thread_startbit_u32"], sc["bucket_bit_base_i64"], n, m,
+                    11, 128, out=o)
+            else:
+                call = lambda sc=sc, w=w, n=n, m=m, o=None: awq.huffman_decode_awq_int4_bucket(  # noqa: E731
+                    w.int4_u8, sc["bitstream_u64"], sc["decode_syms_u16"], sc["decode_lens_u8"],
+                    sc["bucket_table_i32"], sc["bucket_col_start_i32"], sc["bucket_col_len_i32"],
+                    sc["bucket_row_offsets_i32"], sc["row_indices_i32"], sc["bucket_thread_startbit_u32"],
+                    sc["bucket_bit_base_i64"], n, m, 11, out=o)
+            out = torch.empty((n, m), dtype=torch.bfloat16, device=dev)
+            items.append((name, n, m, w, sc, call, out, st))
+        layouts[layout] = items
+        log(f"{layout}: built 7 sidecars")
+
+    def layer_step(items):
+        for _, _, _, _, _, call, out, _ in items:
+            call(o=out)
+
+    results = {}
+    for layout, items in layouts.items():
+        for _ in range(max(1, args.warmup // 10)):
+            layer_step(items)
+        torch.cuda.synchronize()
+        exact = {}
+        for name, _, _, w, _, _, out, st in items:
+            exact[name] = torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16))
+            # only ESC collisions of the row-bucket builder (bare ESC codes) may differ
+            if not exact[name] and st["esc_collisions"] == 0:
+                raise RuntimeError(f"AWQ decode ({layout}) of {name} is not bit-exact")
+        per = []
+        tot_alg = tot_ms = 0.0
+        for name, n, m, w, sc, call, out, st in items:
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(args.steps)]
+            for s, e in ev:
+                s.record(stream)
+                call(o=out)
+                e.record(stream)
+            torch.cuda.synchronize()
+            ms = sum(s.elapsed_time(e) for s, e in ev) / args.steps
+            alg = awq_algorithmic_bytes(n, m, sc)
+            tot_alg += alg
+            tot_ms += ms
+            per.append({"tensor": name, "shape": [n, m], "buckets": int(sc["bucket_table_i32"].shape[0]),
+                        "tables": int(sc["decode_syms_u16"].shape[0]),
+                        "bits_per_elem": round(8 * sc["bitstream_u64"].numel() / (n * m), 3),
+                        "esc_keys": st["esc_keys"], "esc_collisions": st["esc_collisions"],
+                        "bit_exact": exact[name],
+                        "ms": round(ms, 4), "rw_gbs": round(alg / ms / 1e6, 1),
+                        "pct_hbm_peak_rw": round(100 * alg / ms / 1e6 / HBM_PEAK_GBS, 2)})
+            log(f"{layout} {name} {n}x{m}: {ms:.4f} ms, {per[-1]['pct_hbm_peak_rw']}% of HBM peak")
+        elems = sum(n * m for _, n, m, *_ in items)
+        results[layout] = {"layer_decode_ms": round(tot_ms, 4), "out_gbs": round(2 * elems / tot_ms / 1e6, 1),
+                           "algorithmic_bytes": int(tot_alg), "achieved_gbs": round(tot_alg / tot_ms / 1e6, 1),
+                           "per_tensor": per}
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        done = 0
+        elapsed = 0.0
+        while elapsed < args.cpu_seconds:
+            for name, n, m, w, sc, _, _, _ in layouts["by_scale"]:
+                hsc = {k: v.cpu().numpy() for k, v in sc.items()}
+                q = w.int4_u8.cpu().numpy()
+                t0 = time.perf_counter()
+                got = oracle.awq_decode(hsc, q, n, m, nthreads=threads)
+                elapsed += time.perf_counter() - t0
+                if not np.array_equal(got, w.bf16.view(torch.uint16).cpu().numpy()):
+                    raise RuntimeError(f"CPU baseline AWQ decode of {name} is not bit-exact")
+                done += n * m
+                if elapsed >= args.cpu_seconds:
+                    break
+        cpu = {"value": round(2 * done / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"oracle AWQ by-scale decode of layer-0 weights, {done / 1e6:.1f} M elements in "
+                         f"{elapsed:.2f} s"}
+    head = results["by_scale"]
+    result = {
+        "metric": "AWQ int4 -> BF16 decompress GB/s (out); one Llama-3-8B layer",
+        "value": head["out_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head["layer_decode_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u16", "data": "synthetic: seeded N(0,0.02^2) BF16, AWQ-style int4 (group 128), sidecar built on "
+                                "the GPU",
+        "config": {"workload": WORKLOADS["awq8b"], "layouts": results},
+        "roofline": {"bound": "hbm", "achieved": head["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": head["algorithmic_bytes"], "kernel_ms": head["layer_decode_ms"]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def weight_list(workload: str):
@@ -315,6 +445,8 @@ def main(argv=None) -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.workload == "awq8b":
+        return run_awq(args, dev)
     weights = weight_list(args.workload)
     log(f"workload {args.workload}: {len(weights)} tensors, building inputs on {torch.cuda.get_device_name(dev)}")
 

@@ -142,7 +142,7 @@ typedef struct mps_awq_tensor {
   const int64_t *bucket_bit_base;        /* [num_buckets+1] */
   int64_t num_buckets;
   int64_t k;                             /* 1..1024 */
-  int64_t n, m;                          /* output shape [n, m], n*m < 2^32 - 1 */
+  int64_t n, m;                          /* output shape [n, m], n*m < 2^31 */
   uint16_t *out;                         /* [n*m] BF16 bit patterns (device) */
 } mps_awq_tensor;
 

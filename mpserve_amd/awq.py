@@ -47,7 +47,17 @@ BY_SCALE_KEYS = (
 _ESIZE = {torch.uint16: 2, torch.uint8: 1, torch.int32: 4, torch.uint32: 4, torch.int64: 8, torch.uint64: 8}
 
 
-def _build(bf16, int4, scales, max_len, threads, group_cap, by_scale: bool) -> Dict[str, torch.Tensor]:
+def build_awq_sidecar(bf16, int4, scales, max_len: int = 11, threads: int = 256, group_cap: int = 1024,
+                      by_scale: bool = False, *, with_stats: bool = False):
+    """Either AWQ int4 sidecar dict; with ``with_stats`` also {esc_keys, esc_collisions}:
+    keys coded with an ESC symbol, and elements whose symbol equals their key's
+    ESC symbol without being kept (the row-bucket builder can pick such a
+    symbol; those elements are written as a bare ESC code, which decodes to
+    16 bits read from the next codes, in the reference as here)."""
+    return _build(bf16, int4, scales, int(max_len), int(threads), int(group_cap), bool(by_scale), with_stats)
+
+
+def _build(bf16, int4, scales, max_len, threads, group_cap, by_scale: bool, with_stats: bool = False):
     # build_huffman.cu:1082-1123 (by scale) / :1589-1623, in order
     if bf16 is None or int4 is None or scales is None:
         raise ValueError("inputs must be defined")
@@ -106,8 +116,12 @@ def _build(bf16, int4, scales, max_len, threads, group_cap, by_scale: bool) -> D
                 out[key] = t
                 ptrs[slot] = t.data_ptr() if t.numel() else None
             _native.check(lib.mps_fp8_sidecar_copy(handle, ptrs, stream))
+            stats = (ctypes.c_int64 * 4)()
+            _native.check(lib.mps_fp8_sidecar_stats(handle, stats))
         finally:
             lib.mps_fp8_sidecar_free(handle)
+    if with_stats:
+        return out, {"esc_keys": int(stats[0]), "esc_collisions": int(stats[1])}
     return out
 
 
@@ -152,8 +166,8 @@ def _launch(int4, bitstream, syms, lens, table, col_start, col_len, offsets, row
     d.bucket_thread_startbit, d.bucket_bit_base = startbit.data_ptr(), bit_base.data_ptr()
     d.num_buckets, d.k = table.size(0), startbit.size(1) - 1
     d.n, d.m, d.out = n, m, out.data_ptr()
-    if n * m >= (1 << 32) - 1:
-        raise ValueError("tensor too large for the AWQ decode kernel (n*m >= 2^32 - 1)")
+    if n * m >= (1 << 31):
+        raise ValueError("tensor too large for the AWQ decode kernel (n*m >= 2^31)")
     if group_col is not None and rows.numel() > 0 and group_col.data_ptr() == 0:
         raise ValueError("group_col_start_i32 must be defined")
     with torch.cuda.device(dev):

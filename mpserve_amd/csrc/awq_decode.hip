@@ -39,7 +39,15 @@ constexpr int kAwqBlock = 1024;           // work-items per bucket workgroup (>=
 constexpr int kLutEntries = 16 * kAwqTable;
 constexpr int kRowSlots = 8192;           // row (group) start offsets staged in LDS
 constexpr uint32_t kBadBase = 0xFFFFFFFFu;
-constexpr int kDepth = 4;
+// Elements per block, and the chunk queue: a block of kDepth codes without
+// ESC takes at most kStage 32-bit chunks from the queue, kStage chunks are
+// staged (loaded) one block ahead, and the queue holds 2 * kStage.
+#ifndef MPS_AWQ_DEPTH
+#define MPS_AWQ_DEPTH 8
+#endif
+constexpr int kDepth = MPS_AWQ_DEPTH;
+constexpr int kStage = (kDepth * kAwqL + 31) / 32;
+constexpr int kQueue = 2 * kStage;
 
 __device__ __forceinline__ void flag(uint32_t *status, unsigned int f) { atomicOr(status, f); }
 
@@ -54,88 +62,50 @@ __device__ __forceinline__ uint32_t chunk_at(const uint32_t *__restrict__ bs32, 
 
 __device__ uint32_t g_awq_zero_chunks[2];
 
-// Element offset (row * m + column start) of row (group) rr of the bucket.
+// Element offset (row * m + column start) of row (group) rr of the bucket;
+// kStaged: every row of the bucket is staged in LDS.
+template <bool kStaged>
 __device__ __forceinline__ uint32_t row_base(const mps_awq_tensor &T, const uint32_t *__restrict__ s_base,
                                              int32_t ra, int32_t rr, int32_t c0, int32_t cl) {
-  if (rr < kRowSlots) return s_base[rr];
+  if (kStaged || rr < kRowSlots) return s_base[rr];
   const int64_t row = T.row_indices[ra + rr];
   const int64_t col = T.group_col_start ? (int64_t)T.group_col_start[ra + rr] : (int64_t)c0;
   if (row < 0 || row >= T.n || col < 0 || col + cl > T.m) return kBadBase;
   return (uint32_t)(row * T.m + col);
 }
 
-__global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T, uint32_t *status) {
-  __shared__ uint32_t lut[kLutEntries];
-  __shared__ uint32_t s_base[kRowSlots];
-  const int64_t b = blockIdx.x;
-  const int tid = threadIdx.x;
-  // Bucket geometry (decode_huffman.cu:417-444, :528-545).
-  const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
-  const int32_t rows = rb - ra;
-  if (rows <= 0) return;
-  const bool by_scale = T.group_col_start != nullptr;
-  const int32_t c0 = by_scale ? 0 : T.bucket_col_start[b];
-  const int32_t cl = by_scale ? (int32_t)T.group_size : T.bucket_col_len[b];
-  if (cl <= 0 || ra < 0 || (int64_t)rb > T.num_row_indices ||
-      (!by_scale && (c0 < 0 || (int64_t)c0 + cl > T.m))) {
-    if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
-    return;
-  }
-  const int64_t total = (int64_t)rows * cl;
-  const int32_t k = (int32_t)T.k;
-  const int32_t k_eff = total < k ? (int32_t)total : k;
-
-  // Tables: entry (q << 11) | p = sym << 16 | nibble; a missing table (id -1)
-  // is all ESC entries, as the reference decodes it.
-  for (int i = tid; i < kLutEntries; i += kAwqBlock) {
-    const int q = i >> kAwqL, p = i & (kAwqTable - 1);
-    const int32_t gid = T.bucket_table[b * 16 + q];
-    uint32_t ent = 15u;
-    if (gid >= 0 && gid < T.num_tables) {
-      const uint32_t v = T.decode_lens[(int64_t)gid * kAwqPacked + (p >> 1)];
-      ent = ((uint32_t)T.decode_syms[(int64_t)gid * kAwqTable + p] << 16) | ((p & 1) ? (v >> 4) : (v & 15u));
-    } else if (gid != -1 && p == 0) {
-      flag(status, MPS_STATUS_BAD_TABLE);
-    }
-    lut[i] = ent;
-  }
-  const int32_t staged = rows < kRowSlots ? rows : kRowSlots;
-  for (int r = tid; r < staged; r += kAwqBlock) {
-    const int64_t row = T.row_indices[ra + r];
-    const int64_t col = by_scale ? (int64_t)T.group_col_start[ra + r] : (int64_t)c0;
-    uint32_t base = kBadBase;
-    if (row >= 0 && row < T.n && col >= 0 && col + cl <= T.m) base = (uint32_t)(row * T.m + col);
-    else flag(status, MPS_STATUS_BAD_ROW);
-    s_base[r] = base;
-  }
-  __syncthreads();
-  if (tid >= k_eff) return;
-
+// One lane's substream (the element walk, the bit supply and the stores).
+template <bool kStaged>
+__device__ __forceinline__ void awq_lane(const mps_awq_tensor &T, const uint32_t *__restrict__ lut,
+                                         const uint32_t *__restrict__ s_base, int64_t b, int32_t ra, int32_t c0,
+                                         int32_t cl, int64_t total, int32_t k, int32_t k_eff, int lane,
+                                         uint32_t *status) {
   const uint32_t *__restrict__ sb = T.bucket_thread_startbit + b * ((int64_t)k + 1);
-  const uint64_t pos0 = (uint64_t)T.bucket_bit_base[b] + sb[tid];
-  const uint64_t pos_end = (uint64_t)T.bucket_bit_base[b] + sb[tid + 1];
+  const uint64_t pos0 = (uint64_t)T.bucket_bit_base[b] + sb[lane];
+  const uint64_t pos_end = (uint64_t)T.bucket_bit_base[b] + sb[lane + 1];
   const bool empty = T.bitstream_words <= 0;
   const uint32_t *__restrict__ bs32 = empty ? g_awq_zero_chunks : reinterpret_cast<const uint32_t *>(T.bitstream);
   const uint64_t nchunks = empty ? 2u : (uint64_t)T.bitstream_words * 2u;
 
-  // Initial fill: buffer from chunks cb, cb+1; queue = cb+2 .. cb+5; tail = cb+6.
+  // Initial fill: buffer from chunks cb, cb+1; queue = the next kQueue chunks.
   const uint64_t cb = pos0 >> 5;
   const int skip = (int)(pos0 & 31u);
   uint64_t buf = (((uint64_t)chunk_at(bs32, nchunks, cb) << 32) | chunk_at(bs32, nchunks, cb + 1)) << skip;
   int cnt = 64 - skip;
-  uint32_t q0 = chunk_at(bs32, nchunks, cb + 2), q1 = chunk_at(bs32, nchunks, cb + 3);
-  uint32_t q2 = chunk_at(bs32, nchunks, cb + 4), q3 = chunk_at(bs32, nchunks, cb + 5);
-  int qn = 4;
-  uint64_t tail = cb + 6;
+  uint32_t qq[kQueue];
+#pragma unroll
+  for (int j = 0; j < kQueue; ++j) qq[j] = chunk_at(bs32, nchunks, cb + 2 + j);
+  int qn = kQueue;
+  uint64_t tail = cb + 2 + kQueue;  // index of the first chunk not yet in buf/queue
 
   // Element walk e = tid + i*k_eff -> (rr, cc) = (e / cl, e % cl), incrementally.
-  int32_t rr = tid / cl;
-  int32_t cc = tid - rr * cl;
+  int32_t rr = lane / cl;
+  int32_t cc = lane - rr * cl;
   const int32_t dr = k_eff / cl, dc = k_eff - dr * cl;
-  const int32_t count = (int32_t)((total - tid + k_eff - 1) / k_eff);
+  const int32_t count = (int32_t)((total - lane + k_eff - 1) / k_eff);
   const uint8_t *__restrict__ qv = T.int4;
-  uint16_t *__restrict__ out = T.out;
-  const uint32_t first = row_base(T, s_base, ra, rr, c0, cl);
+  char *__restrict__ outb = reinterpret_cast<char *>(T.out);
+  const uint32_t first = row_base<kStaged>(T, s_base, ra, rr, c0, cl);
   const uint32_t safe = first == kBadBase ? 0u : first + (uint32_t)cc;  // an address every lane may read
   int32_t walked = 0;
   auto next_block = [&](uint32_t (&idx)[kDepth]) {
@@ -143,7 +113,7 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
     for (int j = 0; j < kDepth; ++j) {
       uint32_t v = kBadBase;
       if (walked + j < count) {
-        const uint32_t base = row_base(T, s_base, ra, rr, c0, cl);
+        const uint32_t base = row_base<kStaged>(T, s_base, ra, rr, c0, cl);
         if (base != kBadBase) v = base + (uint32_t)cc;
       }
       idx[j] = v;
@@ -160,18 +130,20 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
   next_block(ia);
 #pragma unroll
   for (int j = 0; j < kDepth; ++j) qa[j] = qv[ia[j] == kBadBase ? safe : ia[j]];
-  uint32_t s0 = chunk_at(bs32, nchunks, tail), s1 = chunk_at(bs32, nchunks, tail + 1);
+  uint32_t st[kStage];
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) st[j] = chunk_at(bs32, nchunks, tail + j);
   bool stale = false;
 
   auto refill = [&]() {
     if (cnt < 32) {
       if (qn > 0) {
-        buf |= (uint64_t)q0 << (32 - cnt);
-        q0 = q1;
-        q1 = q2;
-        q2 = q3;
+        buf |= (uint64_t)qq[0] << (32 - cnt);
+#pragma unroll
+        for (int j = 0; j + 1 < kQueue; ++j) qq[j] = qq[j + 1];
         --qn;
       } else {
+        // Queue drained by ESC payloads: read the chunk straight from memory.
         const uint32_t ch = chunk_at(bs32, nchunks, tail);
         buf |= (uint64_t)ch << (32 - cnt);
         ++tail;
@@ -195,25 +167,28 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
       buf <<= nib;
       cnt -= (int)nib;
     }
-    if (idx != kBadBase) out[idx] = (uint16_t)sym;
+    // saddr store: the byte offset fits 32 bits (n*m < 2^31)
+    if (idx != kBadBase) *reinterpret_cast<uint16_t *>(outb + (idx << 1)) = (uint16_t)sym;
     refill();
   };
   auto block = [&](int32_t i0, uint32_t (&qc)[kDepth], uint32_t (&ic)[kDepth], uint32_t (&qnx)[kDepth],
                    uint32_t (&inx)[kDepth]) {
-    if (!stale && qn <= 2) {
-      q0 = (qn == 0) ? s0 : q0;
-      q1 = (qn == 0) ? s1 : (qn == 1) ? s0 : q1;
-      q2 = (qn == 1) ? s1 : (qn == 2) ? s0 : q2;
-      q3 = (qn == 2) ? s1 : q3;
-      qn += 2;
-      tail += 2;
+    // Append the chunks staged one block ago if they are current and fit.
+    if (!stale && qn <= kStage) {
+#pragma unroll
+      for (int j = 0; j < kQueue; ++j)
+#pragma unroll
+        for (int t = 0; t < kStage; ++t)
+          if (j == qn + t) qq[j] = st[t];
+      qn += kStage;
+      tail += kStage;
     }
     stale = false;
     next_block(inx);
 #pragma unroll
     for (int j = 0; j < kDepth; ++j) qnx[j] = qv[inx[j] == kBadBase ? safe : inx[j]];
-    s0 = chunk_at(bs32, nchunks, tail);
-    s1 = chunk_at(bs32, nchunks, tail + 1);
+#pragma unroll
+    for (int j = 0; j < kStage; ++j) st[j] = chunk_at(bs32, nchunks, tail + j);
     if (i0 + kDepth <= count) {
 #pragma unroll
       for (int j = 0; j < kDepth; ++j) decode_one(qc[j], ic[j]);
@@ -232,10 +207,88 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
   if (tail * 32u - (uint64_t)(cnt + 32 * qn) != pos_end) flag(status, MPS_STATUS_DESYNC);
 }
 
+// kSplit workgroups of kAwqBlock / kSplit work-items share a bucket: each
+// stages the bucket's tables and decodes its slice of the lanes (launches with
+// fewer buckets than CUs use several CUs per bucket).
+template <int kSplit>
+__global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T, uint32_t *status) {
+  __shared__ uint32_t lut[kLutEntries];
+  __shared__ uint32_t s_base[kRowSlots];
+  constexpr int kThreads = kAwqBlock / kSplit;
+  const int64_t b = blockIdx.x / kSplit;
+  const int tid = threadIdx.x;
+  const int lane = (int)(blockIdx.x % kSplit) * kThreads + tid;
+  // Bucket geometry (decode_huffman.cu:417-444, :528-545).
+  const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
+  const int32_t rows = rb - ra;
+  if (rows <= 0) return;
+  const bool by_scale = T.group_col_start != nullptr;
+  const int32_t c0 = by_scale ? 0 : T.bucket_col_start[b];
+  const int32_t cl = by_scale ? (int32_t)T.group_size : T.bucket_col_len[b];
+  if (cl <= 0 || ra < 0 || (int64_t)rb > T.num_row_indices ||
+      (!by_scale && (c0 < 0 || (int64_t)c0 + cl > T.m))) {
+    if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
+    return;
+  }
+  const int64_t total = (int64_t)rows * cl;
+  const int32_t k = (int32_t)T.k;
+  const int32_t k_eff = total < k ? (int32_t)total : k;
+
+  // Tables: entry (q << 11) | p = sym << 16 | nibble; a missing table (id -1)
+  // is all ESC entries, as the reference decodes it. The 16 table ids are
+  // bucket-uniform (scalar loads); every work-item then fills 32 entries, two
+  // per table, with all 64 global loads issued before the first LDS store
+  // (addresses of missing tables are clamped to table 0 and the entry selected
+  // afterwards), so the fill costs one memory round trip, not 32.
+  int32_t gid[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) gid[q] = T.bucket_table[b * 16 + q];
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if (gid[q] < -1 || gid[q] >= T.num_tables) flag(status, MPS_STATUS_BAD_TABLE);
+  }
+  const int64_t G = T.num_tables;
+  if (G <= 0) {
+    for (int i = tid; i < kLutEntries; i += kThreads) lut[i] = 15u;
+  } else for (int part = 0; part < kSplit; ++part) {  // kSplit rounds of 32 entries a work-item
+    uint32_t sy[32], ln[32];
+#pragma unroll
+    for (int it = 0; it < 32; ++it) {
+      const int i = (part * 32 + it) * kThreads + tid;
+      const int q = i >> kAwqL, p = i & (kAwqTable - 1);
+      const uint32_t g = (gid[q] >= 0 && gid[q] < G) ? (uint32_t)gid[q] : 0u;  // table 0 exists: G > 0
+      sy[it] = T.decode_syms[(size_t)g * kAwqTable + p];
+      ln[it] = T.decode_lens[(size_t)g * kAwqPacked + (p >> 1)];
+    }
+#pragma unroll
+    for (int it = 0; it < 32; ++it) {
+      const int i = (part * 32 + it) * kThreads + tid;
+      const int q = i >> kAwqL, p = i & (kAwqTable - 1);
+      const bool ok = gid[q] >= 0 && gid[q] < G;
+      lut[i] = ok ? (sy[it] << 16) | ((p & 1) ? (ln[it] >> 4) : (ln[it] & 15u)) : 15u;
+    }
+  }
+  const int32_t staged = rows < kRowSlots ? rows : kRowSlots;
+  for (int r = tid; r < staged; r += kThreads) {
+    const int64_t row = T.row_indices[ra + r];
+    const int64_t col = by_scale ? (int64_t)T.group_col_start[ra + r] : (int64_t)c0;
+    uint32_t base = kBadBase;
+    if (row >= 0 && row < T.n && col >= 0 && col + cl <= T.m) base = (uint32_t)(row * T.m + col);
+    else flag(status, MPS_STATUS_BAD_ROW);
+    s_base[r] = base;
+  }
+  __syncthreads();
+  if (lane >= k_eff) return;
+
+  if (rows <= kRowSlots) awq_lane<true>(T, lut, s_base, b, ra, c0, cl, total, k, k_eff, lane, status);
+  else awq_lane<false>(T, lut, s_base, b, ra, c0, cl, total, k, k_eff, lane, status);
+}
+
 int check_awq(const mps_awq_tensor *t) {
   if (!t) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor is NULL");
   if (t->n <= 0 || t->m <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "n,m must be > 0");
-  if (t->n * t->m >= ((int64_t)1 << 32) - 1) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor too large (n*m >= 2^32)");
+  if (t->n * t->m >= ((int64_t)1 << 31)) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor too large (n*m >= 2^31)");
   if (t->k <= 0 || t->k > kAwqBlock)
     return fail(MPS_ERR_INVALID_ARGUMENT, "bucket_thread_startbit_u32 has invalid k (must be 1..1024)");
   if (t->num_buckets < 0 || t->num_buckets >= ((int64_t)1 << 31))
@@ -271,8 +324,15 @@ int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream) 
   uint32_t *status = nullptr;
   rc = status_word(dev, &status);
   if (rc != MPS_OK) return rc;
-  hipLaunchKernelGGL(awq_decode_kernel, dim3((unsigned)tensor->num_buckets), dim3(kAwqBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), *tensor, status);
+  // Fewer buckets than CUs: split each bucket's lanes over 2 workgroups.
+  int cus = 0;
+  MPS_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int64_t B = tensor->num_buckets;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (B >= cus)
+    hipLaunchKernelGGL(awq_decode_kernel<1>, dim3((unsigned)B), dim3(kAwqBlock), 0, s, *tensor, status);
+  else
+    hipLaunchKernelGGL(awq_decode_kernel<2>, dim3((unsigned)(2 * B)), dim3(kAwqBlock / 2), 0, s, *tensor, status);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
