@@ -152,7 +152,7 @@ def run_awq(args, dev) -> int:
             tot_ms += ms
             per.append({"tensor": name, "shape": [n, m], "buckets": int(sc["bucket_table_i32"].shape[0]),
                         "tables": int(sc["decode_syms_u16"].shape[0]),
-                        "bits_per_elem": round(8 * sc["bitstream_u64"].numel() / (n * m), 3),
+                        "bitstream_bits_per_elem": round(64 * sc["bitstream_u64"].numel() / (n * m), 3),
                         "esc_keys": st["esc_keys"], "esc_collisions": st["esc_collisions"],
                         "bit_exact": exact[name],
                         "ms": round(ms, 4), "rw_gbs": round(alg / ms / 1e6, 1),
