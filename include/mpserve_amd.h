@@ -149,9 +149,9 @@ typedef struct mps_awq_tensor {
 /* Decode one AWQ int4 tensor: out[n,m] = BF16 rebuilt from int4 values + sidecar,
  * on `stream`. Replaces huffman_cpp::huffman_decode_awq_int4_bucket_entry
  * (group_col_start == NULL; reference kernel/decode_huffman.cu:877-1018 and
- * :378-475, bound at kernel/wrapper.cpp:342-386) and
+ * :378-475, bound at kernel/wrapper.cpp:324-369) and
  * ..._by_scale_entry (group_col_start != NULL; kernel/decode_huffman.cu:760-875
- * and :477-589, bound at kernel/wrapper.cpp:388-416). The shape/dtype checks
+ * and :477-589, bound at kernel/wrapper.cpp:371-416). The shape/dtype checks
  * of those entries are done by the caller. max_len must be 11. Columns of a
  * row bucket are walked as e % col_len, as the builder lays them out.
  * Asynchronous: returns after the launch. */
@@ -180,9 +180,9 @@ typedef struct mps_awq_encode_in {
  * reference builders, which run single-threaded on the host:
  *   by_scale = 0: huffman_cpp::huffman_build_awq_int4_bucket_decode_tables_entry
  *     (reference kernel/build_huffman.cu:1583-2126, bound as
- *     MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables at kernel/wrapper.cpp:275-306);
+ *     MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables at kernel/wrapper.cpp:258-288);
  *   by_scale = 1: ..._by_scale_entry (kernel/build_huffman.cu:1075-1580, bound as
- *     MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables_by_scale at kernel/wrapper.cpp:308-340).
+ *     MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables_by_scale at kernel/wrapper.cpp:290-321).
  * Same argument checks and messages. The result uses the FP8 handle's 17
  * slots: slots 0-13 in the reference's order of the row-bucket dict (slot 3 is
  * table_qv_u16, slot 7 bucket_table_i32 [B,16]); by scale, slot 5 holds

@@ -1,7 +1,7 @@
 """AWQ int4 + Huffman-sidecar ops of ``MPServe_cuda``, served by HIP kernels on MI355X.
 
 The reference binds two builders and two decoders for AWQ int4 weights
-(kernel/wrapper.cpp:275-416):
+(kernel/wrapper.cpp:258-416):
 
 * ``huffman_build_awq_int4_bucket_decode_tables`` (row buckets,
   build_huffman.cu:1583-2126) and ``huffman_decode_awq_int4_bucket``
@@ -26,7 +26,7 @@ import torch
 from . import _native
 from .mpserve_cuda import _check_cuda_contig, _maybe_check_status, _stream_handle
 
-# Dict keys in the reference's order (wrapper.cpp:286-301, :320-334) and the
+# Dict keys in the reference's order (wrapper.cpp:268-281, :301-313) and the
 # builder-handle slot each comes from.
 BUCKET_KEYS = (
     ("decode_syms_u16", 0, torch.uint16), ("decode_lens_u8", 1, torch.uint8), ("table_scale_u16", 2, torch.uint16),
@@ -128,7 +128,7 @@ def _build(bf16, int4, scales, max_len, threads, group_cap, by_scale: bool, with
 def huffman_build_awq_int4_bucket_decode_tables(bf16_params: torch.Tensor, int4_values_u8: torch.Tensor,
                                                 scales_u16: torch.Tensor, max_len: int = 11,
                                                 threads_per_block: int = 256) -> Dict[str, torch.Tensor]:
-    """Row-bucket AWQ int4 sidecar, 14 keys (build_huffman.cu:1583-2126, wrapper.cpp:275-306)."""
+    """Row-bucket AWQ int4 sidecar, 14 keys (build_huffman.cu:1583-2126, wrapper.cpp:258-288)."""
     return _build(bf16_params, int4_values_u8, scales_u16, int(max_len), int(threads_per_block), 1, False)
 
 
@@ -136,7 +136,7 @@ def huffman_build_awq_int4_bucket_decode_tables_by_scale(bf16_values: torch.Tens
                                                          scales_u16: torch.Tensor, max_len: int = 11,
                                                          threads: int = 256,
                                                          group_cap: int = 1024) -> Dict[str, torch.Tensor]:
-    """By-scale AWQ int4 sidecar, 13 keys (build_huffman.cu:1075-1580, wrapper.cpp:308-340)."""
+    """By-scale AWQ int4 sidecar, 13 keys (build_huffman.cu:1075-1580, wrapper.cpp:290-321)."""
     return _build(bf16_values, int4_values, scales_u16, int(max_len), int(threads), int(group_cap), True)
 
 

@@ -16,13 +16,15 @@
 // work-item. The bucket's 16 tables are expanded once into LDS as 32-bit
 // entries {sym:16 | nibble:4} indexed (qv << 11) | peek (128 KiB), and the
 // bucket's row (group) start offsets are staged next to them (32 KiB), so an
-// element costs one ds_read_b32 for its code and none for its address. The
-// bit supply is the FP8 generic lane's: a 64-bit MSB-aligned buffer topped up
-// to >= 32 bits after every element from a 4-chunk register queue, whose
-// loads (and the block's int4 bytes) are issued one block of kDepth elements
-// ahead. kDepth = 4 keeps a block's codes (<= 44 bits) within the two chunks
-// staged per block; ESC payloads can drain the queue, which then reads a chunk
-// straight from memory.
+// element costs one ds_read_b32 for its code and one for its row offset. The
+// table fill issues all of a work-item's global loads before its first LDS
+// store (one memory round trip per bucket). The bit supply is a 64-bit
+// MSB-aligned buffer topped up to >= 32 bits after every element from a
+// register queue of 2 * kStage 32-bit chunks; kStage chunks (the most a block
+// of kDepth = 8 codes can take without ESC) and the block's int4 bytes are
+// loaded one block ahead. ESC payloads can drain the queue, which then reads a
+// chunk straight from memory. A tensor with fewer buckets than CUs runs two
+// 512-work-item workgroups per bucket, each with its own copy of the tables.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>

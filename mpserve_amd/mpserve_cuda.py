@@ -232,7 +232,7 @@ for _name in ("init_cuda", "cleanup_cuda", "build_trie_AWQ", "build_trie", "quer
               "huffman_build_awq_decode_tables", "huffman_decode_awq_shared_table"):
     globals()[_name] = _not_in_scope(_name)
 
-# AWQ int4 bucket builders and decoders (wrapper.cpp:275-416).
+# AWQ int4 bucket builders and decoders (wrapper.cpp:258-416).
 from .awq import (huffman_build_awq_int4_bucket_decode_tables,  # noqa: E402
                   huffman_build_awq_int4_bucket_decode_tables_by_scale, huffman_decode_awq_int4_bucket,
                   huffman_decode_awq_int4_bucket_by_scale)

@@ -32,6 +32,18 @@ empty; see the Makefile):
 Parity unpinned (no reference run possible, no golden vectors exist): the
 exact choice among equal-cost length vectors is pinned only by the hand traces
 of the reference's merge order, not by a reference execution.
+
+The AWQ int4 bucket builders and decoders (``awq_huffman_oracle.c``,
+``awq_encode`` / ``awq_decode`` below) share package-merge with the FP8 oracle
+and are pinned in tests/test_awq_oracle.py:
+- round trips for both layouts, every scale mode, and k below and above the
+  column count;
+- numpy closed forms of the keys, ``bucket_table``, row order and group
+  order/chunking;
+- Kraft sums, LUT coverage and the single nibble-15 ESC entry;
+- brute-force scans of both ESC symbol rules;
+- the hand-out order of both ESC lists, (count asc, sym asc) for row buckets
+  against (count desc, sym asc) with ESC last by scale.
 """
 from __future__ import annotations
 
@@ -250,8 +262,8 @@ def awq_encode(bf16_bits: np.ndarray, int4_u8: np.ndarray, scales_u16: np.ndarra
     """AWQ int4 sidecar under the reference's dict keys.
 
     ``by_scale=False`` mirrors huffman_build_awq_int4_bucket_decode_tables_entry
-    (build_huffman.cu:1583-2126, 14 keys, wrapper.cpp:286-301); ``by_scale=True``
-    mirrors ..._by_scale_entry (build_huffman.cu:1075-1580, 13 keys, wrapper.cpp:320-334).
+    (build_huffman.cu:1583-2126, 14 keys, wrapper.cpp:268-281); ``by_scale=True``
+    mirrors ..._by_scale_entry (build_huffman.cu:1075-1580, 13 keys, wrapper.cpp:301-313).
     """
     bf = np.ascontiguousarray(bf16_bits, dtype=np.uint16)
     q = np.ascontiguousarray(int4_u8, dtype=np.uint8)

@@ -47,7 +47,7 @@ def test_out_of_scope_ops_raise_not_implemented():
 
 
 def test_awq_int4_op_signatures_match_reference():
-    """Argument names and defaults of wrapper.cpp:275-416."""
+    """Argument names and defaults of wrapper.cpp:258-416."""
     sig = inspect.signature
     p = sig(MPServe_cuda.huffman_build_awq_int4_bucket_decode_tables).parameters
     assert list(p)[:5] == ["bf16_params", "int4_values_u8", "scales_u16", "max_len", "threads_per_block"]
