@@ -153,3 +153,82 @@ def test_decode_argument_checks():
     bad[4] = d["bucket_table_i32"][:, :8].contiguous()
     with pytest.raises(ValueError, match=r"bucket_table_i32 must be int32 CUDA \[B,16\]"):
         MPServe_cuda.huffman_decode_awq_int4_bucket(*bad)
+
+
+def _tiny_sidecar(values, table_ids, rows, n, m):
+    """One row bucket, k = 1, every element coded through `table_ids` (all -1:
+    the reference decodes each element as ESC, 11 bits then 16 raw bits)."""
+    bits = []
+    for v in values:
+        bits += [0] * 11 + [(v >> (15 - i)) & 1 for i in range(16)]
+    bits += [0] * (-len(bits) % 64)
+    words = np.array([int("".join(map(str, bits[i:i + 64])), 2) for i in range(0, len(bits), 64)], dtype=np.uint64)
+    total = len(values)
+    return {
+        "bitstream_u64": words, "decode_syms_u16": np.zeros((1, 2048), np.uint16),
+        "decode_lens_u8": np.zeros((1, 1024), np.uint8),
+        "bucket_table_i32": np.array([table_ids], dtype=np.int32),
+        "bucket_col_start_i32": np.array([0], np.int32), "bucket_col_len_i32": np.array([m], np.int32),
+        "bucket_row_offsets_i32": np.array([0, len(rows)], np.int32), "row_indices_i32": np.array(rows, np.int32),
+        "bucket_thread_startbit_u32": np.array([[0, 27 * total]], np.uint32),
+        "bucket_bit_base_i64": np.array([0, 27 * total], np.int64),
+    }
+
+
+def _tiny_decode(sc, q, n, m, out=None):
+    t = {k: torch.from_numpy(v.view(np.int64) if v.dtype == np.uint64 else
+                             v.view(np.int16) if v.dtype == np.uint16 else
+                             v.view(np.int32) if v.dtype == np.uint32 else v).to(DEV) for k, v in sc.items()}
+    t["bitstream_u64"] = t["bitstream_u64"].view(torch.uint64)
+    t["decode_syms_u16"] = t["decode_syms_u16"].view(torch.uint16)
+    t["bucket_thread_startbit_u32"] = t["bucket_thread_startbit_u32"].view(torch.uint32)
+    o = MPServe_cuda.huffman_decode_awq_int4_bucket(
+        torch.from_numpy(q).to(DEV), t["bitstream_u64"], t["decode_syms_u16"], t["decode_lens_u8"],
+        t["bucket_table_i32"], t["bucket_col_start_i32"], t["bucket_col_len_i32"], t["bucket_row_offsets_i32"],
+        t["row_indices_i32"], t["bucket_thread_startbit_u32"], t["bucket_bit_base_i64"], n, m, 11, out=out)
+    torch.cuda.synchronize()
+    return o.view(torch.uint16).cpu().numpy()
+
+
+def test_missing_table_decodes_as_esc_like_the_reference():
+    """decode_huffman.cu:448-460: bucket_table -1 -> consume L bits, then 16 raw bits."""
+    vals = [0x3F80, 0xBF80, 0x0001, 0xFFFF, 0x1234, 0x8000]
+    n, m = 2, 3
+    sc = _tiny_sidecar(vals, [-1] * 16, [0, 1], n, m)
+    q = np.array([[0, 5, 15], [3, 8, 12]], np.uint8)
+    read_status(torch.device(DEV))
+    out = _tiny_decode(sc, q, n, m)
+    assert out.reshape(-1).tolist() == vals
+    assert np.array_equal(out, oracle.awq_decode(sc, q, n, m))
+    assert read_status(torch.device(DEV)) == 0
+
+
+def test_integrity_flags_bad_row_and_bad_table():
+    from mpserve_amd._native import MPS_STATUS_BAD_ROW, MPS_STATUS_BAD_TABLE
+
+    vals = [0x3F80, 0xBF80, 0x0001]
+    q = np.zeros((2, 3), np.uint8)
+    read_status(torch.device(DEV))
+    sc = _tiny_sidecar(vals, [-1] * 16, [7], 2, 3)  # row 7 of a 2-row tensor
+    _tiny_decode(sc, q, 2, 3, out=torch.zeros((2, 3), dtype=torch.bfloat16, device=DEV))
+    assert read_status(torch.device(DEV)) & MPS_STATUS_BAD_ROW
+    sc = _tiny_sidecar(vals, [5] + [-1] * 15, [0], 2, 3)  # table id 5 of a 1-table sidecar
+    _tiny_decode(sc, q, 2, 3)
+    assert read_status(torch.device(DEV)) & MPS_STATUS_BAD_TABLE
+
+
+def test_no_buckets_is_a_no_op():
+    bf16, q, sc = _inputs("empty", 8, 64, None)
+    d = {k: v.to(DEV) for k, v in _build(bf16, q, sc, 64, False, 1024).items()}
+    empty = {k: v[:0] if k in ("bucket_table_i32", "bucket_col_start_i32", "bucket_col_len_i32",
+                               "bucket_thread_startbit_u32") else v for k, v in d.items()}
+    empty["bucket_row_offsets_i32"] = d["bucket_row_offsets_i32"][:1]
+    empty["bucket_bit_base_i64"] = d["bucket_bit_base_i64"][:1]
+    out = torch.full((8, 64), 7.0, dtype=torch.bfloat16, device=DEV)
+    MPServe_cuda.huffman_decode_awq_int4_bucket(
+        q.to(DEV), empty["bitstream_u64"], empty["decode_syms_u16"], empty["decode_lens_u8"],
+        empty["bucket_table_i32"], empty["bucket_col_start_i32"], empty["bucket_col_len_i32"],
+        empty["bucket_row_offsets_i32"], empty["row_indices_i32"], empty["bucket_thread_startbit_u32"],
+        empty["bucket_bit_base_i64"], 8, 64, 11, out=out)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
