@@ -159,9 +159,29 @@ def run_awq(args, dev) -> int:
                         "pct_hbm_peak_rw": round(100 * alg / ms / 1e6 / HBM_PEAK_GBS, 2)})
             log(f"{layout} {name} {n}x{m}: {ms:.4f} ms, {per[-1]['pct_hbm_peak_rw']}% of HBM peak")
         elems = sum(n * m for _, n, m, *_ in items)
+        # the same layer through one AwqDecodePlan launch (every bucket of the 7 tensors)
+        plan = awq.AwqDecodePlan([(w.int4_u8, sc, out) for _, _, _, w, sc, _, out, _ in items])
+        for _ in range(max(1, args.warmup // 10)):
+            plan.decode(stream)
+        torch.cuda.synchronize()
+        for name, _, _, w, _, _, out, st in items:
+            if not torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)) and st["esc_collisions"] == 0:
+                raise RuntimeError(f"AWQ plan decode ({layout}) of {name} is not bit-exact")
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        for s0, e0 in ev:
+            s0.record(stream)
+            plan.decode(stream)
+            e0.record(stream)
+        torch.cuda.synchronize()
+        plan_ms = sum(s0.elapsed_time(e0) for s0, e0 in ev) / args.steps
+        log(f"{layout} layer: {tot_ms:.4f} ms as 7 op launches, {plan_ms:.4f} ms as one plan launch "
+            f"({plan.info()['work_items']} buckets)")
         results[layout] = {"layer_decode_ms": round(tot_ms, 4), "out_gbs": round(2 * elems / tot_ms / 1e6, 1),
                            "algorithmic_bytes": int(tot_alg), "achieved_gbs": round(tot_alg / tot_ms / 1e6, 1),
-                           "per_tensor": per}
+                           "plan_layer_ms": round(plan_ms, 4), "plan_out_gbs": round(2 * elems / plan_ms / 1e6, 1),
+                           "plan_achieved_gbs": round(tot_alg / plan_ms / 1e6, 1),
+                           "plan_work_items": plan.info()["work_items"], "per_tensor": per}
+        plan.close()
     cpu = None
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -184,15 +204,15 @@ def run_awq(args, dev) -> int:
                          f"{elapsed:.2f} s"}
     head = results["by_scale"]
     result = {
-        "metric": "AWQ int4 -> BF16 decompress GB/s (out); one Llama-3-8B layer",
-        "value": head["out_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": head["layer_decode_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "metric": "AWQ int4 -> BF16 decompress GB/s (out); one Llama-3-8B layer in one plan launch",
+        "value": head["plan_out_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head["plan_layer_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "u16", "data": "synthetic: seeded N(0,0.02^2) BF16, AWQ-style int4 (group 128), sidecar built on "
                                 "the GPU",
         "config": {"workload": WORKLOADS["awq8b"], "layouts": results},
-        "roofline": {"bound": "hbm", "achieved": head["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes": head["algorithmic_bytes"], "kernel_ms": head["layer_decode_ms"]},
+        "roofline": {"bound": "hbm", "achieved": head["plan_achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["plan_achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": head["algorithmic_bytes"], "kernel_ms": head["plan_layer_ms"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

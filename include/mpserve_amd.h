@@ -157,6 +157,20 @@ typedef struct mps_awq_tensor {
  * Asynchronous: returns after the launch. */
 int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream);
 
+/* Batched AWQ decode plan: one launch decodes every bucket of many AWQ int4
+ * tensors (either layout, mixed), largest buckets first. Reads each tensor's
+ * bucket row offsets (and column lengths) once at create time (synchronously)
+ * and copies the descriptors to device memory it owns; the pointed-to tensors
+ * must stay alive while the plan is used, and a tensor whose bucket metadata
+ * is rewritten needs a new plan. Decodes are asynchronous on `stream`.
+ * No counterpart in the reference, which launches once per tensor
+ * (kernel/decode_huffman.cu:857, :998). */
+typedef struct mps_awq_plan mps_awq_plan;
+int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, mps_awq_plan **plan_out);
+int mps_awq_plan_decode(mps_awq_plan *plan, void *stream);
+int mps_awq_plan_info(const mps_awq_plan *plan, int64_t *work_items);
+int mps_awq_plan_destroy(mps_awq_plan *plan);
+
 /* Inputs of the AWQ int4 sidecar builders, all device pointers: BF16 bit
  * patterns and int4 values (one per byte, low nibble) of an [n, m] weight, and
  * the u16 (BF16 bit) scales: one value, [n] (scale_ndim 1) or block-wise

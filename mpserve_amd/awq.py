@@ -24,7 +24,7 @@ from typing import Dict
 import torch
 
 from . import _native
-from .mpserve_cuda import _check_cuda_contig, _maybe_check_status, _stream_handle
+from ._common import _check_cuda_contig, _maybe_check_status, _stream_handle
 
 # Dict keys in the reference's order (wrapper.cpp:268-281, :301-313) and the
 # builder-handle slot each comes from.
@@ -294,3 +294,112 @@ def huffman_decode_awq_int4_bucket_by_scale(int4_values_u8: torch.Tensor, bitstr
     return _launch(int4_values_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32, None, None,
                    bucket_group_offsets_i32, group_rows_i32, group_col_start_i32, group_size,
                    bucket_thread_startbit_u32, bucket_bit_base_i64, n, m, max_len, out)
+
+
+def _sidecar_descriptor(int4: torch.Tensor, sc, out: torch.Tensor) -> "_native.MpsAwqTensor":
+    """Descriptor of one tensor for a plan: either layout's dict (as the
+    builders return it, on the int4 tensor's device) and a contiguous BF16 out."""
+    by_scale = "bucket_group_offsets_i32" in sc
+    n, m = int(int4.shape[0]), int(int4.shape[1])
+    dev = int4.device
+    names = ["bitstream_u64", "decode_syms_u16", "decode_lens_u8", "bucket_table_i32",
+             "bucket_thread_startbit_u32", "bucket_bit_base_i64"]
+    names += (["bucket_group_offsets_i32", "group_rows_i32", "group_col_start_i32"] if by_scale else
+              ["bucket_col_start_i32", "bucket_col_len_i32", "bucket_row_offsets_i32", "row_indices_i32"])
+    _check_cuda_contig(int4, "int4_values_u8", dev)
+    for key in names:
+        _check_cuda_contig(sc[key], key, dev)
+    if int4.dtype != torch.uint8 or int4.dim() != 2:
+        raise ValueError("int4_values_u8 must be uint8 2D CUDA [n,m]")
+    if sc["decode_syms_u16"].shape[1:] != (2048,) or sc["decode_lens_u8"].shape[1:] != (1024,) \
+            or sc["bucket_table_i32"].dim() != 2 or sc["bucket_table_i32"].shape[1] != 16:
+        raise ValueError("not an AWQ int4 sidecar with max_len 11")
+    B = sc["bucket_table_i32"].shape[0]
+    offs = sc["bucket_group_offsets_i32" if by_scale else "bucket_row_offsets_i32"]
+    if offs.numel() != B + 1 or sc["bucket_thread_startbit_u32"].shape[0] != B or \
+            sc["bucket_bit_base_i64"].numel() != B + 1:
+        raise ValueError("inconsistent bucket counts in the sidecar")
+    if out.dtype != torch.bfloat16 or out.device != dev or not out.is_contiguous() or out.numel() != n * m:
+        raise ValueError("out must be a contiguous bfloat16 tensor of n*m elements on the int4 device")
+    if n * m >= (1 << 31):
+        raise ValueError("tensor too large for the AWQ decode kernel (n*m >= 2^31)")
+    d = _native.MpsAwqTensor()
+    d.int4 = int4.data_ptr()
+    d.bitstream, d.bitstream_words = sc["bitstream_u64"].data_ptr(), sc["bitstream_u64"].numel()
+    d.decode_syms, d.decode_lens = sc["decode_syms_u16"].data_ptr(), sc["decode_lens_u8"].data_ptr()
+    d.num_tables = sc["decode_syms_u16"].shape[0]
+    d.bucket_table = sc["bucket_table_i32"].data_ptr()
+    if by_scale:
+        d.bucket_row_offsets = sc["bucket_group_offsets_i32"].data_ptr()
+        d.row_indices, d.num_row_indices = sc["group_rows_i32"].data_ptr(), sc["group_rows_i32"].numel()
+        if sc["group_col_start_i32"].numel() != sc["group_rows_i32"].numel():
+            raise ValueError("group_rows_i32 and group_col_start_i32 length must match")
+        d.group_col_start = sc["group_col_start_i32"].data_ptr() if B else None
+        d.group_size = int(sc["shape_nmkg_i64"][3])
+    else:
+        if sc["bucket_col_start_i32"].numel() != B or sc["bucket_col_len_i32"].numel() != B:
+            raise ValueError("inconsistent bucket counts in the sidecar")
+        d.bucket_col_start, d.bucket_col_len = sc["bucket_col_start_i32"].data_ptr(), sc["bucket_col_len_i32"].data_ptr()
+        d.bucket_row_offsets = sc["bucket_row_offsets_i32"].data_ptr()
+        d.row_indices, d.num_row_indices = sc["row_indices_i32"].data_ptr(), sc["row_indices_i32"].numel()
+    d.bucket_thread_startbit, d.bucket_bit_base = (sc["bucket_thread_startbit_u32"].data_ptr(),
+                                                   sc["bucket_bit_base_i64"].data_ptr())
+    d.num_buckets, d.k = B, sc["bucket_thread_startbit_u32"].shape[1] - 1
+    d.n, d.m, d.out = n, m, out.data_ptr()
+    return d
+
+
+class AwqDecodePlan:
+    """Decode a fixed list of AWQ int4 tensors (either sidecar layout) in one launch.
+
+    ``items``: (int4_u8 [n, m] uint8, sidecar dict as the AWQ builders return it,
+    out contiguous bfloat16 of n*m elements), all on one device. The reference
+    launches once per tensor (decode_huffman.cu:857, :998); a plan launches one
+    workgroup per bucket of every tensor, largest buckets first. The plan keeps
+    references to every tensor it points at.
+    """
+
+    def __init__(self, items):
+        self._keep = []
+        descs = []
+        self.device = None
+        for int4, sc, out in items:
+            if self.device is None:
+                self.device = int4.device
+            elif int4.device != self.device:
+                raise ValueError("all tensors of an AwqDecodePlan must be on one device")
+            descs.append(_sidecar_descriptor(int4, sc, out))
+            self._keep.append((int4, sc, out))
+        self.outputs = [o for _, _, o in self._keep]
+        arr = (_native.MpsAwqTensor * max(1, len(descs)))(*descs)
+        self._plan = ctypes.c_void_p()
+        if self.device is not None:
+            with torch.cuda.device(self.device):
+                _native.check(_native.lib().mps_awq_plan_create(arr, len(descs), ctypes.byref(self._plan)))
+
+    def decode(self, stream: torch.cuda.Stream | None = None):
+        """Enqueue the decode on ``stream`` (default: the current stream); returns the outputs."""
+        if self.device is None:
+            return self.outputs
+        h = stream.cuda_stream if stream is not None else _stream_handle(self.device)
+        with torch.cuda.device(self.device):
+            _native.check(_native.lib().mps_awq_plan_decode(self._plan, ctypes.c_void_p(h)))
+        return self.outputs
+
+    def info(self) -> Dict[str, int]:
+        """Work items (buckets) of a launch."""
+        wi = ctypes.c_int64(0)
+        if self._plan:
+            _native.check(_native.lib().mps_awq_plan_info(self._plan, ctypes.byref(wi)))
+        return {"work_items": int(wi.value)}
+
+    def close(self) -> None:
+        if getattr(self, "_plan", None):
+            _native.lib().mps_awq_plan_destroy(self._plan)
+            self._plan = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -27,7 +27,11 @@
 // 512-work-item workgroups per bucket, each with its own copy of the tables.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <new>
+#include <utility>
+#include <vector>
 
 #include "mps_common.h"
 
@@ -213,13 +217,11 @@ __device__ __forceinline__ void awq_lane(const mps_awq_tensor &T, const uint32_t
 // stages the bucket's tables and decodes its slice of the lanes (launches with
 // fewer buckets than CUs use several CUs per bucket).
 template <int kSplit>
-__global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T, uint32_t *status) {
-  __shared__ uint32_t lut[kLutEntries];
-  __shared__ uint32_t s_base[kRowSlots];
+__device__ __forceinline__ void awq_bucket(const mps_awq_tensor &T, int64_t b, int part, uint32_t *__restrict__ lut,
+                                           uint32_t *__restrict__ s_base, uint32_t *status) {
   constexpr int kThreads = kAwqBlock / kSplit;
-  const int64_t b = blockIdx.x / kSplit;
   const int tid = threadIdx.x;
-  const int lane = (int)(blockIdx.x % kSplit) * kThreads + tid;
+  const int lane = part * kThreads + tid;
   // Bucket geometry (decode_huffman.cu:417-444, :528-545).
   const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
   const int32_t rows = rb - ra;
@@ -287,6 +289,24 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
   else awq_lane<false>(T, lut, s_base, b, ra, c0, cl, total, k, k_eff, lane, status);
 }
 
+template <int kSplit>
+__global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T, uint32_t *status) {
+  __shared__ uint32_t lut[kLutEntries];
+  __shared__ uint32_t s_base[kRowSlots];
+  awq_bucket<kSplit>(T, blockIdx.x / kSplit, (int)(blockIdx.x % kSplit), lut, s_base, status);
+}
+
+// Plan launch: workgroup i decodes bucket work[i].y of tensor work[i].x (the
+// work list holds every bucket of every tensor of the plan, largest first).
+__global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
+                                                             const int2 *__restrict__ work, uint32_t *status) {
+  __shared__ uint32_t lut[kLutEntries];
+  __shared__ uint32_t s_base[kRowSlots];
+  const int2 w = work[blockIdx.x];
+  const mps_awq_tensor T = tensors[w.x];
+  awq_bucket<1>(T, w.y, 0, lut, s_base, status);
+}
+
 int check_awq(const mps_awq_tensor *t) {
   if (!t) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor is NULL");
   if (t->n <= 0 || t->m <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "n,m must be > 0");
@@ -313,6 +333,13 @@ int check_awq(const mps_awq_tensor *t) {
 
 using namespace mps;
 
+struct mps_awq_plan {
+  int device = 0;
+  int64_t count = 0, nwork = 0;
+  mps_awq_tensor *d_tensors = nullptr;
+  int2 *d_work = nullptr;
+};
+
 extern "C" {
 
 int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream) {
@@ -336,6 +363,85 @@ int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream) 
   else
     hipLaunchKernelGGL(awq_decode_kernel<2>, dim3((unsigned)(2 * B)), dim3(kAwqBlock / 2), 0, s, *tensor, status);
   MPS_HIP_CHECK(hipGetLastError());
+  return MPS_OK;
+}
+
+int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, mps_awq_plan **plan_out) {
+  last_error().clear();
+  if (!plan_out) return fail(MPS_ERR_INVALID_ARGUMENT, "plan_out is NULL");
+  *plan_out = nullptr;
+  if (count < 0 || count >= ((int64_t)1 << 31) || (count > 0 && !tensors))
+    return fail(MPS_ERR_INVALID_ARGUMENT, "invalid tensor list");
+  // Every bucket of every tensor, ordered by elements (largest first), so the
+  // launch's last workgroups are its smallest.
+  std::vector<std::pair<int64_t, int2>> items;
+  std::vector<int32_t> roff, clen;
+  for (int64_t i = 0; i < count; ++i) {
+    const mps_awq_tensor &T = tensors[i];
+    int rc = check_awq(&T);
+    if (rc != MPS_OK) return rc;
+    const int64_t B = T.num_buckets;
+    if (B == 0) continue;
+    roff.resize((size_t)B + 1);
+    MPS_HIP_CHECK(hipMemcpy(roff.data(), T.bucket_row_offsets, sizeof(int32_t) * (B + 1), hipMemcpyDefault));
+    if (!T.group_col_start) {
+      clen.resize((size_t)B);
+      MPS_HIP_CHECK(hipMemcpy(clen.data(), T.bucket_col_len, sizeof(int32_t) * B, hipMemcpyDefault));
+    }
+    for (int64_t b = 0; b < B; ++b) {
+      const int64_t cols = T.group_col_start ? T.group_size : (int64_t)clen[(size_t)b];
+      const int64_t elems = std::max<int64_t>(0, (int64_t)roff[(size_t)b + 1] - roff[(size_t)b]) * std::max<int64_t>(0, cols);
+      items.push_back({elems, make_int2((int)i, (int)b)});
+    }
+  }
+  std::stable_sort(items.begin(), items.end(),
+                   [](const std::pair<int64_t, int2> &x, const std::pair<int64_t, int2> &y) { return x.first > y.first; });
+  auto plan = new (std::nothrow) mps_awq_plan();
+  if (!plan) return fail(MPS_ERR_NO_MEMORY, "out of memory");
+  MPS_HIP_CHECK(hipGetDevice(&plan->device));
+  plan->count = count;
+  plan->nwork = (int64_t)items.size();
+  std::vector<int2> work(items.size());
+  for (size_t j = 0; j < items.size(); ++j) work[j] = items[j].second;
+  hipError_t e = hipSuccess;
+  if (count > 0) e = hipMalloc(&plan->d_tensors, sizeof(mps_awq_tensor) * count);
+  if (e == hipSuccess && count > 0)
+    e = hipMemcpy(plan->d_tensors, tensors, sizeof(mps_awq_tensor) * count, hipMemcpyHostToDevice);
+  if (e == hipSuccess && !work.empty()) e = hipMalloc(&plan->d_work, sizeof(int2) * work.size());
+  if (e == hipSuccess && !work.empty())
+    e = hipMemcpy(plan->d_work, work.data(), sizeof(int2) * work.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    mps_awq_plan_destroy(plan);
+    return hip_fail(e, "mps_awq_plan_create");
+  }
+  *plan_out = plan;
+  return MPS_OK;
+}
+
+int mps_awq_plan_decode(mps_awq_plan *plan, void *stream) {
+  last_error().clear();
+  if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (plan->nwork == 0) return MPS_OK;
+  uint32_t *status = nullptr;
+  int rc = status_word(plan->device, &status);
+  if (rc != MPS_OK) return rc;
+  hipLaunchKernelGGL(awq_decode_plan, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
+                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, status);
+  MPS_HIP_CHECK(hipGetLastError());
+  return MPS_OK;
+}
+
+int mps_awq_plan_info(const mps_awq_plan *plan, int64_t *work_items) {
+  if (!plan || !work_items) return fail(MPS_ERR_INVALID_ARGUMENT, "NULL argument");
+  *work_items = plan->nwork;
+  return MPS_OK;
+}
+
+int mps_awq_plan_destroy(mps_awq_plan *plan) {
+  if (!plan) return MPS_OK;
+  if (plan->d_tensors) (void)hipFree(plan->d_tensors);
+  if (plan->d_work) (void)hipFree(plan->d_work);
+  delete plan;
   return MPS_OK;
 }
 

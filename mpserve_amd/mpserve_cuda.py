@@ -17,6 +17,7 @@ from typing import Dict
 import torch
 
 from . import _native
+from ._common import _check_cuda_contig, _maybe_check_status, _stream_handle, read_status  # noqa: F401
 
 __all__ = [
     "huffman_build_fp8_decode_tables",
@@ -33,22 +34,6 @@ SIDECAR_KEYS = (
     "bucket_bit_base_i64", "bitstream_u64", "shape_nmk_i64", "bucket_U_i32",
     "bucket_unique_gid_i32", "bucket_fp8_uidx_i16",
 )
-
-
-def _stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
-
-
-def _check_cuda_contig(t: torch.Tensor, name: str, device: torch.device | None) -> None:
-    # decode_huffman.cu:59-63
-    if t is None:
-        raise ValueError(f"{name} must be defined")
-    if not t.is_cuda:
-        raise ValueError(f"{name} must be a CUDA tensor")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
-    if device is not None and t.device != device:
-        raise ValueError(f"{name} must be on {device}, got {t.device}")
 
 
 def cuda_clock_rate_khz() -> int:
@@ -151,23 +136,6 @@ def validate_decode_args(fp8_params_u8, bitstream_u64, decode_syms_u16, decode_l
     k = bucket_thread_startbit_u32.size(1) - 1
     if k <= 0 or k > 1024:
         raise ValueError("bucket_thread_startbit_u32 has invalid k (must be 1..1024)")
-
-
-def read_status(device: torch.device | None = None) -> int:
-    """MPS_STATUS_* flags recorded by decodes on ``device`` since the last read (synchronises)."""
-    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
-    v = ctypes.c_uint32(0)
-    _native.check(_native.lib().mps_fp8_read_status(device.index or 0, ctypes.c_void_p(_stream_handle(device)),
-                                                    ctypes.byref(v)))
-    return int(v.value)
-
-
-def _maybe_check_status(device: torch.device) -> None:
-    if os.environ.get("MPSERVE_DECODE_CHECK", "0") == "1":
-        st = read_status(device)
-        if st:
-            raise RuntimeError(f"huffman_decode_fp8: sidecar integrity flags 0x{st:x} "
-                               "(1=bucket range, 2=row index, 4=table id, 8=lane bit desync)")
 
 
 def huffman_decode_fp8(fp8_params_u8: torch.Tensor, bitstream_u64: torch.Tensor, decode_syms_u16: torch.Tensor,

@@ -232,3 +232,28 @@ def test_no_buckets_is_a_no_op():
         empty["bucket_bit_base_i64"], 8, 64, 11, out=out)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+def test_plan_decodes_mixed_layouts_in_one_launch():
+    """AwqDecodePlan: every bucket of four tensors (both layouts, k 256 and 1024) in one launch."""
+    print("[awq] plan over mixed layouts", flush=True)
+    items, srcs = [], []
+    for j, (n, m, group, by_scale) in enumerate([(256, 512, 128, True), (128, 1024, None, False),
+                                                 (64, 256, 64, False), (512, 256, 128, True)]):
+        w = make_awq_weight(n, m, group, seed=500 + j, device=DEV)
+        sc = _build(w.bf16, w.int4_u8, w.scale_u16, 1024 if j % 2 else 256, by_scale, 16)
+        items.append((w.int4_u8, sc, torch.empty((n, m), dtype=torch.bfloat16, device=DEV)))
+        srcs.append(w.bf16)
+    plan = awq.AwqDecodePlan(items)
+    assert plan.info()["work_items"] == sum(sc["bucket_table_i32"].shape[0] for _, sc, _ in items)
+    read_status(torch.device(DEV))
+    for _ in range(2):  # replays give the same outputs
+        for o in plan.outputs:
+            o.zero_()
+        plan.decode()
+        torch.cuda.synchronize()
+        for o, s in zip(plan.outputs, srcs):
+            assert torch.equal(o.view(torch.uint16), s.view(torch.uint16))
+    assert read_status(torch.device(DEV)) == 0
+    plan.close()
+    assert awq.AwqDecodePlan([]).decode() == []
