@@ -20,9 +20,9 @@
 // table fill issues all of a work-item's global loads before its first LDS
 // store (one memory round trip per bucket). The bit supply is a 64-bit
 // MSB-aligned buffer topped up to >= 32 bits after every element from a
-// register queue of 2 * kStage 32-bit chunks; kStage chunks (the most a block
-// of kDepth = 8 codes can take without ESC) and the block's int4 bytes are
-// loaded one block ahead. ESC payloads can drain the queue, which then reads a
+// register queue of 8 32-bit chunks; an aligned quad of 4 chunks (more than a
+// block of kDepth = 8 codes can take without ESC) and the block's int4 bytes
+// are loaded one block ahead, one 16-byte request per quad. ESC payloads can drain the queue, which then reads a
 // chunk straight from memory. A tensor with fewer buckets than CUs runs two
 // 512-work-item workgroups per bucket, each with its own copy of the tables.
 #include <hip/hip_runtime.h>
@@ -46,14 +46,15 @@ constexpr int kLutEntries = 16 * kAwqTable;
 constexpr int kRowSlots = 8192;           // row (group) start offsets staged in LDS
 constexpr uint32_t kBadBase = 0xFFFFFFFFu;
 // Elements per block, and the chunk queue: a block of kDepth codes without
-// ESC takes at most kStage 32-bit chunks from the queue, kStage chunks are
-// staged (loaded) one block ahead, and the queue holds 2 * kStage.
+// ESC takes at most 3 32-bit chunks from the queue; a quad of kStage chunks is
+// staged (loaded) one block ahead, and the queue holds kQueue.
 #ifndef MPS_AWQ_DEPTH
 #define MPS_AWQ_DEPTH 8
 #endif
 constexpr int kDepth = MPS_AWQ_DEPTH;
-constexpr int kStage = (kDepth * kAwqL + 31) / 32;
-constexpr int kQueue = 2 * kStage;
+constexpr int kStage = 4;   // chunks staged a block: one 16-byte aligned quad
+constexpr int kQueue = 8;
+static_assert((kDepth * kAwqL + 31) / 32 <= kQueue - kStage, "a block's codes must fit the queue after an append");
 
 __device__ __forceinline__ void flag(uint32_t *status, unsigned int f) { atomicOr(status, f); }
 
@@ -98,11 +99,13 @@ __device__ __forceinline__ void awq_lane(const mps_awq_tensor &T, const uint32_t
   const int skip = (int)(pos0 & 31u);
   uint64_t buf = (((uint64_t)chunk_at(bs32, nchunks, cb) << 32) | chunk_at(bs32, nchunks, cb + 1)) << skip;
   int cnt = 64 - skip;
+  // The queue starts with the chunks up to the next multiple of 4, so that
+  // every later stage is one aligned quad.
   uint32_t qq[kQueue];
 #pragma unroll
-  for (int j = 0; j < kQueue; ++j) qq[j] = chunk_at(bs32, nchunks, cb + 2 + j);
-  int qn = kQueue;
-  uint64_t tail = cb + 2 + kQueue;  // index of the first chunk not yet in buf/queue
+  for (int j = 0; j < kQueue; ++j) qq[j] = j < 3 ? chunk_at(bs32, nchunks, cb + 2 + j) : 0u;
+  int qn = (int)((4u - ((cb + 2) & 3u)) & 3u);
+  uint64_t tail = cb + 2 + qn;  // index of the first chunk not yet in buf/queue
 
   // Element walk e = tid + i*k_eff -> (rr, cc) = (e / cl, e % cl), incrementally.
   int32_t rr = lane / cl;
@@ -136,9 +139,23 @@ __device__ __forceinline__ void awq_lane(const mps_awq_tensor &T, const uint32_t
   next_block(ia);
 #pragma unroll
   for (int j = 0; j < kDepth; ++j) qa[j] = qv[ia[j] == kBadBase ? safe : ia[j]];
-  uint32_t st[kStage];
+  // Chunks tail .. tail+3: one 16-byte load when the quad is aligned and whole
+  // (u32 words 4j .. 4j+3 hold chunks 4j+1, 4j, 4j+3, 4j+2), else four loads.
+  const bool aligned16 = (reinterpret_cast<uintptr_t>(bs32) & 15u) == 0;
+  auto stage = [&](uint32_t (&st)[kStage]) {
+    if (aligned16 && (tail & 3u) == 0 && tail + 4 <= nchunks) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(bs32 + tail);
+      st[0] = v.y;
+      st[1] = v.x;
+      st[2] = v.w;
+      st[3] = v.z;
+    } else {
 #pragma unroll
-  for (int j = 0; j < kStage; ++j) st[j] = chunk_at(bs32, nchunks, tail + j);
+      for (int j = 0; j < kStage; ++j) st[j] = chunk_at(bs32, nchunks, tail + j);
+    }
+  };
+  uint32_t st[kStage];
+  stage(st);
   bool stale = false;
 
   auto refill = [&]() {
@@ -180,7 +197,7 @@ __device__ __forceinline__ void awq_lane(const mps_awq_tensor &T, const uint32_t
   auto block = [&](int32_t i0, uint32_t (&qc)[kDepth], uint32_t (&ic)[kDepth], uint32_t (&qnx)[kDepth],
                    uint32_t (&inx)[kDepth]) {
     // Append the chunks staged one block ago if they are current and fit.
-    if (!stale && qn <= kStage) {
+    if (!stale && qn <= kQueue - kStage) {
 #pragma unroll
       for (int j = 0; j < kQueue; ++j)
 #pragma unroll
@@ -193,8 +210,7 @@ __device__ __forceinline__ void awq_lane(const mps_awq_tensor &T, const uint32_t
     next_block(inx);
 #pragma unroll
     for (int j = 0; j < kDepth; ++j) qnx[j] = qv[inx[j] == kBadBase ? safe : inx[j]];
-#pragma unroll
-    for (int j = 0; j < kStage; ++j) st[j] = chunk_at(bs32, nchunks, tail + j);
+    stage(st);
     if (i0 + kDepth <= count) {
 #pragma unroll
       for (int j = 0; j < kDepth; ++j) decode_one(qc[j], ic[j]);
