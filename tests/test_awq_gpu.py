@@ -257,3 +257,28 @@ def test_plan_decodes_mixed_layouts_in_one_launch():
     assert read_status(torch.device(DEV)) == 0
     plan.close()
     assert awq.AwqDecodePlan([]).decode() == []
+
+
+def test_truncated_bitstream_and_wild_start_bits_flag_desync_without_faults():
+    """A bitstream cut short, or start bits past its end, must only raise the
+    desync flag: every read stays inside the bitstream and every store inside out."""
+    from mpserve_amd._native import MPS_STATUS_DESYNC
+
+    bf16, q, sc = _inputs("trunc", 64, 512, 128)
+    d = {k: v.to(DEV) for k, v in _build(bf16, q, sc, 256, True, 16).items()}
+    for what in ("truncate", "wild_start"):
+        t = dict(d)
+        if what == "truncate":
+            t["bitstream_u64"] = d["bitstream_u64"][: d["bitstream_u64"].numel() // 2].clone()
+        else:
+            sb = d["bucket_thread_startbit_u32"].clone()
+            sb.view(torch.int32)[:, 5] = -16  # 0xFFFFFFF0: far past the end
+            t["bucket_thread_startbit_u32"] = sb
+        read_status(torch.device(DEV))
+        out = MPServe_cuda.huffman_decode_awq_int4_bucket_by_scale(
+            q.to(DEV), t["bitstream_u64"], t["decode_syms_u16"], t["decode_lens_u8"], t["bucket_table_i32"],
+            t["bucket_group_offsets_i32"], t["group_rows_i32"], t["group_col_start_i32"],
+            t["bucket_thread_startbit_u32"], t["bucket_bit_base_i64"], 64, 512, 11, 128)
+        torch.cuda.synchronize()
+        assert out.shape == (64, 512)
+        assert read_status(torch.device(DEV)) & MPS_STATUS_DESYNC, what

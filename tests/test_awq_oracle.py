@@ -8,10 +8,12 @@ is pinned by what the mathematics or the reference's own structure fixes:
 * tables and buckets: closed forms recomputed with numpy (np.unique of the
   (scale, qv) keys, the row / group order and chunking);
 * code books: Kraft sums, LUT coverage, the ESC entry (nibble 15, length L,
-  one entry); the row-bucket builder's lengths are monotone in frequency
-  (heavier symbol never longer), while the by-scale builder's ESC tables apply
-  sorted-position lengths to a (count desc) list, so there the heavier symbol
-  is never SHORTER - a mistake in either ordering fails one of these;
+  one entry); with ESC the 2^L codes all have length L, so the LUT lists the
+  symbols in hand-out order, which differs between the builders: (count asc,
+  sym asc) with ESC placed by its weight for row buckets, (count desc, sym asc)
+  with ESC last by scale - a mistake in either ordering fails that test;
+* hypothesis: random small shapes, layouts, k and group caps round-trip, with
+  64-bit aligned bucket bases and monotone start bits;
 * ESC symbol choice: smallest u16 outside the kept set (row buckets, where a
   data symbol can collide with it) or outside all of the key's symbols (by
   scale), checked against a brute-force scan.
@@ -243,3 +245,23 @@ def test_validation_messages():
         oracle.awq_encode(bits, q, sc, 11, 256, 0, True)
     with pytest.raises(ValueError, match="unsupported scales_u16 shape"):
         oracle.awq_encode(bits, q, np.zeros(5, np.uint16), 11)
+
+
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as st  # noqa: E402
+
+
+@settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(n=st.integers(1, 24), mcols=st.sampled_from([8, 16, 48, 64]), group=st.sampled_from([None, 8, 16]),
+       k=st.sampled_from([1, 3, 64, 256, 1024]), cap=st.integers(1, 9), by_scale=st.booleans(),
+       seed=st.integers(0, 1 << 16))
+def test_round_trip_property(n, mcols, group, k, cap, by_scale, seed):
+    """Any small shape, scale layout, k (below and above the column count) and
+    group cap: decode(encode(x)) == x, and per-bucket bit counts sum up."""
+    w = make_awq_weight(n, mcols, group, seed=seed)
+    bits, q, sc = _np(w)
+    d = oracle.awq_encode(bits, q, sc, L, k, cap, by_scale)
+    assert np.array_equal(oracle.awq_decode(d, q, n, mcols), bits)
+    base, sb = d["bucket_bit_base_i64"], d["bucket_thread_startbit_u32"]
+    assert np.all(base[:-1] % 64 == 0) and np.all(np.diff(sb.astype(np.int64), axis=1) >= 0)
+    assert np.all(base[:-1] + sb[:, -1] <= np.append(base[1:-1], base[-1]))
