@@ -203,6 +203,7 @@ def run_awq(args, dev) -> int:
                "sample": f"oracle AWQ by-scale decode of layer-0 weights, {done / 1e6:.1f} M elements in "
                          f"{elapsed:.2f} s"}
     head = results["by_scale"]
+    traffic, traffic_src = read_traffic("awq8b_by_scale", os.path.join(ROOT, "profiles", "awq_decode_layer8b.md"))
     result = {
         "metric": "AWQ int4 -> BF16 decompress GB/s (out); one Llama-3-8B layer in one plan launch",
         "value": head["plan_out_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -211,8 +212,9 @@ def run_awq(args, dev) -> int:
                                 "the GPU",
         "config": {"workload": WORKLOADS["awq8b"], "layouts": results},
         "roofline": {"bound": "hbm", "achieved": head["plan_achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["plan_achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes": head["algorithmic_bytes"], "kernel_ms": head["plan_layer_ms"]},
+                     "frac": round(head["plan_achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": head["algorithmic_bytes"], "kernel_ms": head["plan_layer_ms"],
+                     "traffic_source": traffic_src},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -405,16 +407,16 @@ def sidecar_bytes(sc) -> int:
     return sum(t.numel() * t.element_size() for k, t in sc.items() if k not in _NOT_STORED)
 
 
-def read_traffic(workload: str):
-    """HBM bytes per decode launch from the committed rocprofv3 PMC summary, if it covers this workload."""
+def read_traffic(workload: str, path: str = TRAFFIC_PROFILE):
+    """HBM bytes per decode launch from a committed rocprofv3 PMC summary, if it covers this workload."""
     try:
-        text = open(TRAFFIC_PROFILE).read()
+        text = open(path).read()
     except OSError:
         return None, None
     m = re.search(r"^traffic_bytes_per_launch\[%s\]\s*=\s*([0-9.eE+]+)" % re.escape(workload), text, re.M)
     if not m:
         return None, None
-    return float(m.group(1)), os.path.relpath(TRAFFIC_PROFILE, ROOT)
+    return float(m.group(1)), os.path.relpath(path, ROOT)
 
 
 def cpu_baseline(items, seconds: float, threads: int):
