@@ -52,6 +52,8 @@ def parse_args(argv=None):
                         "layer (config 2); layer70b: one 70B layer with outliers and ESC codes (config 3); "
                         "gemm8b: decode share of an 8B layer's latency next to its BF16 GEMMs (config 4); "
                         "awq8b: AWQ int4 decode of one 8B layer, by-scale and row-bucket sidecars")
+    p.add_argument("--awq-k", type=int, default=1024,
+                   help="awq8b: substreams per bucket of the AWQ sidecars (the reference builders default to 256)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="time budget of the CPU baseline sample")
     p.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: min(16, cpu_count))")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -103,7 +105,8 @@ def run_awq(args, dev) -> int:
         for j, (name, n, m) in enumerate(LLAMA3_8B_LAYER):
             w = make_awq_weight(n, m, group, seed=300 + j, device=dev)
             scales = w.scale_u16
-            sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, scales, 11, 1024, 1024, bool(group), with_stats=True)
+            sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, scales, 11, args.awq_k, 1024, bool(group),
+                                           with_stats=True)
             if group:
                 call = lambda sc=sc, w=w, n=n, m=m, o=None: awq.huffman_decode_awq_int4_bucket_by_scale(  # noqa: E731
                     w.int4_u8, sc["bitstream_u64"], sc["decode_syms_u16"], sc["decode_lens_u8"],
@@ -210,7 +213,7 @@ def run_awq(args, dev) -> int:
         "ms_per_step": head["plan_layer_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "u16", "data": "synthetic: seeded N(0,0.02^2) BF16, AWQ-style int4 (group 128), sidecar built on "
                                 "the GPU",
-        "config": {"workload": WORKLOADS["awq8b"], "layouts": results},
+        "config": {"workload": WORKLOADS["awq8b"], "threads_per_block": args.awq_k, "layouts": results},
         "roofline": {"bound": "hbm", "achieved": head["plan_achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["plan_achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": head["algorithmic_bytes"], "kernel_ms": head["plan_layer_ms"],
