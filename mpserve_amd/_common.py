@@ -35,9 +35,10 @@ def read_status(device: torch.device | None = None) -> int:
     return int(v.value)
 
 
-def _maybe_check_status(device: torch.device) -> None:
+def _maybe_check_status(device: torch.device, op: str = "huffman_decode_fp8") -> None:
+    """With MPSERVE_DECODE_CHECK=1: synchronise and raise if the decode flagged the sidecar."""
     if os.environ.get("MPSERVE_DECODE_CHECK", "0") == "1":
         st = read_status(device)
         if st:
-            raise RuntimeError(f"huffman_decode_fp8: sidecar integrity flags 0x{st:x} "
+            raise RuntimeError(f"{op}: sidecar integrity flags 0x{st:x} "
                                "(1=bucket range, 2=row index, 4=table id, 8=lane bit desync)")

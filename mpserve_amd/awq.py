@@ -44,7 +44,6 @@ BY_SCALE_KEYS = (
     ("bucket_thread_startbit_u32", 10, torch.uint32), ("bucket_bit_base_i64", 11, torch.int64),
     ("bitstream_u64", 12, torch.uint64), ("shape_nmkg_i64", 13, torch.int64),
 )
-_ESIZE = {torch.uint16: 2, torch.uint8: 1, torch.int32: 4, torch.uint32: 4, torch.int64: 8, torch.uint64: 8}
 
 
 def build_awq_sidecar(bf16, int4, scales, max_len: int = 11, threads: int = 256, group_cap: int = 1024,
@@ -168,12 +167,10 @@ def _launch(int4, bitstream, syms, lens, table, col_start, col_len, offsets, row
     d.n, d.m, d.out = n, m, out.data_ptr()
     if n * m >= (1 << 31):
         raise ValueError("tensor too large for the AWQ decode kernel (n*m >= 2^31)")
-    if group_col is not None and rows.numel() > 0 and group_col.data_ptr() == 0:
-        raise ValueError("group_col_start_i32 must be defined")
     with torch.cuda.device(dev):
         _native.check(_native.lib().mps_awq_decode(ctypes.byref(d), int(max_len),
                                                    ctypes.c_void_p(_stream_handle(dev))))
-    _maybe_check_status(dev)
+    _maybe_check_status(dev, "AWQ int4 decode")
     return out
 
 
