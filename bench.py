@@ -178,7 +178,7 @@ def run_awq(args, dev) -> int:
         torch.cuda.synchronize()
         plan_ms = sum(s0.elapsed_time(e0) for s0, e0 in ev) / args.steps
         log(f"{layout} layer: {tot_ms:.4f} ms as 7 op launches, {plan_ms:.4f} ms as one plan launch "
-            f"({plan.info()['work_items']} buckets)")
+            f"({plan.info()['work_items']} work items)")
         results[layout] = {"layer_decode_ms": round(tot_ms, 4), "out_gbs": round(2 * elems / tot_ms / 1e6, 1),
                            "algorithmic_bytes": int(tot_alg), "achieved_gbs": round(tot_alg / tot_ms / 1e6, 1),
                            "plan_layer_ms": round(plan_ms, 4), "plan_out_gbs": round(2 * elems / plan_ms / 1e6, 1),

@@ -312,15 +312,91 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
   awq_bucket<kSplit>(T, blockIdx.x / kSplit, (int)(blockIdx.x % kSplit), lut, s_base, status);
 }
 
-// Plan launch: workgroup i decodes bucket work[i].y of tensor work[i].x (the
-// work list holds every bucket of every tensor of the plan, largest first).
+// Plan launch: workgroup i decodes buckets work[i].y .. work[i].y + work[i].z - 1
+// of tensor work[i].x. A record's buckets have identical table ids (one scale),
+// so they share the tables in LDS; each gets kAwqBlock / nsub work-items (its k
+// lanes) and a kRowSlots / nsub slice of the row offsets. With k = 256 four
+// buckets run in one workgroup instead of one (the tables allow one
+// workgroup per CU).
 __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
-                                                             const int2 *__restrict__ work, uint32_t *status) {
+                                                             const int4 *__restrict__ work, uint32_t *status) {
   __shared__ uint32_t lut[kLutEntries];
   __shared__ uint32_t s_base[kRowSlots];
-  const int2 w = work[blockIdx.x];
+  const int4 w = work[blockIdx.x];
   const mps_awq_tensor T = tensors[w.x];
-  awq_bucket<1>(T, w.y, 0, lut, s_base, status);
+  const int nsub = w.z;
+  const int per = kAwqBlock / nsub;
+  const int slots = kRowSlots / nsub;
+  const int tid = threadIdx.x;
+  const int sub = tid / per, lane = tid - sub * per;
+  const int64_t b = (int64_t)w.y + (sub < nsub ? sub : 0);
+
+  // Tables of the record's first bucket, filled by all work-items (as awq_bucket<1>).
+  {
+    const int64_t b0 = w.y;
+    int32_t gid[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) gid[q] = T.bucket_table[b0 * 16 + q];
+    if (tid == 0) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        if (gid[q] < -1 || gid[q] >= T.num_tables) flag(status, MPS_STATUS_BAD_TABLE);
+    }
+    const int64_t G = T.num_tables;
+    if (G <= 0) {
+      for (int i = tid; i < kLutEntries; i += kAwqBlock) lut[i] = 15u;
+    } else {
+      uint32_t sy[32], ln[32];
+#pragma unroll
+      for (int it = 0; it < 32; ++it) {
+        const int i = it * kAwqBlock + tid;
+        const int q = i >> kAwqL, p = i & (kAwqTable - 1);
+        const uint32_t g = (gid[q] >= 0 && gid[q] < G) ? (uint32_t)gid[q] : 0u;
+        sy[it] = T.decode_syms[(size_t)g * kAwqTable + p];
+        ln[it] = T.decode_lens[(size_t)g * kAwqPacked + (p >> 1)];
+      }
+#pragma unroll
+      for (int it = 0; it < 32; ++it) {
+        const int i = it * kAwqBlock + tid;
+        const int q = i >> kAwqL, p = i & (kAwqTable - 1);
+        const bool ok = gid[q] >= 0 && gid[q] < G;
+        lut[i] = ok ? (sy[it] << 16) | ((p & 1) ? (ln[it] >> 4) : (ln[it] & 15u)) : 15u;
+      }
+    }
+  }
+  // This work-item's bucket (decode_huffman.cu:417-444, :528-545).
+  const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
+  const int32_t rows = rb - ra;
+  const bool by_scale = T.group_col_start != nullptr;
+  const int32_t c0 = by_scale ? 0 : T.bucket_col_start[b];
+  const int32_t cl = by_scale ? (int32_t)T.group_size : T.bucket_col_len[b];
+  bool ok = sub < nsub && rows > 0;
+  if (ok && (cl <= 0 || ra < 0 || (int64_t)rb > T.num_row_indices ||
+             (!by_scale && (c0 < 0 || (int64_t)c0 + cl > T.m)))) {
+    if (lane == 0) flag(status, MPS_STATUS_BAD_BUCKET);
+    ok = false;
+  }
+  uint32_t *__restrict__ my_base = s_base + sub * slots;
+  if (ok) {
+    const int32_t staged = rows < slots ? rows : slots;
+    for (int r = lane; r < staged; r += per) {
+      const int64_t row = T.row_indices[ra + r];
+      const int64_t col = by_scale ? (int64_t)T.group_col_start[ra + r] : (int64_t)c0;
+      uint32_t base = kBadBase;
+      if (row >= 0 && row < T.n && col >= 0 && col + cl <= T.m) base = (uint32_t)(row * T.m + col);
+      else flag(status, MPS_STATUS_BAD_ROW);
+      my_base[r] = base;
+    }
+  }
+  __syncthreads();
+  if (!ok) return;
+  const int64_t total = (int64_t)rows * cl;
+  const int32_t k = (int32_t)T.k;
+  const int32_t k_eff = total < k ? (int32_t)total : k;
+  if (lane >= k_eff) return;
+  // nsub > 1 only for buckets whose rows all fit their slice (the plan checks)
+  if (rows <= slots) awq_lane<true>(T, lut, my_base, b, ra, c0, cl, total, k, k_eff, lane, status);
+  else awq_lane<false>(T, lut, my_base, b, ra, c0, cl, total, k, k_eff, lane, status);
 }
 
 int check_awq(const mps_awq_tensor *t) {
@@ -353,7 +429,7 @@ struct mps_awq_plan {
   int device = 0;
   int64_t count = 0, nwork = 0;
   mps_awq_tensor *d_tensors = nullptr;
-  int2 *d_work = nullptr;
+  int4 *d_work = nullptr;  // {tensor, first bucket, buckets, 0}
 };
 
 extern "C" {
@@ -388,10 +464,12 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, mps_awq_pl
   *plan_out = nullptr;
   if (count < 0 || count >= ((int64_t)1 << 31) || (count > 0 && !tensors))
     return fail(MPS_ERR_INVALID_ARGUMENT, "invalid tensor list");
-  // Every bucket of every tensor, ordered by elements (largest first), so the
-  // launch's last workgroups are its smallest.
-  std::vector<std::pair<int64_t, int2>> items;
-  std::vector<int32_t> roff, clen;
+  // Work records: runs of up to 1024 / k consecutive buckets of one tensor with
+  // identical table ids (one scale) and at most kRowSlots / 4 rows each, so
+  // they can share a workgroup's tables; ordered by elements, largest first,
+  // so the launch's last workgroups are its smallest.
+  std::vector<std::pair<int64_t, int4>> items;
+  std::vector<int32_t> roff, clen, btab;
   for (int64_t i = 0; i < count; ++i) {
     const mps_awq_tensor &T = tensors[i];
     int rc = check_awq(&T);
@@ -399,33 +477,50 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, mps_awq_pl
     const int64_t B = T.num_buckets;
     if (B == 0) continue;
     roff.resize((size_t)B + 1);
+    btab.resize((size_t)B * 16);
     MPS_HIP_CHECK(hipMemcpy(roff.data(), T.bucket_row_offsets, sizeof(int32_t) * (B + 1), hipMemcpyDefault));
+    MPS_HIP_CHECK(hipMemcpy(btab.data(), T.bucket_table, sizeof(int32_t) * B * 16, hipMemcpyDefault));
     if (!T.group_col_start) {
       clen.resize((size_t)B);
       MPS_HIP_CHECK(hipMemcpy(clen.data(), T.bucket_col_len, sizeof(int32_t) * B, hipMemcpyDefault));
     }
-    for (int64_t b = 0; b < B; ++b) {
+    auto rows_of = [&](int64_t b) { return std::max<int64_t>(0, (int64_t)roff[(size_t)b + 1] - roff[(size_t)b]); };
+    auto elems_of = [&](int64_t b) {
       const int64_t cols = T.group_col_start ? T.group_size : (int64_t)clen[(size_t)b];
-      const int64_t elems = std::max<int64_t>(0, (int64_t)roff[(size_t)b + 1] - roff[(size_t)b]) * std::max<int64_t>(0, cols);
-      items.push_back({elems, make_int2((int)i, (int)b)});
+      return rows_of(b) * std::max<int64_t>(0, cols);
+    };
+    const int64_t maxsub = T.k <= kAwqBlock / 4 ? 4 : T.k <= kAwqBlock / 2 ? 2 : 1;
+    const int64_t row_cap = kRowSlots / 4;
+    int64_t b = 0;
+    while (b < B) {
+      int64_t nsub = 1, elems = elems_of(b);
+      if (rows_of(b) <= row_cap) {
+        while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap &&
+               std::equal(btab.begin() + b * 16, btab.begin() + b * 16 + 16, btab.begin() + (b + nsub) * 16)) {
+          elems += elems_of(b + nsub);
+          ++nsub;
+        }
+      }
+      items.push_back({elems, make_int4((int)i, (int)b, (int)nsub, 0)});
+      b += nsub;
     }
   }
   std::stable_sort(items.begin(), items.end(),
-                   [](const std::pair<int64_t, int2> &x, const std::pair<int64_t, int2> &y) { return x.first > y.first; });
+                   [](const std::pair<int64_t, int4> &x, const std::pair<int64_t, int4> &y) { return x.first > y.first; });
   auto plan = new (std::nothrow) mps_awq_plan();
   if (!plan) return fail(MPS_ERR_NO_MEMORY, "out of memory");
   MPS_HIP_CHECK(hipGetDevice(&plan->device));
   plan->count = count;
   plan->nwork = (int64_t)items.size();
-  std::vector<int2> work(items.size());
+  std::vector<int4> work(items.size());
   for (size_t j = 0; j < items.size(); ++j) work[j] = items[j].second;
   hipError_t e = hipSuccess;
   if (count > 0) e = hipMalloc(&plan->d_tensors, sizeof(mps_awq_tensor) * count);
   if (e == hipSuccess && count > 0)
     e = hipMemcpy(plan->d_tensors, tensors, sizeof(mps_awq_tensor) * count, hipMemcpyHostToDevice);
-  if (e == hipSuccess && !work.empty()) e = hipMalloc(&plan->d_work, sizeof(int2) * work.size());
+  if (e == hipSuccess && !work.empty()) e = hipMalloc(&plan->d_work, sizeof(int4) * work.size());
   if (e == hipSuccess && !work.empty())
-    e = hipMemcpy(plan->d_work, work.data(), sizeof(int2) * work.size(), hipMemcpyHostToDevice);
+    e = hipMemcpy(plan->d_work, work.data(), sizeof(int4) * work.size(), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     mps_awq_plan_destroy(plan);
     return hip_fail(e, "mps_awq_plan_create");

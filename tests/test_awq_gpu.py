@@ -245,7 +245,8 @@ def test_plan_decodes_mixed_layouts_in_one_launch():
         items.append((w.int4_u8, sc, torch.empty((n, m), dtype=torch.bfloat16, device=DEV)))
         srcs.append(w.bf16)
     plan = awq.AwqDecodePlan(items)
-    assert plan.info()["work_items"] == sum(sc["bucket_table_i32"].shape[0] for _, sc, _ in items)
+    # k = 256 tensors: runs of same-scale buckets share a workgroup, so fewer records than buckets
+    assert 0 < plan.info()["work_items"] < sum(sc["bucket_table_i32"].shape[0] for _, sc, _ in items)
     read_status(torch.device(DEV))
     for _ in range(2):  # replays give the same outputs
         for o in plan.outputs:
