@@ -158,8 +158,10 @@ typedef struct mps_awq_tensor {
 int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream);
 
 /* Batched AWQ decode plan: one launch decodes every bucket of many AWQ int4
- * tensors (either layout, mixed), largest buckets first. Reads each tensor's
- * bucket row offsets (and column lengths) once at create time (synchronously)
+ * tensors (either layout, mixed), largest work first. Runs of up to 1024 / k
+ * consecutive buckets with identical table ids share one workgroup and its
+ * tables. Reads each tensor's bucket row offsets, table ids (and column
+ * lengths) once at create time (synchronously)
  * and copies the descriptors to device memory it owns; the pointed-to tensors
  * must stay alive while the plan is used, and a tensor whose bucket metadata
  * is rewritten needs a new plan. Decodes are asynchronous on `stream`.
