@@ -187,7 +187,7 @@ def huffman_build_fp8_decode_tables(bf16_params: torch.Tensor, fp8_params: torch
 def _not_in_scope(name: str):
     def f(*args, **kwargs):
         raise NotImplementedError(f"MPServe_cuda.{name} is not provided by the MI355X build "
-                                  "(only the FP8 Huffman path is)")
+                                  "(the FP8 and AWQ int4 bucket Huffman paths are)")
     f.__name__ = name
     return f
 
