@@ -81,6 +81,8 @@ def make_awq_weight(n: int, m: int, group: int | None = 128, sigma: float = 0.02
     w = (torch.randn((n, m), generator=g, device=device, dtype=torch.float32) * sigma).to(torch.bfloat16)
     wf = w.float()
     gs = m if group is None else int(group)
+    if gs <= 0 or m % gs != 0:
+        raise ValueError(f"group ({gs}) must divide the column count ({m})")
     amax = wf.reshape(n, m // gs, gs).abs().amax(dim=2)
     s = (amax / 7.0).to(torch.bfloat16)
     s = torch.where(s.float() > 0, s, torch.ones_like(s))

@@ -247,17 +247,27 @@ def test_validation_messages():
         oracle.awq_encode(bits, q, np.zeros(5, np.uint16), 11)
 
 
-from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import HealthCheck, assume, example, given, settings  # noqa: E402
 from hypothesis import strategies as st  # noqa: E402
+
+
+def test_make_awq_weight_rejects_group_not_dividing_columns():
+    with pytest.raises(ValueError, match="must divide the column count"):
+        make_awq_weight(1, 8, 16, seed=0)
 
 
 @settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.too_slow])
 @given(n=st.integers(1, 24), mcols=st.sampled_from([8, 16, 48, 64]), group=st.sampled_from([None, 8, 16]),
        k=st.sampled_from([1, 3, 64, 256, 1024]), cap=st.integers(1, 9), by_scale=st.booleans(),
        seed=st.integers(0, 1 << 16))
+@example(n=1, mcols=16, group=16, k=1, cap=1, by_scale=True, seed=0)
+@example(n=1, mcols=8, group=8, k=1, cap=1, by_scale=False, seed=0)
 def test_round_trip_property(n, mcols, group, k, cap, by_scale, seed):
     """Any small shape, scale layout, k (below and above the column count) and
-    group cap: decode(encode(x)) == x, and per-bucket bit counts sum up."""
+    group cap: decode(encode(x)) == x, and per-bucket bit counts sum up. The
+    group width must divide the column count (a quantisation group never
+    straddles rows)."""
+    assume(group is None or mcols % group == 0)
     w = make_awq_weight(n, mcols, group, seed=seed)
     bits, q, sc = _np(w)
     d = oracle.awq_encode(bits, q, sc, L, k, cap, by_scale)
