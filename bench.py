@@ -226,19 +226,9 @@ def run_awq(args, dev) -> int:
 
 def weight_list(workload: str):
     """(name, n, m, seed, sigma, outlier_p) of every weight of a workload."""
-    from mpserve_amd.synthetic import LLAMA3_8B_LAYER, LLAMA3_8B_LM_HEAD, LLAMA3_70B_LAYER
+    from mpserve_amd.synthetic import config_weights
 
-    if workload == "layer70b":
-        return [(f"layers.0.{name}", n, m, 200 + j, 0.015, 1e-3) for j, (name, n, m) in enumerate(LLAMA3_70B_LAYER)]
-    layers = 32 if workload == "model8b" else 1
-    out = []
-    for layer in range(layers):
-        for j, (name, n, m) in enumerate(LLAMA3_8B_LAYER):
-            out.append((f"layers.{layer}.{name}", n, m, 100 + 16 * layer + j, 0.02, 0.0))
-    if workload == "model8b":
-        name, n, m = LLAMA3_8B_LM_HEAD
-        out.append((name, n, m, 99, 0.02, 0.0))
-    return out
+    return config_weights("layer8b" if workload == "gemm8b" else workload)
 
 
 def data_note(workload: str) -> str:

@@ -28,6 +28,27 @@ LLAMA3_70B_LAYER: List[Tuple[str, int, int]] = [
 LLAMA3_8B_LM_HEAD = ("lm_head", 128256, 4096)
 
 
+def config_weights(workload: str) -> List[Tuple[str, int, int, int, float, float]]:
+    """(name, n, m, seed, sigma, outlier_p) of every weight of a benchmark configuration.
+
+    ``layer8b`` (config 2): one Llama-3-8B layer; ``layer70b`` (config 3): one
+    Llama-3-70B layer, sigma 0.015 with 0.1% outliers at +-8 sigma;
+    ``model8b`` (config 5): 32 Llama-3-8B layers plus lm_head. Seeds are fixed
+    per (layer, projection), so every caller builds the same inputs.
+    """
+    if workload == "layer70b":
+        return [(f"layers.0.{name}", n, m, 200 + j, 0.015, 1e-3) for j, (name, n, m) in enumerate(LLAMA3_70B_LAYER)]
+    if workload not in ("layer8b", "model8b"):
+        raise ValueError(f"unknown workload {workload!r}")
+    layers = 32 if workload == "model8b" else 1
+    out = [(f"layers.{layer}.{name}", n, m, 100 + 16 * layer + j, 0.02, 0.0)
+           for layer in range(layers) for j, (name, n, m) in enumerate(LLAMA3_8B_LAYER)]
+    if workload == "model8b":
+        name, n, m = LLAMA3_8B_LM_HEAD
+        out.append((name, n, m, 99, 0.02, 0.0))
+    return out
+
+
 @dataclass
 class SyntheticWeight:
     bf16: torch.Tensor        # [n, m] bfloat16
