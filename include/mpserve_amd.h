@@ -71,27 +71,37 @@ int mps_clock_rate_khz(int device, int64_t *khz_out);
 int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
 
 /* Batched decode plan: one launch decodes many tensors (a layer, a model).
- * The plan copies the descriptors to device memory it owns and reads each
- * tensor's bucket row offsets, column ranges and bit bases (synchronously, at
- * create time) to order the work largest first and to build one work record
- * per bucket. When the buckets are few or uneven for the device's CUs, large
- * buckets are split into row ranges: a kernel on the legacy default stream
- * walks their substreams' code lengths once and records each substream's bit
- * position at every range's first row (the lane checkpoints, owned by the
- * plan). A sidecar whose bucket metadata, row indices, start bits, tables,
- * FP8 bytes or bitstream is rewritten needs a new plan in that case. The
- * pointed-to sidecars must stay alive while the plan is used. Launches (like
- * mps_fp8_decode's) are persistent: one workgroup per CU walks its share of
- * the work.
+ * Creation first synchronises `stream` (the caller's stream, which may still
+ * be writing the sidecars), then reads each tensor's bucket row offsets,
+ * column ranges and bit bases to order the work largest first and to build
+ * one work record per bucket, and copies the descriptors into one device
+ * allocation the plan owns (with its own status word). When the buckets are
+ * few or uneven for the device's CUs, large buckets are split into row
+ * ranges: a kernel on `stream` walks their substreams' code lengths once and
+ * records each substream's bit position at every range's first row (the lane
+ * checkpoints, also owned by the plan). A sidecar whose bucket metadata, row
+ * indices, start bits, tables, FP8 bytes or bitstream is rewritten needs a
+ * new plan in that case. The pointed-to sidecars must stay alive while the
+ * plan is used. Launches (like mps_fp8_decode's) are persistent: one
+ * workgroup per CU walks its share of the work. Decodes are asynchronous on
+ * their stream and OR their MPS_STATUS_* flags into the plan's status word
+ * (mps_fp8_plan_read_status).
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:739); it serves its apply() and model loading paths
  * (scripts/mpserve_vllm_fp8_huffman.py:491-557). */
 typedef struct mps_fp8_plan mps_fp8_plan;
-int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_plan **plan_out);
+int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stream, mps_fp8_plan **plan_out);
 int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream);
+/* A plan of one tensor, decoded into `out` (device, n*m BF16) instead of the
+ * output it was created with. Its flags go to the device status word
+ * (mps_fp8_read_status), as a single-tensor decode's do: this serves the
+ * drop-in decode op's per-sidecar plan cache. */
+int mps_fp8_plan_decode_into(mps_fp8_plan *plan, uint16_t *out, void *stream);
 /* The plan's work list (for profiling tools): work items (buckets, and the row
  * ranges of the buckets it split), bytes of LDS per workgroup. */
 int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes);
+/* Read and clear the plan's MPS_STATUS_* flags; synchronises `stream` first. */
+int mps_fp8_plan_read_status(mps_fp8_plan *plan, void *stream, uint32_t *status_out);
 int mps_fp8_plan_destroy(mps_fp8_plan *plan);
 
 /* Inputs of the GPU sidecar builder, all device pointers: BF16 bit patterns
@@ -160,17 +170,19 @@ int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream);
 /* Batched AWQ decode plan: one launch decodes every bucket of many AWQ int4
  * tensors (either layout, mixed), largest work first. Runs of up to 1024 / k
  * consecutive buckets with identical table ids share one workgroup and its
- * tables. Reads each tensor's bucket row offsets, table ids (and column
- * lengths) once at create time (synchronously)
- * and copies the descriptors to device memory it owns; the pointed-to tensors
- * must stay alive while the plan is used, and a tensor whose bucket metadata
- * is rewritten needs a new plan. Decodes are asynchronous on `stream`.
+ * tables. Creation synchronises `stream` first, then reads each tensor's
+ * bucket row offsets, table ids (and column lengths) once and copies the
+ * descriptors into one device allocation the plan owns (with its own status
+ * word, mps_awq_plan_read_status); the pointed-to tensors must stay alive
+ * while the plan is used, and a tensor whose bucket metadata is rewritten
+ * needs a new plan. Decodes are asynchronous on `stream`.
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:857, :998). */
 typedef struct mps_awq_plan mps_awq_plan;
-int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, mps_awq_plan **plan_out);
+int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stream, mps_awq_plan **plan_out);
 int mps_awq_plan_decode(mps_awq_plan *plan, void *stream);
 int mps_awq_plan_info(const mps_awq_plan *plan, int64_t *work_items);
+int mps_awq_plan_read_status(mps_awq_plan *plan, void *stream, uint32_t *status_out);
 int mps_awq_plan_destroy(mps_awq_plan *plan);
 
 /* Inputs of the AWQ int4 sidecar builders, all device pointers: BF16 bit
@@ -218,8 +230,11 @@ int mps_fp8_sidecar_copy(const mps_fp8_sidecar *sc, void *const *dst17, void *st
 int mps_fp8_sidecar_stats(const mps_fp8_sidecar *sc, int64_t *stats4);
 int mps_fp8_sidecar_free(mps_fp8_sidecar *sc);
 
-/* Read and clear the MPS_STATUS_* flags the decodes on `device` recorded
- * since the last call. Synchronises `stream` first. */
+/* Read and clear the MPS_STATUS_* flags the single-tensor decodes
+ * (mps_fp8_decode, mps_awq_decode, mps_fp8_plan_decode_into) on `device`
+ * recorded since the last call. The word is per device, not per stream:
+ * flags of decodes on any stream of the device accumulate in it. It is a
+ * module global of the library (no allocation). Synchronises `stream` first. */
 int mps_fp8_read_status(int device, void *stream, uint32_t *status_out);
 
 #ifdef __cplusplus

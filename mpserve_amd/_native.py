@@ -92,9 +92,11 @@ def lib():
     L.mps_last_error.restype = ctypes.c_char_p
     L.mps_clock_rate_khz.argtypes = [ctypes.c_int, ctypes.POINTER(_i64)]
     L.mps_fp8_decode.argtypes = [ctypes.POINTER(MpsFp8Tensor), _i64, _p]
-    L.mps_fp8_plan_create.argtypes = [ctypes.POINTER(MpsFp8Tensor), _i64, ctypes.POINTER(_p)]
+    L.mps_fp8_plan_create.argtypes = [ctypes.POINTER(MpsFp8Tensor), _i64, _p, ctypes.POINTER(_p)]
     L.mps_fp8_plan_decode.argtypes = [_p, _p]
+    L.mps_fp8_plan_decode_into.argtypes = [_p, _p, _p]
     L.mps_fp8_plan_info.argtypes = [_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
+    L.mps_fp8_plan_read_status.argtypes = [_p, _p, ctypes.POINTER(ctypes.c_uint32)]
     L.mps_fp8_plan_destroy.argtypes = [_p]
     L.mps_fp8_read_status.argtypes = [ctypes.c_int, _p, ctypes.POINTER(ctypes.c_uint32)]
     if hasattr(L, "mps_fp8_encode"):
@@ -105,13 +107,15 @@ def lib():
         L.mps_fp8_sidecar_stats.argtypes = [_p, ctypes.POINTER(_i64)]
     L.mps_awq_decode.argtypes = [ctypes.POINTER(MpsAwqTensor), _i64, _p]
     L.mps_awq_encode.argtypes = [ctypes.POINTER(MpsAwqEncodeIn), _p, ctypes.POINTER(_p)]
-    L.mps_awq_plan_create.argtypes = [ctypes.POINTER(MpsAwqTensor), _i64, ctypes.POINTER(_p)]
+    L.mps_awq_plan_create.argtypes = [ctypes.POINTER(MpsAwqTensor), _i64, _p, ctypes.POINTER(_p)]
     L.mps_awq_plan_decode.argtypes = [_p, _p]
     L.mps_awq_plan_info.argtypes = [_p, ctypes.POINTER(_i64)]
+    L.mps_awq_plan_read_status.argtypes = [_p, _p, ctypes.POINTER(ctypes.c_uint32)]
     L.mps_awq_plan_destroy.argtypes = [_p]
     for name in ("mps_clock_rate_khz", "mps_fp8_decode", "mps_fp8_plan_create", "mps_fp8_plan_decode",
-                 "mps_fp8_plan_info", "mps_fp8_plan_destroy", "mps_fp8_read_status", "mps_awq_decode",
-                 "mps_awq_encode", "mps_awq_plan_create", "mps_awq_plan_decode", "mps_awq_plan_info",
+                 "mps_fp8_plan_decode_into", "mps_fp8_plan_info", "mps_fp8_plan_read_status",
+                 "mps_fp8_plan_destroy", "mps_fp8_read_status", "mps_awq_decode", "mps_awq_encode",
+                 "mps_awq_plan_create", "mps_awq_plan_decode", "mps_awq_plan_info", "mps_awq_plan_read_status",
                  "mps_awq_plan_destroy"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L

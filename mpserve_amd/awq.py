@@ -371,8 +371,11 @@ class AwqDecodePlan:
         arr = (_native.MpsAwqTensor * max(1, len(descs)))(*descs)
         self._plan = ctypes.c_void_p()
         if self.device is not None:
+            # creation waits for the current stream, which may still be writing the sidecars
             with torch.cuda.device(self.device):
-                _native.check(_native.lib().mps_awq_plan_create(arr, len(descs), ctypes.byref(self._plan)))
+                _native.check(_native.lib().mps_awq_plan_create(arr, len(descs),
+                                                                ctypes.c_void_p(_stream_handle(self.device)),
+                                                                ctypes.byref(self._plan)))
 
     def decode(self, stream: torch.cuda.Stream | None = None):
         """Enqueue the decode on ``stream`` (default: the current stream); returns the outputs."""
@@ -389,6 +392,14 @@ class AwqDecodePlan:
         if self._plan:
             _native.check(_native.lib().mps_awq_plan_info(self._plan, ctypes.byref(wi)))
         return {"work_items": int(wi.value)}
+
+    def read_status(self, stream: torch.cuda.Stream | None = None) -> int:
+        """MPS_STATUS_* flags this plan's decodes recorded since the last read (synchronises)."""
+        v = ctypes.c_uint32(0)
+        if self._plan:
+            h = stream.cuda_stream if stream is not None else _stream_handle(self.device)
+            _native.check(_native.lib().mps_awq_plan_read_status(self._plan, ctypes.c_void_p(h), ctypes.byref(v)))
+        return int(v.value)
 
     def close(self) -> None:
         if getattr(self, "_plan", None):

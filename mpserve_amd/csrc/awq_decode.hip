@@ -27,6 +27,8 @@
 // 512-work-item workgroups per bucket, each with its own copy of the tables.
 #include <hip/hip_runtime.h>
 
+#include <cstring>
+
 #include <algorithm>
 #include <cstdint>
 #include <new>
@@ -425,11 +427,15 @@ int check_awq(const mps_awq_tensor *t) {
 
 using namespace mps;
 
+// A plan owns one device allocation: its status word, the tensor descriptors
+// and the work records {tensor, first bucket, buckets, 0}.
 struct mps_awq_plan {
   int device = 0;
   int64_t count = 0, nwork = 0;
+  void *d_block = nullptr;
+  uint32_t *d_status = nullptr;
   mps_awq_tensor *d_tensors = nullptr;
-  int4 *d_work = nullptr;  // {tensor, first bucket, buckets, 0}
+  int4 *d_work = nullptr;
 };
 
 extern "C" {
@@ -458,12 +464,15 @@ int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream) 
   return MPS_OK;
 }
 
-int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, mps_awq_plan **plan_out) {
+int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stream, mps_awq_plan **plan_out) {
   last_error().clear();
   if (!plan_out) return fail(MPS_ERR_INVALID_ARGUMENT, "plan_out is NULL");
   *plan_out = nullptr;
   if (count < 0 || count >= ((int64_t)1 << 31) || (count > 0 && !tensors))
     return fail(MPS_ERR_INVALID_ARGUMENT, "invalid tensor list");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // The sidecars may still be being written by work on the caller's stream.
+  MPS_HIP_CHECK(hipStreamSynchronize(st));
   // Work records: runs of up to 1024 / k consecutive buckets of one tensor with
   // identical table ids (one scale) and at most kRowSlots / 4 rows each, so
   // they can share a workgroup's tables; ordered by elements, largest first,
@@ -512,15 +521,22 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, mps_awq_pl
   MPS_HIP_CHECK(hipGetDevice(&plan->device));
   plan->count = count;
   plan->nwork = (int64_t)items.size();
-  std::vector<int4> work(items.size());
-  for (size_t j = 0; j < items.size(); ++j) work[j] = items[j].second;
-  hipError_t e = hipSuccess;
-  if (count > 0) e = hipMalloc(&plan->d_tensors, sizeof(mps_awq_tensor) * count);
-  if (e == hipSuccess && count > 0)
-    e = hipMemcpy(plan->d_tensors, tensors, sizeof(mps_awq_tensor) * count, hipMemcpyHostToDevice);
-  if (e == hipSuccess && !work.empty()) e = hipMalloc(&plan->d_work, sizeof(int4) * work.size());
-  if (e == hipSuccess && !work.empty())
-    e = hipMemcpy(plan->d_work, work.data(), sizeof(int4) * work.size(), hipMemcpyHostToDevice);
+  // status word (zero) | descriptors | work records: one allocation, one copy
+  const size_t o_tensors = 256;
+  const size_t o_work = o_tensors + ((sizeof(mps_awq_tensor) * (size_t)count + 255) & ~(size_t)255);
+  std::vector<char> host(o_work + sizeof(int4) * items.size(), 0);
+  if (count > 0) std::memcpy(host.data() + o_tensors, tensors, sizeof(mps_awq_tensor) * (size_t)count);
+  for (size_t j = 0; j < items.size(); ++j)
+    std::memcpy(host.data() + o_work + j * sizeof(int4), &items[j].second, sizeof(int4));
+  hipError_t e = hipMalloc(&plan->d_block, host.size());
+  if (e == hipSuccess) {
+    char *blk = static_cast<char *>(plan->d_block);
+    plan->d_status = reinterpret_cast<uint32_t *>(blk);
+    plan->d_tensors = reinterpret_cast<mps_awq_tensor *>(blk + o_tensors);
+    plan->d_work = reinterpret_cast<int4 *>(blk + o_work);
+    e = hipMemcpyAsync(blk, host.data(), host.size(), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+  }
   if (e != hipSuccess) {
     mps_awq_plan_destroy(plan);
     return hip_fail(e, "mps_awq_plan_create");
@@ -533,11 +549,8 @@ int mps_awq_plan_decode(mps_awq_plan *plan, void *stream) {
   last_error().clear();
   if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
   if (plan->nwork == 0) return MPS_OK;
-  uint32_t *status = nullptr;
-  int rc = status_word(plan->device, &status);
-  if (rc != MPS_OK) return rc;
   hipLaunchKernelGGL(awq_decode_plan, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, status);
+                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_status);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
@@ -548,10 +561,16 @@ int mps_awq_plan_info(const mps_awq_plan *plan, int64_t *work_items) {
   return MPS_OK;
 }
 
+int mps_awq_plan_read_status(mps_awq_plan *plan, void *stream, uint32_t *status_out) {
+  last_error().clear();
+  if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (!status_out) return fail(MPS_ERR_INVALID_ARGUMENT, "status_out is NULL");
+  return read_and_clear(plan->device, plan->d_status, stream, "mps_awq_plan_read_status", status_out);
+}
+
 int mps_awq_plan_destroy(mps_awq_plan *plan) {
   if (!plan) return MPS_OK;
-  if (plan->d_tensors) (void)hipFree(plan->d_tensors);
-  if (plan->d_work) (void)hipFree(plan->d_work);
+  if (plan->d_block) (void)hipFree(plan->d_block);
   delete plan;
   return MPS_OK;
 }

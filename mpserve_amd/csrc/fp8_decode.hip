@@ -125,7 +125,8 @@ static_assert(sizeof(WorkItem) == 64, "one scalar load per work item");
 constexpr int kDepth = 8;
 
 template <typename Idx>
-__device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+__device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, uint16_t *__restrict__ out,
+                                            const uint32_t *__restrict__ lut,
                                             const int32_t *__restrict__ s_rows, int32_t lane, int32_t k_eff,
                                             int64_t total, int32_t c0, int32_t cl, uint64_t pos0, uint64_t pos_end,
                                             uint32_t *status) {
@@ -152,7 +153,6 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, const uint3
   const int32_t last_row = (int32_t)((total - 1) / cl);
   const Idx m = (Idx)T.m;
   const uint8_t *__restrict__ fp8 = T.fp8;
-  uint16_t *__restrict__ out = T.out;
 
   // Addresses of the next kDepth elements (elements past `count` repeat the
   // lane's first element, whose address is always valid).
@@ -310,7 +310,8 @@ constexpr int kLdsWords = kQWords + kLutWords;
 
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 
-__device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+__device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, uint16_t *out,
+                                                 const uint32_t *__restrict__ lut,
                                                  uint32_t *__restrict__ queue, uint32_t lane, uint32_t k_eff,
                                                  uint32_t rows, uint32_t P, uint32_t rowoff_lo,
                                                  uint32_t rowoff_hi, uint64_t bucket_bit,
@@ -325,7 +326,7 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, const 
   bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
   const uint32_t nm = (uint32_t)(T.n * T.m);
   const __amdgpu_buffer_rsrc_t r_fp8 = make_rsrc(T.fp8, nm);
-  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(T.out, 2u * nm);
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(out, 2u * nm);
   // Bitstream window of this bucket: from its 64-bit aligned base to the end.
   const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
   const uint64_t base_byte = bucket_bit >> 3;
@@ -500,7 +501,7 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, const 
 // throughout and track the position per code.
 // ---------------------------------------------------------------------------
 template <int G, bool kEsc>
-__device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+__device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, uint16_t *out, const uint32_t *__restrict__ lut,
                                              uint32_t *__restrict__ queue, uint32_t lane, uint32_t col,
                                              uint32_t rows, uint32_t P, uint32_t rowoff_lo, uint32_t rowoff_hi,
                                              uint64_t bucket_bit, const uint2 (&first)[4], uint32_t pos,
@@ -615,7 +616,7 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
   // brought up to date once per step.
   auto decode_block = [&](auto chk, int s, int b, uint32_t &pw) {
     constexpr bool kChk = decltype(chk)::value;
-    uint16_t *dst = T.out + so[s][b];
+    uint16_t *dst = out + so[s][b];
 #pragma unroll
     for (int g = 0; g < G; g += 4) {
       uint32_t win = kChk ? window_chk(pb) : window_q(pw);
@@ -726,7 +727,7 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, const uint
 // straight from np.
 // ---------------------------------------------------------------------------
 template <bool kWrap>
-__device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint32_t *__restrict__ lut,
+__device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *out, const uint32_t *__restrict__ lut,
                                              uint32_t *__restrict__ queue, uint32_t lane, uint32_t rows, uint32_t P,
                                              uint32_t rowoff_lo, uint32_t rowoff_hi, uint64_t bucket_bit,
                                              const uint2 (&first)[4], uint32_t pos, uint32_t pos_end,
@@ -745,7 +746,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, const uint
   const uint32_t gall = nfull + (tail ? 1u : 0u);
   const uint32_t nm = (uint32_t)(T.n * T.m);
   const __amdgpu_buffer_rsrc_t r_fp8 = make_rsrc(T.fp8, nm);
-  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(T.out, 2u * nm);
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(out, 2u * nm);
   const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
   const uint64_t base_byte = bucket_bit >> 3;
   const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
@@ -1017,8 +1018,8 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
   return w;
 }
 
-__device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const WorkItem &w, uint32_t *lds,
-                                              uint32_t *status) {
+__device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t *out, const WorkItem &w,
+                                              uint32_t *lds, uint32_t *status) {
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
@@ -1187,21 +1188,21 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
     const uint32_t P = (uint32_t)cl / 1024u;
     if (!has_esc && P >= 4) {
       if (P % 4 == 0)
-        decode_slab4<false>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
+        decode_slab4<false>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
                             pos, pos_end, status);
       else
-        decode_slab4<true>(T, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
+        decode_slab4<true>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
                            pos, pos_end, status);
       return;
     }
-#define MPS_K1024(GG)                                                                                          \
-  do {                                                                                                         \
-    if (has_esc)                                                                                               \
-      decode_k1024<GG, true>(T, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P, rowoff_lo,     \
-                             rowoff_hi, base, first, pos, pos_end, status);                                    \
-    else                                                                                                       \
-      decode_k1024<GG, false>(T, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P, rowoff_lo,    \
-                              rowoff_hi, base, first, pos, pos_end, status);                                   \
+#define MPS_K1024(GG)                                                                                     \
+  do {                                                                                                    \
+    if (has_esc)                                                                                          \
+      decode_k1024<GG, true>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P,      \
+                             rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);                    \
+    else                                                                                                  \
+      decode_k1024<GG, false>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P,     \
+                              rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);                   \
   } while (0)
     if (P % 8 == 0) MPS_K1024(8);
     else if (P % 7 == 0) MPS_K1024(7);
@@ -1210,15 +1211,15 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, const Wor
     else MPS_K1024(1);
 #undef MPS_K1024
   } else if (fast) {
-    decode_rows_fast(T, lut, qregion, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows, (uint32_t)(cl / k_eff),
+    decode_rows_fast(T, out, lut, qregion, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows, (uint32_t)(cl / k_eff),
                      rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
   } else {
     const uint64_t pos0 = base + sb[lane];
     const uint64_t pend = base + w.endbits[lane];
     if (nm <= 0xFFFFFFFFull)
-      decode_lane<uint32_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
+      decode_lane<uint32_t>(T, out, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
     else
-      decode_lane<uint64_t>(T, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
+      decode_lane<uint64_t>(T, out, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
   }
 }
 
@@ -1238,14 +1239,16 @@ __device__ __forceinline__ void end_bucket() {
 __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
-    decode_bucket(T, bucket_item(T, b), lds, status);
+    decode_bucket(T, T.out, bucket_item(T, b), lds, status);
     end_bucket();
   }
 }
 
+// out0: when not null, the output of every item (a plan of one tensor decoding
+// into a buffer other than the one it was created with).
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
                                                           const WorkItem *__restrict__ work, int64_t nwork,
-                                                          uint32_t *status) {
+                                                          uint32_t *status, uint16_t *out0) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   if ((int64_t)blockIdx.x >= nwork) return;
   // The next bucket's record (scalar registers) is loaded with this bucket's
@@ -1254,7 +1257,8 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
   for (int64_t i = blockIdx.x; i < nwork; i += gridDim.x) {
     const int64_t inext = i + gridDim.x;
     const WorkItem wn = work[inext < nwork ? inext : i];
-    decode_bucket(tensors[w.tensor], w, lds, status);
+    const mps_fp8_tensor &T = tensors[w.tensor];
+    decode_bucket(T, out0 ? out0 : T.out, w, lds, status);
     end_bucket();
     w = wn;
   }
@@ -1376,24 +1380,29 @@ int check_tensor(const mps_fp8_tensor *t) {
 
 }  // namespace
 
-// One 4-byte status word per device, allocated on first use and kept for the
-// life of the process (it is cleared by mps_fp8_read_status).
+// The status word of the single-tensor decodes (FP8 and AWQ) on a device: a
+// module global, so each device holds its own copy, zero from module load to
+// the end of the process, and no decode allocates it. It is per device, not
+// per stream: decodes on different streams of one device OR into the same
+// word (mps_fp8_read_status reads and clears it). Plans carry a word of their own.
+static __device__ __align__(256) uint32_t g_status[64];
+
 int status_word(int device, uint32_t **out) {
   static std::mutex mu;
   static uint32_t *words[kMaxDevices] = {};
   if (device < 0 || device >= kMaxDevices) return fail(MPS_ERR_INVALID_ARGUMENT, "device ordinal out of range");
   std::lock_guard<std::mutex> lock(mu);
   if (!words[device]) {
+    // The host-side name of a device global is not its device address: look
+    // it up once per device, with that device current.
     int prev = 0;
     MPS_HIP_CHECK(hipGetDevice(&prev));
     if (prev != device) MPS_HIP_CHECK(hipSetDevice(device));
-    uint32_t *p = nullptr;
-    hipError_t e = hipMalloc(&p, 256);
-    const uint32_t zero[64] = {};
-    if (e == hipSuccess) e = hipMemcpy(p, zero, sizeof(zero), hipMemcpyHostToDevice);
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_status));
     if (prev != device) (void)hipSetDevice(prev);
-    if (e != hipSuccess) return hip_fail(e, "status word allocation");
-    words[device] = p;
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(status word)");
+    words[device] = static_cast<uint32_t *>(p);
   }
   *out = words[device];
   return MPS_OK;
@@ -1404,14 +1413,39 @@ std::string &last_error() {
   return s;
 }
 
+// Read a device status word and clear it, after `stream`'s work (synchronous).
+int read_and_clear(int device, uint32_t *word, void *stream, const char *what, uint32_t *status_out) {
+  int prev = 0;
+  MPS_HIP_CHECK(hipGetDevice(&prev));
+  if (prev != device) MPS_HIP_CHECK(hipSetDevice(device));
+  uint32_t v = 0;
+  const uint32_t zero = 0;
+  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+  if (e == hipSuccess) e = hipMemcpy(&v, word, sizeof(v), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  if (prev != device) (void)hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(e, what);
+  *status_out = v;
+  return MPS_OK;
+}
+
 }  // namespace mps
 
 using namespace mps;
 
+namespace {
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
+}  // namespace
+
+// A plan owns one device allocation: its status word, the tensor descriptors,
+// the lane checkpoints of the buckets it split, the work records and (during
+// creation) the checkpoint jobs and their failure flags.
 struct mps_fp8_plan {
+  void *d_block = nullptr;
+  uint32_t *d_status = nullptr;
   mps_fp8_tensor *d_tensors = nullptr;
   WorkItem *d_work = nullptr;
-  uint32_t *d_ckpt = nullptr;  // lane checkpoints of the buckets split into row ranges
   int64_t count = 0;
   int64_t work_items = 0;
   int device = 0;
@@ -1449,11 +1483,19 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream) 
   return MPS_OK;
 }
 
-int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_plan **plan_out) {
+int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stream, mps_fp8_plan **plan_out) {
   last_error().clear();
   if (!plan_out) return fail(MPS_ERR_INVALID_ARGUMENT, "plan_out is NULL");
   *plan_out = nullptr;
   if (count < 0 || (count > 0 && !tensors)) return fail(MPS_ERR_INVALID_ARGUMENT, "invalid tensor list");
+  for (int64_t i = 0; i < count; ++i) {
+    const int rc = check_tensor(&tensors[i]);
+    if (rc != MPS_OK) return rc;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // The sidecars may still be being written by work on the caller's stream:
+  // everything below reads them after that work.
+  MPS_HIP_CHECK(hipStreamSynchronize(st));
   // One work record per bucket.
   std::vector<WorkItem> bucket;
   std::vector<int64_t> elems;  // elements of each bucket (0: a bad bucket)
@@ -1461,8 +1503,6 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
   std::vector<int64_t> bbase;
   for (int64_t i = 0; i < count; ++i) {
     const mps_fp8_tensor &T = tensors[i];
-    int rc = check_tensor(&T);
-    if (rc != MPS_OK) return rc;
     const int64_t nb = T.num_buckets;
     if (nb == 0) continue;
     roff.resize((size_t)nb + 1);
@@ -1492,20 +1532,9 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
     }
   }
   if (bucket.size() > (size_t)INT32_MAX) return fail(MPS_ERR_INVALID_ARGUMENT, "too many buckets for one plan");
-  auto *p = new mps_fp8_plan();
-  p->count = count;
-  auto cleanup = [&](hipError_t e) {
-    if (p->d_tensors) (void)hipFree(p->d_tensors);
-    if (p->d_work) (void)hipFree(p->d_work);
-    if (p->d_ckpt) (void)hipFree(p->d_ckpt);
-    delete p;
-    return hip_fail(e, "mps_fp8_plan_create");
-  };
-  hipError_t e = hipGetDevice(&p->device);
-  if (e == hipSuccess && count > 0) e = hipMalloc(&p->d_tensors, sizeof(mps_fp8_tensor) * count);
-  if (e == hipSuccess && count > 0)
-    e = hipMemcpy(p->d_tensors, tensors, sizeof(mps_fp8_tensor) * count, hipMemcpyHostToDevice);
-  if (e != hipSuccess) return cleanup(e);
+  int device = 0, cus = 0;
+  MPS_HIP_CHECK(hipGetDevice(&device));
+  MPS_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
 
   // Row ranges. A plan whose buckets are few or uneven for the CUs (a layer,
   // a single tensor) would leave CUs idle behind its largest buckets: buckets
@@ -1513,17 +1542,15 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
   // split into row ranges of at most that size (and at least 64 elements per
   // substream, 16 groups, so that a range's set-up stays small beside its
   // decode). Each range starts from lane checkpoints (fp8_checkpoints).
-  int cus = 0;
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device);
-  if (e != hipSuccess) return cleanup(e);
   int64_t total = 0;
   for (int64_t x : elems) total += x;
   const int64_t cap = std::max<int64_t>(total / (2 * (int64_t)std::max(cus, 1)), 65536);
   std::vector<SplitJob> jobs;
   std::vector<size_t> job_of(bucket.size(), SIZE_MAX);
-  int64_t ck_words = 0;
+  int64_t ck_words = 0, max_items = 0;
   for (size_t i = 0; i < bucket.size(); ++i) {
     const WorkItem &w = bucket[i];
+    ++max_items;
     if ((w.path != kPathK1024 && w.path != kPathFast) || elems[i] <= cap || w.rows < 2) continue;
     const int32_t P = w.cl / w.k_eff;
     const int32_t min_rows = std::max<int32_t>(1, (64 + P - 1) / P);
@@ -1548,27 +1575,52 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
     job_of[i] = jobs.size();
     jobs.push_back(j);
     ck_words += (ranges - 1) * w.k_eff;
+    max_items += ranges - 1;
   }
+
+  // The plan's device block.
+  const size_t o_tensors = kAlign;
+  const size_t o_ckpt = o_tensors + align_up(sizeof(mps_fp8_tensor) * (size_t)count);
+  const size_t o_jobs = o_ckpt + align_up(sizeof(uint32_t) * (size_t)ck_words);
+  const size_t o_failed = o_jobs + align_up(sizeof(SplitJob) * jobs.size());
+  const size_t o_work = o_failed + align_up(sizeof(uint32_t) * jobs.size());
+  const size_t bytes = o_work + sizeof(WorkItem) * (size_t)max_items;
+  auto *p = new (std::nothrow) mps_fp8_plan();
+  if (!p) return fail(MPS_ERR_NO_MEMORY, "out of memory");
+  p->count = count;
+  p->device = device;
+  hipError_t e = hipMalloc(&p->d_block, bytes);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(e, "mps_fp8_plan_create");
+  }
+  auto cleanup = [&](hipError_t err) {
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(p->d_block);
+    delete p;
+    return hip_fail(err, "mps_fp8_plan_create");
+  };
+  char *blk = static_cast<char *>(p->d_block);
+  p->d_status = reinterpret_cast<uint32_t *>(blk);
+  p->d_tensors = reinterpret_cast<mps_fp8_tensor *>(blk + o_tensors);
+  p->d_work = reinterpret_cast<WorkItem *>(blk + o_work);
+  uint32_t *d_ckpt = reinterpret_cast<uint32_t *>(blk + o_ckpt);
+  // Status word (zero), descriptors, jobs and their flags (zero): one copy, on the caller's stream.
+  std::vector<char> head(o_work, 0);
+  if (count > 0) std::memcpy(head.data() + o_tensors, tensors, sizeof(mps_fp8_tensor) * (size_t)count);
+  if (!jobs.empty()) std::memcpy(head.data() + o_jobs, jobs.data(), sizeof(SplitJob) * jobs.size());
+  e = hipMemcpyAsync(blk, head.data(), head.size(), hipMemcpyHostToDevice, st);
   std::vector<uint32_t> failed(jobs.size(), 0u);
-  if (!jobs.empty()) {
-    SplitJob *d_jobs = nullptr;
-    uint32_t *d_failed = nullptr;
-    e = hipMalloc(&p->d_ckpt, sizeof(uint32_t) * (size_t)ck_words);
-    if (e == hipSuccess) e = hipMalloc(&d_jobs, sizeof(SplitJob) * jobs.size());
-    if (e == hipSuccess) e = hipMalloc(&d_failed, sizeof(uint32_t) * jobs.size());
-    if (e == hipSuccess) e = hipMemcpy(d_jobs, jobs.data(), sizeof(SplitJob) * jobs.size(), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(d_failed, failed.data(), sizeof(uint32_t) * jobs.size(), hipMemcpyHostToDevice);
-    if (e == hipSuccess) {
-      // the legacy default stream: ordered after the work that wrote the sidecars
-      hipLaunchKernelGGL(fp8_checkpoints, dim3((unsigned)jobs.size()), dim3(kBlock), 0, 0, p->d_tensors, d_jobs,
-                         p->d_ckpt, d_failed);
-      e = hipGetLastError();
-    }
-    if (e == hipSuccess) e = hipMemcpy(failed.data(), d_failed, sizeof(uint32_t) * jobs.size(), hipMemcpyDeviceToHost);
-    if (d_jobs) (void)hipFree(d_jobs);
-    if (d_failed) (void)hipFree(d_failed);
-    if (e != hipSuccess) return cleanup(e);
+  if (e == hipSuccess && !jobs.empty()) {
+    hipLaunchKernelGGL(fp8_checkpoints, dim3((unsigned)jobs.size()), dim3(kBlock), 0, st, p->d_tensors,
+                       reinterpret_cast<const SplitJob *>(blk + o_jobs), d_ckpt,
+                       reinterpret_cast<uint32_t *>(blk + o_failed));
+    e = hipGetLastError();
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(failed.data(), blk + o_failed, sizeof(uint32_t) * jobs.size(), hipMemcpyDeviceToHost, st);
   }
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return cleanup(e);
 
   // Work items (buckets and ranges), largest first: the persistent launch
   // deals them round-robin to the CUs, which then finish at about the same
@@ -1583,7 +1635,7 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
       continue;
     }
     const SplitJob &j = jobs[job_of[i]];
-    const uint32_t *ck = p->d_ckpt + j.out;
+    const uint32_t *ck = d_ckpt + j.out;
     for (int32_t r = 0; r < j.ranges; ++r) {
       WorkItem x = w;
       x.rows = std::min(j.range_rows, w.rows - r * j.range_rows);
@@ -1603,28 +1655,40 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, mps_fp8_pl
     work.swap(sorted);
   }
   p->work_items = (int64_t)work.size();
-  if (!work.empty()) e = hipMalloc(&p->d_work, sizeof(WorkItem) * work.size());
-  if (e == hipSuccess && !work.empty())
-    e = hipMemcpy(p->d_work, work.data(), sizeof(WorkItem) * work.size(), hipMemcpyHostToDevice);
-  if (e != hipSuccess) return cleanup(e);
+  if (!work.empty()) {
+    e = hipMemcpyAsync(p->d_work, work.data(), sizeof(WorkItem) * work.size(), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return cleanup(e);
+  }
   *plan_out = p;
   return MPS_OK;
 }
 
+namespace {
+int plan_launch(mps_fp8_plan *plan, uint16_t *out0, void *stream) {
+  if (plan->work_items == 0) return MPS_OK;
+  unsigned grid = 0;
+  const int rc = persistent_grid(plan->work_items, &grid);
+  if (rc != MPS_OK) return rc;
+  hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
+                     plan->d_tensors, plan->d_work, plan->work_items, plan->d_status, out0);
+  MPS_HIP_CHECK(hipGetLastError());
+  return MPS_OK;
+}
+}  // namespace
+
 int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream) {
   last_error().clear();
   if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
-  if (plan->work_items == 0) return MPS_OK;
-  uint32_t *status = nullptr;
-  int rc = status_word(plan->device, &status);
-  if (rc != MPS_OK) return rc;
-  unsigned grid = 0;
-  rc = persistent_grid(plan->work_items, &grid);
-  if (rc != MPS_OK) return rc;
-  hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                     plan->d_tensors, plan->d_work, plan->work_items, status);
-  MPS_HIP_CHECK(hipGetLastError());
-  return MPS_OK;
+  return plan_launch(plan, nullptr, stream);
+}
+
+int mps_fp8_plan_decode_into(mps_fp8_plan *plan, uint16_t *out, void *stream) {
+  last_error().clear();
+  if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (!out) return fail(MPS_ERR_INVALID_ARGUMENT, "out is NULL");
+  if (plan->count != 1) return fail(MPS_ERR_INVALID_ARGUMENT, "decode into another output needs a plan of one tensor");
+  return plan_launch(plan, out, stream);
 }
 
 int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes) {
@@ -1634,11 +1698,16 @@ int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *ld
   return MPS_OK;
 }
 
+int mps_fp8_plan_read_status(mps_fp8_plan *plan, void *stream, uint32_t *status_out) {
+  last_error().clear();
+  if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (!status_out) return fail(MPS_ERR_INVALID_ARGUMENT, "status_out is NULL");
+  return read_and_clear(plan->device, plan->d_status, stream, "mps_fp8_plan_read_status", status_out);
+}
+
 int mps_fp8_plan_destroy(mps_fp8_plan *plan) {
   if (!plan) return MPS_OK;
-  if (plan->d_tensors) (void)hipFree(plan->d_tensors);
-  if (plan->d_work) (void)hipFree(plan->d_work);
-  if (plan->d_ckpt) (void)hipFree(plan->d_ckpt);
+  if (plan->d_block) (void)hipFree(plan->d_block);
   delete plan;
   return MPS_OK;
 }
@@ -1647,20 +1716,9 @@ int mps_fp8_read_status(int device, void *stream, uint32_t *status_out) {
   last_error().clear();
   if (!status_out) return fail(MPS_ERR_INVALID_ARGUMENT, "status_out is NULL");
   uint32_t *word = nullptr;
-  int rc = status_word(device, &word);
+  const int rc = status_word(device, &word);
   if (rc != MPS_OK) return rc;
-  int prev = 0;
-  MPS_HIP_CHECK(hipGetDevice(&prev));
-  if (prev != device) MPS_HIP_CHECK(hipSetDevice(device));
-  uint32_t v = 0;
-  const uint32_t zero = 0;
-  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
-  if (e == hipSuccess) e = hipMemcpy(&v, word, sizeof(v), hipMemcpyDeviceToHost);
-  if (e == hipSuccess) e = hipMemcpy(word, &zero, sizeof(zero), hipMemcpyHostToDevice);
-  if (prev != device) (void)hipSetDevice(prev);
-  if (e != hipSuccess) return hip_fail(e, "mps_fp8_read_status");
-  *status_out = v;
-  return MPS_OK;
+  return read_and_clear(device, word, stream, "mps_fp8_read_status", status_out);
 }
 
 }  // extern "C"

@@ -28,9 +28,12 @@ inline int hip_fail(hipError_t e, const char *what) {
   return fail(MPS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// The per-device word the decode kernels OR their MPS_STATUS_* flags into
-// (allocated on first use, kept for the life of the process).
+// The per-device word the single-tensor decode kernels OR their MPS_STATUS_*
+// flags into: a module global (nothing is allocated), per device, not per stream.
 int status_word(int device, uint32_t **out);
+
+// Read a device status word and clear it, after `stream`'s work (synchronous).
+int read_and_clear(int device, uint32_t *word, void *stream, const char *what, uint32_t *status_out);
 
 }  // namespace mps
 

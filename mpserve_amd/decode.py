@@ -56,10 +56,14 @@ class DecodePlan:
 
     ``items``: (fp8_u8 [n, m] uint8, sidecar mapping, out) with ``out`` a
     contiguous bfloat16 tensor of n*m elements; all on one device. The plan
-    keeps references to every tensor it points at.
+    keeps references to every tensor it points at. Creation synchronises
+    ``stream`` (default: the current stream), which may still be writing the
+    sidecars, and reads their bucket metadata; it allocates the plan's device
+    memory. Decodes allocate nothing and flag into the plan's own status word.
     """
 
-    def __init__(self, items: Iterable[Tuple[torch.Tensor, Mapping[str, torch.Tensor], torch.Tensor]]):
+    def __init__(self, items: Iterable[Tuple[torch.Tensor, Mapping[str, torch.Tensor], torch.Tensor]],
+                 stream: torch.cuda.Stream | None = None):
         self._keep = []
         descs = []
         device = None
@@ -81,8 +85,10 @@ class DecodePlan:
         arr = (_native.MpsFp8Tensor * max(1, self.count))(*descs)
         self._plan = ctypes.c_void_p()
         if device is not None:
+            h = stream.cuda_stream if stream is not None else _stream_handle(device)
             with torch.cuda.device(device):
-                _native.check(_native.lib().mps_fp8_plan_create(arr, self.count, ctypes.byref(self._plan)))
+                _native.check(_native.lib().mps_fp8_plan_create(arr, self.count, ctypes.c_void_p(h),
+                                                                ctypes.byref(self._plan)))
         self.outputs = [o for _, o in self._keep]
         self.bytes_out = sum(o.numel() * 2 for o in self.outputs)
 
@@ -94,6 +100,14 @@ class DecodePlan:
         with torch.cuda.device(self.device):
             _native.check(_native.lib().mps_fp8_plan_decode(self._plan, ctypes.c_void_p(h)))
         return self.outputs
+
+    def read_status(self, stream: torch.cuda.Stream | None = None) -> int:
+        """MPS_STATUS_* flags this plan's decodes recorded since the last read (synchronises)."""
+        v = ctypes.c_uint32(0)
+        if self._plan:
+            h = stream.cuda_stream if stream is not None else _stream_handle(self.device)
+            _native.check(_native.lib().mps_fp8_plan_read_status(self._plan, ctypes.c_void_p(h), ctypes.byref(v)))
+        return int(v.value)
 
     def info(self) -> Dict[str, int]:
         """Work items of a launch (buckets, or row ranges of buckets the plan split)

@@ -10,9 +10,12 @@ library the ops raise ImportError, and without a GPU they raise RuntimeError.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import os
-from typing import Dict
+import threading
+import weakref
+from typing import Dict, Optional, Sequence
 
 import torch
 
@@ -23,6 +26,7 @@ __all__ = [
     "huffman_build_fp8_decode_tables",
     "huffman_decode_fp8",
     "cuda_clock_rate_khz",
+    "clear_decode_plans",
     "SIDECAR_KEYS",
 ]
 
@@ -138,6 +142,113 @@ def validate_decode_args(fp8_params_u8, bitstream_u64, decode_syms_u16, decode_l
         raise ValueError("bucket_thread_startbit_u32 has invalid k (must be 1..1024)")
 
 
+class _TensorPlan:
+    """A device plan of one tensor that holds no reference to its tensors (the
+    cache entry that owns it checks they are alive before every use)."""
+
+    def __init__(self, desc: _native.MpsFp8Tensor, stream: int):
+        arr = (_native.MpsFp8Tensor * 1)(desc)
+        self.handle = ctypes.c_void_p()
+        _native.check(_native.lib().mps_fp8_plan_create(arr, 1, ctypes.c_void_p(stream), ctypes.byref(self.handle)))
+
+    def decode_into(self, out: torch.Tensor, stream: int) -> None:
+        _native.check(_native.lib().mps_fp8_plan_decode_into(self.handle, ctypes.c_void_p(out.data_ptr()),
+                                                             ctypes.c_void_p(stream)))
+
+    def close(self) -> None:
+        if self.handle:
+            _native.lib().mps_fp8_plan_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+
+class _SidecarPlans:
+    """Single-tensor decode plans behind huffman_decode_fp8, one per sidecar.
+
+    The reference decodes every call over whole buckets, one workgroup each
+    (decode_huffman.cu:699-739), so a tensor with few buckets for the CUs (a
+    70B k_proj has 8 for 256 CUs) runs on few CUs. A plan splits large buckets
+    into row ranges that start from lane checkpoints, but computing those
+    walks every substream once and synchronises. So the op decodes a sidecar's
+    first call over whole buckets, builds its plan on the second call, and
+    launches the plan from then on.
+
+    Invalidation rule. An entry is keyed by the device addresses of the FP8
+    tensor and the ten sidecar arrays, with n and m. For each of the eleven
+    tensors it keeps a weak reference to the tensor's storage and the tensor's
+    version counter (dtype views such as int64 -> uint64 share both with the
+    tensor they view). It is used only while every storage is alive and no
+    version has changed, so a sidecar that was freed (another may now sit at
+    the same addresses) or rewritten in place through torch gets a new plan. A writer that bypasses torch's version counters (another library
+    writing through the raw pointers) must call clear_decode_plans(). No plan
+    is built while the current stream captures a graph (building
+    synchronises); built plans launch there like any kernel. At most
+    ``capacity`` entries are kept, least recently used first out;
+    MPSERVE_DECODE_PLANS=0 turns the cache off.
+    """
+
+    def __init__(self, capacity: int = 256):
+        self.capacity = capacity
+        self._entries: "collections.OrderedDict[tuple, list]" = collections.OrderedDict()
+        self._lock = threading.Lock()
+
+    @staticmethod
+    def _valid(entry, tensors: Sequence[torch.Tensor]) -> bool:
+        refs, versions = entry[0], entry[1]
+        for r, v, t in zip(refs, versions, tensors):
+            if r() is not t.untyped_storage() or t._version != v:
+                return False
+        return True
+
+    def get(self, tensors: Sequence[torch.Tensor], n: int, m: int, desc: _native.MpsFp8Tensor,
+            device: torch.device, stream: int) -> Optional[_TensorPlan]:
+        """The sidecar's plan, building it on its second sighting; None: decode over whole buckets."""
+        if self.capacity <= 0 or os.environ.get("MPSERVE_DECODE_PLANS", "1") == "0":
+            return None
+        key = (device.index, n, m) + tuple(t.data_ptr() for t in tensors)
+        dropped = []
+        try:
+            with self._lock:
+                entry = self._entries.get(key)
+                if entry is not None and not self._valid(entry, tensors):
+                    dropped.append(self._entries.pop(key))
+                    entry = None
+                if entry is None:
+                    self._entries[key] = [[weakref.ref(t.untyped_storage()) for t in tensors],
+                                          [t._version for t in tensors], None]
+                    while len(self._entries) > self.capacity:
+                        dropped.append(self._entries.popitem(last=False)[1])
+                    return None
+                self._entries.move_to_end(key)
+                if entry[2] is None:
+                    if torch.cuda.is_current_stream_capturing():
+                        return None
+                    entry[2] = _TensorPlan(desc, stream)
+                return entry[2]
+        finally:
+            for e in dropped:
+                if e[2] is not None:
+                    e[2].close()
+
+    def clear(self) -> None:
+        with self._lock:
+            entries = list(self._entries.values())
+            self._entries.clear()
+        for e in entries:
+            if e[2] is not None:
+                e[2].close()
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+
+_PLANS = _SidecarPlans()
+
+
+def clear_decode_plans() -> None:
+    """Drop every cached per-sidecar plan of huffman_decode_fp8 (see _SidecarPlans)."""
+    _PLANS.clear()
+
+
 def huffman_decode_fp8(fp8_params_u8: torch.Tensor, bitstream_u64: torch.Tensor, decode_syms_u16: torch.Tensor,
                        decode_lens_u8: torch.Tensor, bucket_table_i32: torch.Tensor,
                        bucket_col_start_i32: torch.Tensor, bucket_col_len_i32: torch.Tensor,
@@ -148,25 +259,31 @@ def huffman_decode_fp8(fp8_params_u8: torch.Tensor, bitstream_u64: torch.Tensor,
 
     Runs on the current stream of the FP8 tensor's device. ``out`` (keyword
     only, not in the reference) decodes into a caller-owned contiguous BF16
-    buffer of n*m elements, e.g. a preallocated scratch weight.
+    buffer of n*m elements, e.g. a preallocated scratch weight. From its
+    second call on a sidecar the op launches a cached plan of that sidecar
+    (_SidecarPlans); the second call synchronises the stream once.
     """
     n = int(n)
     m = int(m)
     max_len = int(max_len)
-    validate_decode_args(fp8_params_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32,
-                         bucket_col_start_i32, bucket_col_len_i32, bucket_row_offsets_i32, row_indices_i32,
-                         bucket_thread_startbit_u32, bucket_bit_base_i64, n, m, max_len)
+    tensors = (fp8_params_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32,
+               bucket_col_start_i32, bucket_col_len_i32, bucket_row_offsets_i32, row_indices_i32,
+               bucket_thread_startbit_u32, bucket_bit_base_i64)
+    validate_decode_args(*tensors, n, m, max_len)
     dev = fp8_params_u8.device
     if out is None:
         out = torch.empty((n, m), dtype=torch.bfloat16, device=dev)
     else:
         if out.dtype != torch.bfloat16 or out.device != dev or not out.is_contiguous() or out.numel() != n * m:
             raise ValueError("out must be a contiguous bfloat16 tensor of n*m elements on the fp8 device")
-    d = _descriptor(fp8_params_u8, bitstream_u64, decode_syms_u16, decode_lens_u8, bucket_table_i32,
-                    bucket_col_start_i32, bucket_col_len_i32, bucket_row_offsets_i32, row_indices_i32,
-                    bucket_thread_startbit_u32, bucket_bit_base_i64, n, m, out)
+    d = _descriptor(*tensors, n, m, out)
     with torch.cuda.device(dev):
-        _native.check(_native.lib().mps_fp8_decode(ctypes.byref(d), max_len, ctypes.c_void_p(_stream_handle(dev))))
+        stream = _stream_handle(dev)
+        plan = _PLANS.get(tensors, n, m, d, dev, stream) if bucket_table_i32.size(0) > 0 else None
+        if plan is not None:
+            plan.decode_into(out, stream)
+        else:
+            _native.check(_native.lib().mps_fp8_decode(ctypes.byref(d), max_len, ctypes.c_void_p(stream)))
     _maybe_check_status(dev)
     return out
 

@@ -255,7 +255,7 @@ def test_plan_decodes_mixed_layouts_in_one_launch():
         torch.cuda.synchronize()
         for o, s in zip(plan.outputs, srcs):
             assert torch.equal(o.view(torch.uint16), s.view(torch.uint16))
-    assert read_status(torch.device(DEV)) == 0
+    assert plan.read_status() == 0
     plan.close()
     assert awq.AwqDecodePlan([]).decode() == []
 

@@ -215,18 +215,18 @@ def test_plan_decodes_many_tensors():
         torch.cuda.synchronize()
         for o, r in zip(outs, refs):
             assert np.array_equal(o.view(torch.uint16).cpu().numpy(), r)
-    assert _status() == 0
+    assert plan.read_status() == 0
 
 
 def test_integrity_flags_on_corrupt_sidecar():
-    """Corrupt lane starts / row indices / table ids are flagged, never written out of bounds."""
+    """Corrupt lane starts / row indices / table ids are flagged (writes are checked
+    against the output's bounds in test_corrupt_sidecar_writes_stay_inside_out)."""
     import MPServe_cuda
 
     n, m = 256, 1024
     bf, q, sc_u16 = synth(n, m, seed=71)
     sc = oracle.encode(bf, q, sc_u16, 7, 1024)
     q_t = torch.from_numpy(q).to(DEV)
-    guard = torch.zeros(4096, dtype=torch.uint16, device=DEV)
 
     bad = {k: v.copy() for k, v in sc.items()}
     bad["bucket_thread_startbit_u32"][0, 5] += 3
@@ -242,11 +242,12 @@ def test_integrity_flags_on_corrupt_sidecar():
     bad["bucket_table_i32"][0, 10] = 10 ** 8
     MPServe_cuda.huffman_decode_fp8(*decode_args(to_torch(bad, DEV), q_t))
     assert _status() & 0x4
-    assert int(guard.sum().item()) == 0 and out.shape == (n, m)
+    assert out.shape == (n, m)
 
 
 def _plan_decode(items):
-    """Decode [(bf16 ref or None, fp8 u8 numpy, oracle sidecar)] in one plan; (outputs, plan info)."""
+    """Decode [(bf16 ref or None, fp8 u8 numpy, oracle sidecar)] in one plan;
+    (outputs, plan info, the plan's status flags)."""
     from mpserve_amd.decode import DecodePlan
 
     dev_items = []
@@ -256,7 +257,7 @@ def _plan_decode(items):
     plan = DecodePlan(dev_items)
     plan.decode()
     torch.cuda.synchronize()
-    return [o.view(torch.uint16).cpu().numpy() for _, _, o in dev_items], plan.info()
+    return [o.view(torch.uint16).cpu().numpy() for _, _, o in dev_items], plan.info(), plan.read_status()
 
 
 @pytest.mark.parametrize("case", ["slab_p8", "slab_wrap_p14", "esc_k1024", "fast_k256", "mixed"])
@@ -285,12 +286,11 @@ def test_plan_splits_buckets_into_row_ranges(case):
                  (b[0], b[1], oracle.encode(b[0], b[1], b[2], 7, 1024)),
                  (c[0], c[1], oracle.encode(c[0], c[1], c[2], 7, 1024))]
     buckets = sum(sc["bucket_table_i32"].shape[0] for _, _, sc in items)
-    _status()
-    outs, info = _plan_decode(items)
+    outs, info, status = _plan_decode(items)
     assert info["work_items"] > buckets
     for (bf, _, _), got in zip(items, outs):
         assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
-    assert _status() == 0
+    assert status == 0
 
 
 def test_plan_split_with_bad_row_keeps_bucket_whole():
@@ -301,5 +301,131 @@ def test_plan_split_with_bad_row_keeps_bucket_whole():
     bad = {k: v.copy() for k, v in side.items()}
     bad["row_indices_i32"][130] = 10 ** 6
     _status()
-    outs, info = _plan_decode([(None, q, bad)])
-    assert _status() & 0x2
+    outs, info, status = _plan_decode([(None, q, bad)])
+    assert status & 0x2
+    assert _status() == 0  # a plan's flags go to its own word, not the device's
+
+
+def test_op_plan_cache_alternating_sidecars():
+    """huffman_decode_fp8 keeps one plan per sidecar from its second call on: two
+    sidecars alternated through the op (fresh dtype views each call, as the
+    reference's apply() passes them) decode bit-exact on every call, and an
+    in-place rewrite of one sidecar's tensor (its version changes) drops that
+    sidecar's plan until it is seen twice again."""
+    import MPServe_cuda
+    from mpserve_amd import mpserve_cuda as mc
+
+    mc.clear_decode_plans()
+    cases = []
+    for n, m, scalar, seed in ((256, 8192, True, 90), (1024, 4096, False, 91)):
+        bf, q, sc_u16 = synth(n, m, seed=seed)
+        sc = oracle.encode(bf, q, sc_u16[:1].copy() if scalar else sc_u16, 7, 1024)
+        stored = to_torch(sc, DEV)
+        stored["bitstream_u64"] = stored["bitstream_u64"].view(torch.int64)  # stored signed, like safetensors
+        cases.append((stored, torch.from_numpy(q).to(DEV), bf))
+    _status()
+    for call in range(4):
+        for stored, q_t, bf in cases:
+            args = list(decode_args(stored, q_t))
+            args[1] = stored["bitstream_u64"].view(torch.uint64)  # a new view object every call
+            out = MPServe_cuda.huffman_decode_fp8(*args)
+            torch.cuda.synchronize()
+            assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf), f"call {call}"
+        assert _status() == 0
+    entries = list(mc._PLANS._entries.values())
+    assert len(entries) == 2 and all(e[2] is not None for e in entries)
+    # the few-bucket sidecar's plan splits its 2 buckets into row ranges
+    wi = ctypes_work_items(entries[0][2])
+    assert wi > 2
+    stored, q_t, bf = cases[1]
+    q_t.copy_(q_t.clone())  # same bytes, new version
+    out = MPServe_cuda.huffman_decode_fp8(*decode_args(stored, q_t)[:1], stored["bitstream_u64"].view(torch.uint64),
+                                          *decode_args(stored, q_t)[2:])
+    torch.cuda.synchronize()
+    assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf)
+    assert sum(e[2] is None for e in mc._PLANS._entries.values()) == 1
+    mc.clear_decode_plans()
+    assert len(mc._PLANS) == 0
+
+
+def ctypes_work_items(plan) -> int:
+    import ctypes
+
+    from mpserve_amd import _native
+
+    wi, lds = ctypes.c_int64(0), ctypes.c_int64(0)
+    _native.check(_native.lib().mps_fp8_plan_info(plan.handle, ctypes.byref(wi), ctypes.byref(lds)))
+    return int(wi.value)
+
+
+def test_corrupt_sidecar_writes_stay_inside_out():
+    """Decoding corrupt sidecars into the middle of a larger buffer (op, then a
+    plan): the flags are raised and the words around the output stay zero."""
+    import MPServe_cuda
+    from mpserve_amd.decode import DecodePlan
+
+    n, m = 256, 1024
+    bf, q, sc_u16 = synth(n, m, seed=72)
+    sc = oracle.encode(bf, q, sc_u16, 7, 1024)
+    q_t = torch.from_numpy(q).to(DEV)
+    guard = 4096
+    corruptions = [
+        ("start bit", 0x8, lambda b: b["bucket_thread_startbit_u32"].__setitem__((0, 5), b["bucket_thread_startbit_u32"][0, 5] + 3)),
+        ("row index", 0x2, lambda b: b["row_indices_i32"].__setitem__(3, n + 1000)),
+        ("table id", 0x4, lambda b: b["bucket_table_i32"].__setitem__((0, 10), 10 ** 8)),
+        ("bit base", 0x8, lambda b: b["bucket_bit_base_i64"].__setitem__(1, b["bucket_bit_base_i64"][1] + 64 * 5000)),
+    ]
+    for what, flag_bit, corrupt in corruptions:
+        bad = {k: v.copy() for k, v in sc.items()}
+        corrupt(bad)
+        bad_t = to_torch(bad, DEV)
+        for via in ("op", "plan"):
+            buf = torch.zeros(n * m + 2 * guard, dtype=torch.bfloat16, device=DEV)
+            out = buf[guard:guard + n * m]
+            _status()
+            if via == "op":
+                MPServe_cuda.huffman_decode_fp8(*decode_args(bad_t, q_t), out=out)
+                st = _status()
+            else:
+                plan = DecodePlan([(q_t, bad_t, out)])
+                plan.decode()
+                st = plan.read_status()
+                plan.close()
+            torch.cuda.synchronize()
+            assert st & flag_bit, (what, via, st)
+            g = buf.view(torch.uint16)
+            assert int((g[:guard] != 0).sum()) == 0 and int((g[guard + n * m:] != 0).sum()) == 0, (what, via)
+
+
+def test_plan_creation_waits_for_the_stream_writing_the_sidecar():
+    """A plan built on the stream that is still writing its sidecar (behind a long
+    kernel) reads the finished sidecar: creation synchronises that stream."""
+    from mpserve_amd.decode import DecodePlan
+
+    n, m = 128, 8192
+    bf, q, sc_u16 = synth(n, m, seed=73)
+    good = to_torch(oracle.encode(bf, q, sc_u16[:1].copy(), 7, 1024), DEV)
+    dst = {k: torch.zeros_like(v) for k, v in good.items()}
+    q_t = torch.from_numpy(q).to(DEV)
+    out = torch.zeros((n, m), dtype=torch.bfloat16, device=DEV)
+    busy = torch.randn((2048, 2048), device=DEV)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        for _ in range(30):
+            busy = torch.tanh(busy @ busy)
+        for k in dst:
+            dst[k].copy_(good[k])
+    plan = DecodePlan([(q_t, dst, out)], stream=side)
+    plan.decode(side)
+    side.synchronize()
+    assert plan.info()["work_items"] > 1
+    assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf)
+    assert plan.read_status(side) == 0
+
+
+def test_cuda_clock_rate_khz():
+    import MPServe_cuda
+
+    khz = MPServe_cuda.cuda_clock_rate_khz()
+    assert isinstance(khz, int) and khz > 0

@@ -104,4 +104,5 @@ def test_gpu_plan_decodes_all_fixtures():
         torch.cuda.synchronize()
         for (_, _, o), bf in zip(items, refs):
             assert np.array_equal(o.view(torch.uint16).cpu().numpy(), bf)
-    assert read_status(torch.device(DEV)) == 0
+    assert plan.read_status() == 0
+    assert read_status(torch.device(DEV)) == 0  # plans flag into their own word
