@@ -104,6 +104,20 @@ int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *ld
 int mps_fp8_plan_read_status(mps_fp8_plan *plan, void *stream, uint32_t *status_out);
 int mps_fp8_plan_destroy(mps_fp8_plan *plan);
 
+/* Allocation-free batched decode: decodes `count` tensors (at most 1024, with
+ * at most 63,104 buckets in all) in one persistent launch, as a plan would,
+ * but without creating one. It calls no hipMalloc, hipFree or other
+ * allocating routine and does not synchronise: the descriptors (read from the
+ * host array before the call returns) and one work record per bucket go into
+ * a static device array of 4 MiB that each device holds from library load to
+ * the end of the process. Buckets are not split into row ranges. Flags go to
+ * the device status word (mps_fp8_read_status). Calls that overlap on one
+ * device share that array and race: issue them on one stream, or order them.
+ * Larger inputs are rejected with MPS_ERR_INVALID_ARGUMENT before any work.
+ * No counterpart in the reference; it serves callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops). */
+int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, int64_t max_len, void *stream);
+
 /* Inputs of the GPU sidecar builder, all device pointers: BF16 bit patterns
  * and FP8 bytes of the same tensor (`numel` elements, shape dims[0..ndim)),
  * and the u16 scale keys (shape scale_dims[0..scale_ndim), scale_numel

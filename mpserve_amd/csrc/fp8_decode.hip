@@ -1355,6 +1355,90 @@ __global__ __launch_bounds__(kBlock) void fp8_checkpoints(const mps_fp8_tensor *
   }
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free batched decode. Some callers cannot allocate device memory
+// (code under graph capture, tight serving loops). For them
+// mps_fp8_decode_batch_noalloc decodes a list of tensors in one persistent
+// launch, like a plan, with its descriptors and work records in `scratch`, a
+// static device array of kScratchBytes that each device holds from module
+// load to the end of the process. Buckets are not split into row ranges
+// (that needs lane checkpoints, which a plan computes once).
+//
+// Layout of `scratch`: the descriptors (at most kMaxBatchTensors), then one
+// 64-byte work record per bucket (at most kMaxBatchWork).
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(4) << 20;
+constexpr int64_t kMaxBatchTensors = 1024;
+constexpr size_t kBatchWorkOff = ((sizeof(mps_fp8_tensor) * kMaxBatchTensors + 255) / 256) * 256;
+constexpr int64_t kMaxBatchWork = (int64_t)((kScratchBytes - kBatchWorkOff) / sizeof(WorkItem));
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// One work record per bucket, in tensor order. Every workgroup first scans the
+// bucket counts of the (at most 1024) tensors in LDS, then each work-item
+// writes the record of one bucket from that bucket's metadata.
+__global__ __launch_bounds__(256) void fp8_batch_records(const mps_fp8_tensor *__restrict__ tensors, int32_t count,
+                                                        int64_t total, WorkItem *__restrict__ work) {
+  constexpr int kPer = kMaxBatchTensors / 256;  // tensors per work-item in the scan
+  __shared__ int64_t s_first[kMaxBatchTensors + 1];
+  __shared__ int64_t s_part[256];
+  const int t = threadIdx.x;
+  int64_t v[kPer], sum = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int32_t i = t * kPer + j;
+    v[j] = i < count ? tensors[i].num_buckets : 0;
+    sum += v[j];
+  }
+  s_part[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan of the 256 partial sums
+    const int64_t add = t >= off ? s_part[t - off] : 0;
+    __syncthreads();
+    s_part[t] += add;
+    __syncthreads();
+  }
+  int64_t acc = s_part[t] - sum;  // exclusive prefix of this work-item's tensors
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    s_first[t * kPer + j] = acc;
+    acc += v[j];
+  }
+  if (t == 255) s_first[kMaxBatchTensors] = acc;
+  __syncthreads();
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= total) return;
+  int32_t lo = 0, hi = count - 1;  // the tensor i with s_first[i] <= g < s_first[i + 1]
+  while (lo < hi) {
+    const int32_t mid = (lo + hi + 1) >> 1;
+    if (s_first[mid] <= g) lo = mid;
+    else hi = mid - 1;
+  }
+  const mps_fp8_tensor &T = tensors[lo];
+  WorkItem w = bucket_item(T, g - s_first[lo]);
+  w.tensor = lo;
+  work[g] = w;
+}
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the host-side name of a device array is not its address).
+int scratch_ptr(uint8_t **out) {
+  static std::mutex mu;
+  static uint8_t *ptrs[kMaxDevices] = {};
+  int dev = 0;
+  MPS_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MPS_ERR_INVALID_ARGUMENT, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    ptrs[dev] = static_cast<uint8_t *>(p);
+  }
+  *out = ptrs[dev];
+  return MPS_OK;
+}
+
 // Workgroups of a persistent launch on the current device: one per CU.
 int persistent_grid(int64_t items, unsigned *grid) {
   int dev = 0, cus = 0;
@@ -1719,6 +1803,51 @@ int mps_fp8_read_status(int device, void *stream, uint32_t *status_out) {
   const int rc = status_word(device, &word);
   if (rc != MPS_OK) return rc;
   return read_and_clear(device, word, stream, "mps_fp8_read_status", status_out);
+}
+
+
+int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, int64_t max_len, void *stream) {
+  last_error().clear();
+  if (max_len != kL) return fail(MPS_ERR_INVALID_ARGUMENT, "decode kernel is specialized: max_len must be 7");
+  if (count < 0 || (count > 0 && !tensors)) return fail(MPS_ERR_INVALID_ARGUMENT, "invalid tensor list");
+  if (count > kMaxBatchTensors)
+    return fail(MPS_ERR_INVALID_ARGUMENT,
+                "mps_fp8_decode_batch_noalloc: %lld tensors exceed its static scratch (at most %lld)",
+                (long long)count, (long long)kMaxBatchTensors);
+  int64_t total = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const int rc = check_tensor(&tensors[i]);
+    if (rc != MPS_OK) return rc;
+    total += tensors[i].num_buckets;
+  }
+  if (total > kMaxBatchWork)
+    return fail(MPS_ERR_INVALID_ARGUMENT,
+                "mps_fp8_decode_batch_noalloc: %lld buckets exceed its static scratch (at most %lld)",
+                (long long)total, (long long)kMaxBatchWork);
+  if (total == 0) return MPS_OK;
+  int dev = 0;
+  MPS_HIP_CHECK(hipGetDevice(&dev));
+  uint32_t *status = nullptr;
+  int rc = status_word(dev, &status);
+  if (rc != MPS_OK) return rc;
+  uint8_t *base = nullptr;
+  rc = scratch_ptr(&base);
+  if (rc != MPS_OK) return rc;
+  auto *d_tensors = reinterpret_cast<mps_fp8_tensor *>(base);
+  auto *d_work = reinterpret_cast<WorkItem *>(base + kBatchWorkOff);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // The descriptors are read from the caller's host array before this returns.
+  MPS_HIP_CHECK(hipMemcpyAsync(d_tensors, tensors, sizeof(mps_fp8_tensor) * (size_t)count, hipMemcpyHostToDevice, st));
+  hipLaunchKernelGGL(fp8_batch_records, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, d_tensors,
+                     (int32_t)count, total, d_work);
+  MPS_HIP_CHECK(hipGetLastError());
+  unsigned grid = 0;
+  rc = persistent_grid(total, &grid);
+  if (rc != MPS_OK) return rc;
+  hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, st, d_tensors, d_work, total, status,
+                     static_cast<uint16_t *>(nullptr));
+  MPS_HIP_CHECK(hipGetLastError());
+  return MPS_OK;
 }
 
 }  // extern "C"
