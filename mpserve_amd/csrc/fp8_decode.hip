@@ -691,8 +691,8 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, uint16_t *
 }
 
 // ---------------------------------------------------------------------------
-// k = 1024, col_len = P * 1024 with P >= 4, no ESC entry in the bucket's
-// tables (every bucket of a Llama-shaped checkpoint).
+// k = 1024, col_len = P * 1024 with P >= 4 (every bucket of a Llama-shaped
+// checkpoint).
 //
 // Element i of a substream lives in slab i: the 1024 columns
 // [c0 + 1024 (i % P), +1024) of the bucket's row i / P. Lane l of wave w,
@@ -725,8 +725,16 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, uint16_t *
 // slot), and positions are kept negated (np = -p, p biased by two chunks as
 // in decode_k1024), so the window's slot addresses and its funnel shift come
 // straight from np.
+//
+// ESC (kEsc: the bucket's tables hold ESC entries). An ESC entry's low half is
+// 16 + len, so the running shift already steps over the 16 raw bits that
+// follow the code; but four codes with ESC payloads can need more than one
+// 32-bit window. A lane whose group holds an ESC code (one ballot per group)
+// decodes that group again one code at a time, a window per code, taking the
+// symbol from the 16 raw bits. ESC codes are rare (the symbols a key's
+// 127 most frequent leave out), so the wave almost never takes that branch.
 // ---------------------------------------------------------------------------
-template <bool kWrap>
+template <bool kWrap, bool kEsc>
 __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *out, const uint32_t *__restrict__ lut,
                                              uint32_t *__restrict__ queue, uint32_t lane, uint32_t rows, uint32_t P,
                                              uint32_t rowoff_lo, uint32_t rowoff_hi, uint64_t bucket_bit,
@@ -919,6 +927,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
     const uint32_t gq = __builtin_amdgcn_perm(p1[1], p1[0], selA);
     const auto p2 = __builtin_amdgcn_permlane16_swap(gq, gq, false, false);
     const uint32_t fq = __builtin_amdgcn_perm(p2[1], p2[0], selB);  // byte j = element j's FP8 byte
+    const uint32_t np0 = np;
     const uint32_t win = window(np);
     uint32_t e[4];
     uint32_t s = 23u;
@@ -934,6 +943,31 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
       }
     }
     np += (uint32_t)((int32_t)(s << 16) >> 16) - 23u;  // minus the bits consumed
+    if constexpr (kEsc) {
+      // The first ESC code of the group is read from the right place, so its
+      // flag is seen even when the window does not reach the codes after it.
+      const bool esc = ((e[0] | e[1] | e[2] | e[3]) & kEscBit) != 0u;
+      if (__builtin_amdgcn_ballot_w64(esc)) {
+        if (esc) {
+          uint32_t p = np0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (!kTail || (uint32_t)j < tail) {
+              const uint32_t q9 = ((fq >> (8 * j)) & 0xFFu) << 9;
+              const uint32_t w = window(p);
+              uint32_t ent = *reinterpret_cast<const uint32_t *>(lbytes + (((w >> 23) & 0x1FCu) | q9));
+              p -= ent & 7u;
+              if (ent & kEscBit) {
+                ent = window(p) & 0xFFFF0000u;  // the symbol: the 16 raw bits after the code
+                p -= 16u;
+              }
+              e[j] = ent;
+            }
+          }
+          np = p;
+        }
+      }
+    }
     const auto t0 = __builtin_amdgcn_permlane32_swap(e[0], e[2], false, false);
     const auto t1 = __builtin_amdgcn_permlane32_swap(e[1], e[3], false, false);
     const uint32_t a = __builtin_amdgcn_perm(t0[1], t0[0], 0x07060302u);
@@ -1186,13 +1220,18 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   if (!active) return;
   if (k1024) {
     const uint32_t P = (uint32_t)cl / 1024u;
-    if (!has_esc && P >= 4) {
-      if (P % 4 == 0)
-        decode_slab4<false>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
-                            pos, pos_end, status);
-      else
-        decode_slab4<true>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, first,
-                           pos, pos_end, status);
+    if (P >= 4) {
+#define MPS_SLAB(WRAP, ESC)                                                                                \
+  decode_slab4<WRAP, ESC>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, \
+                          first, pos, pos_end, status)
+      if (P % 4 == 0) {
+        if (has_esc) MPS_SLAB(false, true);
+        else MPS_SLAB(false, false);
+      } else {
+        if (has_esc) MPS_SLAB(true, true);
+        else MPS_SLAB(true, false);
+      }
+#undef MPS_SLAB
       return;
     }
 #define MPS_K1024(GG)                                                                                     \

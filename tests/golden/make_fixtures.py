@@ -7,9 +7,10 @@ pinned by hand-traced vectors, brute force and invariants
 reference ships no fixtures of its own. The cases are chosen to reach every
 decode path and bucketing mode: per-row, scalar and block-2D scale keys; the
 k = 1024 slab path with P = 4 and with P = 14 (rows straddle groups); k = 1024
-with P < 4; tables with ESC codes; other k; and col_len < k.
+with P < 4; tables with ESC codes on the slab path at P = 4 and P = 14; other
+k; and col_len < k.
 
-    python tests/golden/make_fixtures.py
+    python tests/golden/make_fixtures.py [name ...]   (default: every fixture)
 """
 from __future__ import annotations
 
@@ -32,6 +33,7 @@ CASES = {
     "slab_wrap_p14": (4, 14336, 1024, 102, 0.02, 0.0, "row"),
     "k1024_p2": (16, 2048, 1024, 103, 0.02, 0.0, "row"),
     "esc_k1024": (12, 4096, 1024, 104, 0.0, 0.0, "esc"),
+    "esc_slab_p14": (6, 14336, 1024, 108, 0.0, 0.0, "esc"),
     "scalar_k256": (300, 513, 256, 105, 0.02, 0.0, "scalar"),
     "narrow_k1024": (40, 100, 1024, 106, 0.02, 0.0, "row"),
     "block2d": (256, 256, 64, 107, 0.02, 0.0, "block2d"),
@@ -67,9 +69,15 @@ def inputs(n, m, seed, sigma, outlier_p, mode):
     return bf, q, sc
 
 
-def main() -> int:
+def main(names=None) -> int:
+    path = os.path.join(HERE, "manifest.json")
     manifest = {}
+    if names and os.path.exists(path):
+        with open(path) as f:
+            manifest = json.load(f)
     for name, (n, m, k, seed, sigma, outlier_p, mode) in CASES.items():
+        if names and name not in names:
+            continue
         bf, q, sc = inputs(n, m, seed, sigma, outlier_p, mode)
         side, stats = oracle.encode(bf, q, sc, MAX_LEN, k, with_stats=True)
         arrays = {"in_bf16": bf, "in_fp8": q, "in_scales": sc}
@@ -81,11 +89,11 @@ def main() -> int:
                           "tables": int(side["decode_syms_u16"].shape[0]),
                           "bitstream_words": int(side["bitstream_u64"].shape[0]), **stats}
         print(name, manifest[name])
-    with open(os.path.join(HERE, "manifest.json"), "w") as f:
+    with open(path, "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)
         f.write("\n")
     return 0
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    sys.exit(main(sys.argv[1:]))
