@@ -1,56 +1,51 @@
-"""Offline compressor: FP8 checkpoint + BF16 checkpoint -> FP8 + Huffman sidecar model.
+"""Offline compressor: a BF16 checkpoint and its FP8 checkpoint -> an FP8 model
+with a Huffman sidecar per linear weight, built on the GPU.
 
-Drop-in for the reference's scripts/compress_llm_fp8_huffman.py (same command
-line, same sidecar keys and dtypes, same index.json / config.json rewrite),
-with the sidecars built on the GPU by the HIP builder
-(MPServe_cuda.huffman_build_fp8_decode_tables, byte-identical to the
-reference's host builder)::
+    python -m mpserve_amd.compress --bf16_model <dir> --fp8_model <dir> --out_dir <dir> [options]
 
-    python -m mpserve_amd.compress --bf16_model <bf16 dir> --fp8_model <fp8 dir> --out_dir <out dir>
+It takes the command line of the reference's offline compressor
+(scripts/compress_llm_fp8_huffman.py:164-198) and writes the same files: the
+output directory mirrors the base model (the FP8 model unless --base_model is
+given), gains ``<sidecar_name>`` with 16 ``<module>.huff_*`` tensors per module
+(names and stored dtypes of compress:284-306), and its safetensors index and
+config.json are rewritten (compress:318-367). The sidecars come from the GPU
+builder behind ``MPServe_cuda.huffman_build_fp8_decode_tables``, whose output
+is byte-identical to the reference's host builder.
 
-Steps (reference line numbers in scripts/compress_llm_fp8_huffman.py):
-  1. out_dir gets the base model tree (default: the FP8 model), files
-     hard-linked where possible; model.safetensors.index.json and config.json
-     are copied, since they are rewritten (:143-160).
-  2. Every BF16 ``*.weight`` key accepted by --include / --exclude whose FP8
-     checkpoint has the same key and a ``weight_scale_inv`` or ``weight_scale``
-     is one module (:232-253); 2-D BF16 weights only (:255-258).
-  3. FP8 bytes, scale dtype and scale shape are normalised as the reference
-     does (:71-140), then the sidecar is built on the GPU.
-  4. Sidecar tensors are stored under ``<module>.huff_*`` with the reference's
-     signed dtypes (:284-306) into --sidecar_name (one shard, as the reference
-     writes it; --max_shard_gb splits it into several shards named
-     ``<stem>-NNNNN.safetensors``, all listed in the index).
-  5. The index maps every sidecar key to its shard; with
-     --override_common_from_bf16, keys in both checkpoints that match
-     --override_allow_regex come from the BF16 checkpoint (:330-344).
-     config.json gets quantization_config.quant_method = "fp8_huffman" and
-     max_len (:350-362).
-
-Host memory: the reference keeps every sidecar tensor of the model in one dict
-until the end. Here a shard is written as soon as it reaches --max_shard_gb
-(0, the default, keeps the reference's single shard).
+The work is split into four passes:
+  1. ``mirror_tree``: link (or copy) the base model into the output directory.
+  2. ``select_modules``: pair each BF16 ``*.weight`` with the FP8 weight of the
+     same name and its scale, using only the safetensors headers.
+  3. ``build_sidecars``: per module, read the three tensors, bring the FP8
+     bytes and the scales into the builder's input forms (``fp8_bytes``,
+     ``scale_keys``, ``scale_rows``), build, and hand the stored tensors to a
+     ``SidecarStore`` (one shard, as the reference writes, or shards of about
+     --max_shard_gb, written as they fill so the host never holds the whole
+     model's sidecar).
+  4. ``finish``: index, optional BF16 overrides, config.json.
 """
 from __future__ import annotations
 
 import argparse
+import collections
 import json
 import os
 import re
 import shutil
 import sys
 import time
+from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Callable, Dict, List, Optional, Tuple
 
 import torch
 
 INDEX = "model.safetensors.index.json"
-# builder outputs that the sidecar does not store (they are returned by the build op only)
-_NOT_STORED = ("table_scale_u16", "table_fp8_u16", "bucket_scale_u16", "shape_nmk_i64", "bucket_U_i32",
-               "bucket_unique_gid_i32", "bucket_fp8_uidx_i16")
-# build-op key -> (sidecar suffix, stored dtype): safetensors has no u16/u32/u64
-_STORED = (
+OVERRIDES = "overrides_from_bf16.safetensors"
+
+# (build-op key, stored suffix, stored dtype): safetensors has no u16/u32/u64,
+# so those arrays are stored as the signed type of the same width (bit for bit)
+STORED = (
     ("bitstream_u64", "huff_bitstream_u64", torch.int64),
     ("decode_syms_u16", "huff_decode_syms_u16", torch.int16),
     ("decode_lens_u8", "huff_decode_lens_u8", torch.uint8),
@@ -62,296 +57,344 @@ _STORED = (
     ("bucket_thread_startbit_u32", "huff_bucket_thread_startbit_u32", torch.int32),
     ("bucket_bit_base_i64", "huff_bucket_bit_base_i64", torch.int64),
 )
+# fields of the packed-layer modes (one layer's linears packed into one weight):
+# a plain sidecar stores them at their neutral values
+PACK_FIELDS = {"huff_2d_nb1_i32": (1,), "huff_attn_block_row_start_i32": (), "huff_attn_block_row_len_i32": (),
+               "huff_attn_block_col_start_i32": (), "huff_attn_block_col_len_i32": ()}
 
 
-def log(msg: str) -> None:
-    print(f"[{time.strftime('%Y-%m-%d %H:%M:%S')}] {msg}", flush=True)
+def say(msg: str) -> None:
+    print(f"compress [{time.strftime('%H:%M:%S')}] {msg}", flush=True)
 
 
 def parse_args(argv=None) -> argparse.Namespace:
-    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    p.add_argument("--bf16_model", type=str, required=True, help="Path to BF16 model dir (safetensors)")
-    p.add_argument("--fp8_model", type=str, required=True, help="Path to FP8 model dir (safetensors)")
-    p.add_argument("--out_dir", type=str, required=True, help="Output model dir (FP8 + Huffman sidecar)")
+    p = argparse.ArgumentParser(description="Add a Huffman sidecar to an FP8 checkpoint (GPU builder).")
+    p.add_argument("--bf16_model", type=str, required=True, help="directory of the BF16 safetensors model")
+    p.add_argument("--fp8_model", type=str, required=True, help="directory of the FP8 safetensors model")
+    p.add_argument("--out_dir", type=str, required=True, help="where the FP8 + sidecar model is written")
     p.add_argument("--base_model", type=str, default=None,
-                   help="Directory tree to copy/link into out_dir before adding sidecar (default: fp8_model)")
-    p.add_argument("--include", type=str, default=None, help="Regex to include BF16 weight keys")
-    p.add_argument("--exclude", type=str, default=None, help="Regex to exclude BF16 weight keys")
-    p.add_argument("--max_len", type=int, default=7, help="Max Huffman code length (must be 7)")
-    p.add_argument("--threads", type=int, default=1024, help="threads_per_block used for bucket metadata")
-    p.add_argument("--sidecar_name", type=str, default="huffman_fp8.safetensors", help="Sidecar shard filename")
-    p.add_argument("--store_fp8_u8", action="store_true", default=True, help="Store huff_fp8_u8 tensors")
-    p.add_argument("--no_store_fp8_u8", action="store_false", dest="store_fp8_u8")
+                   help="model tree mirrored into out_dir first (default: the FP8 model)")
+    p.add_argument("--include", type=str, default=None, help="only BF16 weight keys matching this regex")
+    p.add_argument("--exclude", type=str, default=None, help="skip BF16 weight keys matching this regex")
+    p.add_argument("--max_len", type=int, default=7, help="longest Huffman code (the decoder requires 7)")
+    p.add_argument("--threads", type=int, default=1024, help="substreams per bucket (threads_per_block)")
+    p.add_argument("--sidecar_name", type=str, default="huffman_fp8.safetensors", help="file name of the sidecar")
+    p.add_argument("--store_fp8_u8", action="store_true", default=True,
+                   help="store each module's FP8 bytes in the sidecar as huff_fp8_u8 (default)")
+    p.add_argument("--no_store_fp8_u8", action="store_false", dest="store_fp8_u8",
+                   help="store an empty huff_fp8_u8 instead")
     p.add_argument("--override_common_from_bf16", action="store_true",
-                   help="Write a small overrides shard for keys that exist in both BF16 and FP8 checkpoints")
+                   help="serve keys present in both checkpoints (filtered by --override_allow_regex) from BF16")
     p.add_argument("--override_allow_regex", type=str, default=r"^(?:model\.embed_tokens\.weight|lm_head\.weight)$",
-                   help="Regex filter for override keys (when --override_common_from_bf16 is set)")
+                   help="which common keys --override_common_from_bf16 takes from BF16")
     p.add_argument("--max_shard_gb", type=float, default=0.0,
-                   help="Split the sidecar into shards of about this size (0: one shard, as the reference)")
+                   help="split the sidecar into shards of about this many GB (0: a single file)")
     return p.parse_args(argv)
 
 
-# --- checkpoint access ----------------------------------------------------------
-def weight_map(model_dir: Path) -> Dict[str, str]:
-    """The ``weight_map`` of a model's safetensors index (compress:45-54)."""
-    path = model_dir / INDEX
-    if not path.exists():
-        raise FileNotFoundError(f"Missing safetensors index: {path}")
-    with open(path, "r", encoding="utf-8") as f:
-        wm = json.load(f).get("weight_map")
-    if not isinstance(wm, dict):
-        raise ValueError(f"Invalid weight_map in {path}")
-    return wm
+# --------------------------------------------------------------------------- checkpoints
+class Checkpoint:
+    """A safetensors model directory read through its index; shards are opened
+    once and tensors read on demand."""
+
+    def __init__(self, root: Path):
+        self.root = Path(root)
+        path = self.root / INDEX
+        if not path.is_file():
+            raise FileNotFoundError(f"{path}: no safetensors index")
+        with open(path, "r", encoding="utf-8") as f:
+            wm = json.load(f).get("weight_map")
+        if not isinstance(wm, dict):
+            raise ValueError(f"{path}: weight_map is missing or not an object")
+        self.index: Dict[str, str] = wm
+        self._open: Dict[str, object] = {}
+
+    def __contains__(self, key: str) -> bool:
+        return key in self.index
+
+    def _shard(self, key: str):
+        name = self.index.get(key)
+        if not isinstance(name, str):
+            raise KeyError(f"{key}: not in the index of {self.root}")
+        h = self._open.get(name)
+        if h is None:
+            path = self.root / name
+            if not path.is_file():
+                raise FileNotFoundError(f"{path}: shard of {key} not found")
+            from safetensors import safe_open
+
+            h = safe_open(str(path), framework="pt", device="cpu")
+            self._open[name] = h
+        return h
+
+    def header(self, key: str) -> Tuple[str, List[int]]:
+        """(safetensors dtype name, shape) of a tensor, without reading it."""
+        s = self._shard(key).get_slice(key)
+        return s.get_dtype(), list(s.get_shape())
+
+    def tensor(self, key: str) -> torch.Tensor:
+        return self._shard(key).get_tensor(key)
 
 
-def load_tensor(model_dir: Path, wm: Dict[str, str], key: str) -> torch.Tensor:
-    """One tensor from the shard the index names for it (compress:57-68)."""
-    shard = wm.get(key)
-    if not isinstance(shard, str):
-        raise KeyError(f"Key not in safetensors index: {key}")
-    path = model_dir / shard
-    if not path.exists():
-        raise FileNotFoundError(f"Missing safetensors shard for {key}: {path}")
-    from safetensors import safe_open
-
-    with safe_open(str(path), framework="pt", device="cpu") as f:
-        return f.get_tensor(key)
+# --------------------------------------------------------------------------- module selection
+@dataclass
+class Module:
+    prefix: str        # "model.layers.0.self_attn.q_proj"
+    weight_key: str    # prefix + ".weight" (BF16 and FP8 checkpoints)
+    scale_key: str     # prefix + ".weight_scale_inv" or ".weight_scale" (FP8 checkpoint)
 
 
-# --- normalisation of the FP8 checkpoint's tensors ------------------------------------
-def fp8_bytes(t: torch.Tensor, shape: Tuple[int, int]) -> torch.Tensor:
-    """The stored FP8 weight as uint8 [n, m] (compress:71-93): uint8 as is, float8
-    and 16-bit dtypes by their bytes, float32 through a bf16 cast."""
-    if t.dtype == torch.uint8 or str(t.dtype).startswith("torch.float8"):
-        u = t.view(torch.uint8)
-    elif t.dtype in (torch.bfloat16, torch.float16):
-        u = t.view(torch.uint16).view(torch.uint8)
-    elif t.dtype == torch.float32:
-        u = t.to(torch.bfloat16).view(torch.uint16).view(torch.uint8)
-    else:
-        u = t.view(torch.uint8)
-    n, m = shape
-    if int(u.numel()) != n * m:
-        raise ValueError(f"FP8 numel mismatch: got {int(u.numel())} expected {n * m}")
-    return u.reshape(n, m)
+@dataclass
+class Selection:
+    modules: List[Module] = field(default_factory=list)
+    skipped: collections.Counter = field(default_factory=collections.Counter)
 
 
-def scale_keys(scales: torch.Tensor) -> torch.Tensor:
-    """Scales in a dtype the build op accepts (compress:96-104): u16 bits and bf16
-    as they are, fp16 by its bits, fp32 rounded to fp16 bits, others to bf16."""
-    if scales.dtype in (torch.uint16, torch.bfloat16):
-        return scales
-    if scales.dtype == torch.float16:
-        return scales.view(torch.uint16)
-    if scales.dtype == torch.float32:
-        return scales.to(torch.float16).view(torch.uint16)
-    return scales.to(torch.bfloat16)
+def select_modules(bf16: Checkpoint, fp8: Checkpoint, include: Optional[str], exclude: Optional[str]) -> Selection:
+    """Modules to build, in the BF16 index's order: a BF16 ``*.weight`` that the
+    filters accept, that is a 2-D bfloat16 tensor, and whose FP8 checkpoint has
+    the same key and a scale (``weight_scale_inv`` preferred to ``weight_scale``)."""
+    inc = re.compile(include) if include else None
+    exc = re.compile(exclude) if exclude else None
+    sel = Selection()
+    for key in bf16.index:
+        if not key.endswith(".weight"):
+            continue
+        if (inc is not None and not inc.search(key)) or (exc is not None and exc.search(key)):
+            continue
+        prefix = key[: -len(".weight")]
+        scale = next((s for s in (prefix + ".weight_scale_inv", prefix + ".weight_scale") if s in fp8), None)
+        if key not in fp8 or scale is None:
+            sel.skipped["no FP8 weight or scale"] += 1
+            continue
+        dtype, shape = bf16.header(key)
+        if dtype != "BF16" or len(shape) != 2:
+            sel.skipped["not a 2-D BF16 weight"] += 1
+            continue
+        sel.modules.append(Module(prefix, key, scale))
+    return sel
 
 
-def scale_shape(scales: torch.Tensor, n: int, m: int) -> torch.Tensor:
-    """Scale layouts reduced to what the builder keys rows by (compress:107-140):
-    scalar and [n] stay; [n, 1] -> [n]; [n / g] and [n / g, 1] repeat each entry
-    g times; a block grid [n / bn, m / bm] keeps its first column block, repeated
-    bn times. Anything else is passed through (the build op then rejects it)."""
-    total = int(scales.numel())
-    if total == 1:
-        return scales
-    if scales.dim() == 2 and int(scales.size(0)) == n and int(scales.size(1)) == 1:
-        scales = scales.squeeze(1)
-    if scales.dim() == 1 and total == n:
-        return scales
-    if scales.dim() == 1 and total > 0 and n % total == 0:
-        return scales.repeat_interleave(n // total)
-    if scales.dim() == 2 and int(scales.size(1)) == 1 and int(scales.size(0)) > 0 and n % int(scales.size(0)) == 0:
-        return scales.squeeze(1).repeat_interleave(n // int(scales.size(0)))
-    if scales.dim() == 2 and int(scales.size(0)) > 0 and int(scales.size(1)) > 0:
-        if n % int(scales.size(0)) == 0 and m % int(scales.size(1)) == 0:
-            return scales[:, 0].repeat_interleave(n // int(scales.size(0)))
-    return scales
+# --------------------------------------------------------------------------- builder inputs
+def fp8_bytes(t: torch.Tensor, n: int, m: int) -> torch.Tensor:
+    """The FP8 checkpoint's weight as the builder's uint8 [n, m].
+
+    Whatever the stored dtype, the weight's bytes are taken as they lie, with one
+    exception: a float32 store is rounded to bfloat16 first, since such files
+    carry byte pairs widened to float (compress:71-93). A byte count other than
+    n*m is an error.
+    """
+    if t.dtype == torch.float32:
+        t = t.to(torch.bfloat16)
+    raw = t.contiguous().view(torch.uint8) if t.dim() > 0 else t.reshape(1).view(torch.uint8)
+    if raw.numel() != n * m:
+        raise ValueError(f"FP8 weight has {raw.numel()} bytes, the BF16 weight {n}x{m} needs {n * m}")
+    return raw.reshape(n, m)
 
 
-def sidecar_entries(prefix: str, built: Dict[str, torch.Tensor], fp8_u8: torch.Tensor,
-                    store_fp8: bool) -> Dict[str, torch.Tensor]:
-    """The ``<prefix>.huff_*`` tensors of one module, as the reference stores them
-    (compress:284-306): the FP8 copy (or an empty [0, 0] one), the ten decode
-    arrays with signed dtypes, and the five packed-mode fields left at their
-    defaults."""
-    out = {f"{prefix}.huff_fp8_u8": fp8_u8.contiguous() if store_fp8 else torch.empty((0, 0), dtype=torch.uint8)}
-    for key, suffix, dtype in _STORED:
-        t = built[key].cpu()
-        # bit-preserving for the unsigned -> signed views (u64/u16/u32 do not exist in safetensors)
-        out[f"{prefix}.{suffix}"] = (t.view(dtype) if t.element_size() == torch.empty(0, dtype=dtype).element_size()
-                                     else t.to(dtype)).contiguous()
-    out[f"{prefix}.huff_2d_nb1_i32"] = torch.tensor([1], dtype=torch.int32)
-    for f in ("row_start", "row_len", "col_start", "col_len"):
-        out[f"{prefix}.huff_attn_block_{f}_i32"] = torch.empty((0,), dtype=torch.int32)
+# stored scale dtype -> the 16-bit key the builder groups rows by (compress:96-104)
+_SCALE_KEY = {
+    torch.uint16: lambda s: s,
+    torch.bfloat16: lambda s: s,
+    torch.float16: lambda s: s.view(torch.uint16),
+    torch.float32: lambda s: s.to(torch.float16).view(torch.uint16),
+}
+
+
+def scale_keys(s: torch.Tensor) -> torch.Tensor:
+    """Scales in a dtype the builder takes: u16 bits or bf16 as stored, fp16 by its
+    bits, fp32 rounded to fp16 bits; any other dtype is cast to bf16."""
+    return _SCALE_KEY.get(s.dtype, lambda x: x.to(torch.bfloat16))(s)
+
+
+def scale_rows(s: torch.Tensor, n: int, m: int) -> torch.Tensor:
+    """Scales in a layout the builder keys rows by (compress:107-140).
+
+    * one value: unchanged;
+    * a column of L values ([L] or [L, 1]) with L dividing n: each value covers
+      n / L consecutive rows (L = n: one per row);
+    * a block grid [R, C] with R | n and C | m: each row block takes the scale
+      of its first column block;
+    * anything else: unchanged (the builder then rejects it).
+    """
+    if s.numel() == 1:
+        return s
+    column = s.dim() == 1 or (s.dim() == 2 and s.shape[1] == 1)
+    rows = int(s.shape[0]) if s.dim() >= 1 else 0
+    if column and rows > 0 and n % rows == 0:
+        return s.reshape(rows).repeat_interleave(n // rows)
+    if s.dim() == 2 and rows > 0 and s.shape[1] > 0 and n % rows == 0 and m % int(s.shape[1]) == 0:
+        return s[:, 0].repeat_interleave(n // rows)
+    return s
+
+
+def stored_tensors(prefix: str, built: Dict[str, torch.Tensor], fp8_u8: torch.Tensor,
+                   keep_fp8: bool) -> Dict[str, torch.Tensor]:
+    """The 16 tensors stored for one module: its FP8 bytes (or an empty [0, 0]),
+    the ten decode arrays in their stored dtypes, and the packed-mode fields."""
+    out = {f"{prefix}.huff_fp8_u8": fp8_u8 if keep_fp8 else torch.empty((0, 0), dtype=torch.uint8)}
+    for key, suffix, dtype in STORED:
+        t = built[key].cpu().contiguous()
+        out[f"{prefix}.{suffix}"] = t if t.dtype == dtype else t.view(dtype)
+    for name, value in PACK_FIELDS.items():
+        out[f"{prefix}.{name}"] = torch.tensor(list(value), dtype=torch.int32)
     return out
 
 
-def link_or_copy_tree(src: Path, dst: Path) -> None:
-    """Mirror src into dst: hard links where possible, copies otherwise; the
-    index and config.json are always copied (they are rewritten); existing files
-    are kept (compress:143-160)."""
-    dst.mkdir(parents=True, exist_ok=True)
-    for root, dirs, files in os.walk(src):
-        rel = Path(root).relative_to(src)
-        (dst / rel).mkdir(parents=True, exist_ok=True)
-        for d in dirs:
-            (dst / rel / d).mkdir(parents=True, exist_ok=True)
-        for fn in files:
-            sp, dp = Path(root) / fn, dst / rel / fn
-            if dp.exists():
-                continue
-            if fn in (INDEX, "config.json"):
-                shutil.copy2(sp, dp)
-                continue
-            try:
-                os.link(sp, dp)
-            except OSError:
-                shutil.copy2(sp, dp)
-
-
-def default_builder(bf16: torch.Tensor, fp8_u8: torch.Tensor, scales: torch.Tensor, max_len: int,
-                    threads: int) -> Dict[str, torch.Tensor]:
-    """The GPU sidecar builder through the MPServe_cuda op surface."""
+def gpu_builder(bf16: torch.Tensor, fp8_u8: torch.Tensor, scales: torch.Tensor, max_len: int,
+                threads: int) -> Dict[str, torch.Tensor]:
+    """The GPU sidecar builder, through the MPServe_cuda op."""
     from mpserve_amd import mpserve_cuda
 
     return mpserve_cuda.huffman_build_fp8_decode_tables(bf16, fp8_u8, scales, max_len=max_len,
                                                         threads_per_block=threads)
 
 
-class ShardWriter:
-    """Sidecar shards: one file, or files of about ``max_bytes`` each."""
+# --------------------------------------------------------------------------- output
+def mirror_tree(src: Path, dst: Path) -> int:
+    """Give dst every file of src that it lacks: a hard link where the file system
+    allows one, else a copy; the index and config.json are always copies, since
+    they are rewritten. Returns the number of files added."""
+    added = 0
+    for here, _dirs, files in os.walk(src):
+        target = dst / Path(here).relative_to(src)
+        target.mkdir(parents=True, exist_ok=True)
+        for name in files:
+            a, b = Path(here) / name, target / name
+            if b.exists():
+                continue
+            linked = False
+            if name not in (INDEX, "config.json"):
+                try:
+                    os.link(a, b)
+                    linked = True
+                except OSError:
+                    pass
+            if not linked:
+                shutil.copy2(a, b)
+            added += 1
+    for here, dirs, _files in os.walk(src):  # empty directories too
+        for d in dirs:
+            (dst / Path(here).relative_to(src) / d).mkdir(parents=True, exist_ok=True)
+    return added
 
-    def __init__(self, out_dir: Path, name: str, max_bytes: int):
-        self.out_dir, self.name, self.max_bytes = out_dir, name, max_bytes
-        self.pending: Dict[str, torch.Tensor] = {}
-        self.pending_bytes = 0
+
+class SidecarStore:
+    """Collects modules' stored tensors and writes them as one file, or as files
+    of about ``shard_bytes`` each (``<stem>-00001.safetensors`` ...) written as
+    soon as they fill."""
+
+    def __init__(self, out_dir: Path, name: str, shard_bytes: int):
+        self.out_dir, self.name, self.shard_bytes = out_dir, name, shard_bytes
+        self._held: Dict[str, torch.Tensor] = {}
+        self._held_bytes = 0
         self.files: List[str] = []
-        self.key_file: Dict[str, str] = {}
+        self.where: Dict[str, str] = {}  # tensor key -> file
 
-    def _shard_name(self, i: int) -> str:
+    def _next_name(self) -> str:
         stem, ext = os.path.splitext(self.name)
-        return f"{stem}-{i + 1:05d}{ext}"
+        return f"{stem}-{len(self.files) + 1:05d}{ext}"
 
-    def add(self, tensors: Dict[str, torch.Tensor]) -> None:
-        self.pending.update(tensors)
-        self.pending_bytes += sum(t.numel() * t.element_size() for t in tensors.values())
-        if self.max_bytes > 0 and self.pending_bytes >= self.max_bytes:
-            self._flush(self._shard_name(len(self.files)))
-
-    def _flush(self, fname: str) -> None:
+    def _write(self, fname: str) -> None:
         from safetensors.torch import save_file
 
-        log(f"Writing sidecar shard: {self.out_dir / fname} (tensors={len(self.pending)})")
-        save_file(self.pending, str(self.out_dir / fname))
-        for k in self.pending:
-            self.key_file[k] = fname
+        save_file(self._held, str(self.out_dir / fname))
+        say(f"wrote {fname}: {len(self._held)} tensors, {self._held_bytes / 1e6:.1f} MB")
+        self.where.update(dict.fromkeys(self._held, fname))
         self.files.append(fname)
-        self.pending, self.pending_bytes = {}, 0
+        self._held, self._held_bytes = {}, 0
+
+    def add(self, tensors: Dict[str, torch.Tensor]) -> None:
+        self._held.update(tensors)
+        self._held_bytes += sum(t.numel() * t.element_size() for t in tensors.values())
+        if 0 < self.shard_bytes <= self._held_bytes:
+            self._write(self._next_name())
 
     def close(self) -> None:
-        if self.pending:
-            self._flush(self.name if self.max_bytes <= 0 else self._shard_name(len(self.files)))
+        if self._held:
+            self._write(self.name if self.shard_bytes <= 0 else self._next_name())
 
 
-def compress(args: argparse.Namespace, builder: Callable = default_builder) -> Dict[str, object]:
-    """Run the compressor; returns a summary (modules built, keys added, shard files)."""
-    if int(args.max_len) != 7:
-        raise SystemExit("--max_len must be 7 for the FP8 Huffman decode kernel")
-    bf16_dir, fp8_dir, out_dir = Path(args.bf16_model), Path(args.fp8_model), Path(args.out_dir)
-    base_dir = Path(args.base_model) if args.base_model else fp8_dir
-    if not bf16_dir.is_dir():
-        raise SystemExit(f"--bf16_model must be a directory: {bf16_dir}")
-    if not fp8_dir.is_dir():
-        raise SystemExit(f"--fp8_model must be a directory: {fp8_dir}")
-    include = re.compile(args.include) if args.include else None
-    exclude = re.compile(args.exclude) if args.exclude else None
+def build_sidecars(mods: List[Module], bf16: Checkpoint, fp8: Checkpoint, store: SidecarStore, args,
+                   builder: Callable) -> int:
+    for i, mod in enumerate(mods, 1):
+        w = bf16.tensor(mod.weight_key).contiguous()
+        n, m = int(w.shape[0]), int(w.shape[1])
+        q = fp8_bytes(fp8.tensor(mod.weight_key), n, m).contiguous()
+        s = scale_rows(scale_keys(fp8.tensor(mod.scale_key).contiguous()), n, m).contiguous()
+        t0 = time.time()
+        built = builder(w, q, s, int(args.max_len), int(args.threads))
+        store.add(stored_tensors(mod.prefix, built, q, bool(args.store_fp8_u8)))
+        say(f"[{i}/{len(mods)}] {mod.prefix} {n}x{m}: {int(built['bucket_table_i32'].shape[0])} buckets, "
+            f"{int(built['decode_syms_u16'].shape[0])} tables ({time.time() - t0:.2f} s)")
+    return len(mods)
 
-    def selected(key: str) -> bool:
-        return (include is None or include.search(key) is not None) and \
-               (exclude is None or exclude.search(key) is None)
 
-    log(f"Start FP8 Huffman sidecar build: bf16_model={bf16_dir} fp8_model={fp8_dir} out_dir={out_dir} "
-        f"max_len={args.max_len} threads={args.threads}")
-    t0 = time.time()
-    link_or_copy_tree(base_dir, out_dir)
-    log(f"Prepared out_dir (copy/link): elapsed={time.time() - t0:.2f}s")
-    wm_b, wm_f = weight_map(bf16_dir), weight_map(fp8_dir)
-    candidates = [k for k in wm_b if k.endswith(".weight")]
-    log(f"Loaded safetensors index: bf16_keys={len(wm_b)} fp8_keys={len(wm_f)}; BF16 .weight candidates: "
-        f"{len(candidates)}")
-
-    writer = ShardWriter(out_dir, str(args.sidecar_name), int(args.max_shard_gb * 1e9))
-    built = missing = not_2d = 0
-    for key in candidates:
-        if not selected(key):
-            continue
-        prefix = key[: -len(".weight")]
-        scales_key = next((c for c in (f"{prefix}.weight_scale_inv", f"{prefix}.weight_scale") if c in wm_f), None)
-        if key not in wm_f or scales_key is None:
-            missing += 1
-            continue
-        bf16 = load_tensor(bf16_dir, wm_b, key).contiguous()
-        if bf16.dtype != torch.bfloat16 or bf16.dim() != 2:
-            not_2d += 1
-            continue
-        n, m = int(bf16.shape[0]), int(bf16.shape[1])
-        q = fp8_bytes(load_tensor(fp8_dir, wm_f, key).contiguous(), (n, m)).contiguous()
-        scales = scale_shape(scale_keys(load_tensor(fp8_dir, wm_f, scales_key).contiguous()), n, m).contiguous()
-        log(f"Building artifact '{prefix}'")
-        out = builder(bf16, q, scales, int(args.max_len), int(args.threads))
-        writer.add(sidecar_entries(prefix, out, q, bool(args.store_fp8_u8)))
-        built += 1
-        if built % 16 == 0:
-            log(f"Built {built} modules...")
-    if built == 0:
-        raise SystemExit(f"No modules matched. skipped_missing_fp8={missing} skipped_non_bf16_2d={not_2d}")
-    writer.close()
-
-    index_path = out_dir / INDEX
-    with open(index_path, "r", encoding="utf-8") as f:
+def finish(out_dir: Path, bf16: Checkpoint, fp8: Checkpoint, store: SidecarStore, args) -> Path:
+    """Point the index at the sidecar (and at the BF16 overrides), and mark
+    config.json's quantization method. JSON is written as the reference writes
+    it (2-space indent, sorted keys, no trailing newline)."""
+    path = out_dir / INDEX
+    with open(path, "r", encoding="utf-8") as f:
         idx = json.load(f)
     wm = idx.get("weight_map")
     if not isinstance(wm, dict):
-        raise ValueError(f"Invalid weight_map in {index_path}")
-    wm.update(writer.key_file)
+        raise ValueError(f"{path}: weight_map is missing or not an object")
+    wm.update(store.where)
     if args.override_common_from_bf16:
         allow = re.compile(args.override_allow_regex) if args.override_allow_regex else None
-        common = sorted(set(wm_b) & set(wm_f))
-        keys = [k for k in common if allow is None or allow.search(k) is not None]
-        log(f"Overriding common keys from BF16: common={len(common)} selected={len(keys)}")
-        overrides = {k: load_tensor(bf16_dir, wm_b, k) for k in keys}
-        if overrides:
+        both = sorted(set(bf16.index) & set(fp8.index))
+        chosen = [k for k in both if allow is None or allow.search(k)]
+        say(f"BF16 overrides: {len(chosen)} of the {len(both)} keys both checkpoints hold")
+        if chosen:
             from safetensors.torch import save_file
 
-            name = "overrides_from_bf16.safetensors"
-            log(f"Writing override shard: {out_dir / name} (tensors={len(overrides)})")
-            save_file(overrides, str(out_dir / name))
-            for k in keys:
-                wm[k] = name
+            save_file({k: bf16.tensor(k) for k in chosen}, str(out_dir / OVERRIDES))
+            wm.update(dict.fromkeys(chosen, OVERRIDES))
     idx["weight_map"] = wm
-    with open(index_path, "w", encoding="utf-8") as f:
+    with open(path, "w", encoding="utf-8") as f:
         json.dump(idx, f, indent=2, sort_keys=True)
-
-    cfg_path = out_dir / "config.json"
-    if cfg_path.exists():
+    cfg = out_dir / "config.json"
+    if cfg.exists():
         try:
-            cfg = json.loads(cfg_path.read_text(encoding="utf-8"))
-            qc = cfg.get("quantization_config")
+            c = json.loads(cfg.read_text(encoding="utf-8"))
+        except ValueError:
+            c = None  # an unreadable config.json is left as it is
+        if isinstance(c, dict):
+            qc = c.get("quantization_config")
             qc = qc if isinstance(qc, dict) else {}
             qc["quant_method"] = "fp8_huffman"
             qc.setdefault("max_len", int(args.max_len))
-            cfg["quantization_config"] = qc
-            cfg_path.write_text(json.dumps(cfg, indent=2, sort_keys=True), encoding="utf-8")
-        except (ValueError, OSError):
-            # the reference also leaves an unreadable config.json as it is
-            pass
-    for f in writer.files:
-        print(f"Wrote sidecar shard: {out_dir / f}")
-    print(f"Updated index: {index_path}")
-    print(f"Added keys: {len(writer.key_file)}")
-    return {"modules": built, "keys": len(writer.key_file), "files": list(writer.files)}
+            c["quantization_config"] = qc
+            try:
+                cfg.write_text(json.dumps(c, indent=2, sort_keys=True), encoding="utf-8")
+            except OSError:
+                say(f"{cfg}: could not be rewritten; left as it was")
+    return path
+
+
+def compress(args: argparse.Namespace, builder: Callable = gpu_builder) -> Dict[str, object]:
+    """Run the four passes; returns {"modules", "keys", "files"}."""
+    if int(args.max_len) != 7:
+        raise SystemExit(f"--max_len {args.max_len}: the FP8 decode kernel only reads max_len 7 sidecars")
+    for flag in ("bf16_model", "fp8_model"):
+        if not Path(getattr(args, flag)).is_dir():
+            raise SystemExit(f"--{flag} {getattr(args, flag)}: not a directory")
+    out_dir = Path(args.out_dir)
+    t0 = time.time()
+    added = mirror_tree(Path(args.base_model or args.fp8_model), out_dir)
+    say(f"mirrored the base model into {out_dir} ({added} files, {time.time() - t0:.1f} s)")
+    bf16, fp8 = Checkpoint(Path(args.bf16_model)), Checkpoint(Path(args.fp8_model))
+    sel = select_modules(bf16, fp8, args.include, args.exclude)
+    say(f"{len(sel.modules)} modules to build; skipped: {dict(sel.skipped) or 'none'}")
+    if not sel.modules:
+        raise SystemExit("no module to build: " + ", ".join(f"{v} {k}" for k, v in sel.skipped.items()))
+    store = SidecarStore(out_dir, str(args.sidecar_name), int(args.max_shard_gb * 1e9))
+    build_sidecars(sel.modules, bf16, fp8, store, args, builder)
+    store.close()
+    index = finish(out_dir, bf16, fp8, store, args)
+    say(f"done: {len(store.where)} sidecar tensors in {', '.join(store.files)}; index {index}")
+    return {"modules": len(sel.modules), "keys": len(store.where), "files": list(store.files)}
 
 
 def main(argv=None) -> int:

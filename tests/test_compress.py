@@ -134,26 +134,39 @@ def test_compress_shards_filters_and_overrides(tmp_path):
 
 def test_compress_rejects_bad_max_len_and_no_match(tmp_path):
     bf_dir, f8_dir, _ = _model_pair(tmp_path)
-    with pytest.raises(SystemExit, match="max_len must be 7"):
+    with pytest.raises(SystemExit, match="only reads max_len 7"):
         cz.compress(_args(bf_dir, f8_dir, tmp_path / "o1", max_len=6), builder=_oracle_builder)
-    with pytest.raises(SystemExit, match="No modules matched"):
+    with pytest.raises(SystemExit, match="no module to build"):
         cz.compress(_args(bf_dir, f8_dir, tmp_path / "o2", include=r"nothing"), builder=_oracle_builder)
 
 
 def test_scale_normalisation_matches_reference_rules():
+    """compress_llm_fp8_huffman.py:71-140: the dtype and layout rules, case by case."""
     n, m = 256, 512
     s = torch.arange(4, dtype=torch.float32)
-    assert cz.scale_shape(torch.tensor([3.0]), n, m).numel() == 1
-    assert cz.scale_shape(torch.ones(n, 1), n, m).shape == (n,)
-    assert cz.scale_shape(s, n, m).tolist() == sum([[float(i)] * 64 for i in range(4)], [])
-    assert cz.scale_shape(s.reshape(4, 1), n, m).shape == (n,)
+    assert cz.scale_rows(torch.tensor([3.0]), n, m).numel() == 1
+    assert cz.scale_rows(torch.ones(n, 1), n, m).shape == (n,)
+    assert cz.scale_rows(s, n, m).tolist() == sum([[float(i)] * 64 for i in range(4)], [])
+    assert cz.scale_rows(s.reshape(4, 1), n, m).shape == (n,)
     grid = torch.arange(8, dtype=torch.float32).reshape(2, 4)  # [n/128, m/128] blocks: first column block per row block
-    assert cz.scale_shape(grid, n, m).tolist() == [0.0] * 128 + [4.0] * 128
+    assert cz.scale_rows(grid, n, m).tolist() == [0.0] * 128 + [4.0] * 128
+    odd = torch.ones(3)  # 3 does not divide 256: left for the builder to reject
+    assert cz.scale_rows(odd, n, m) is odd
+    assert cz.scale_rows(torch.ones(2, 2, 2), n, m).shape == (2, 2, 2)
     assert cz.scale_keys(torch.tensor([1.0])).dtype == torch.uint16
+    assert cz.scale_keys(torch.tensor([1.0])).view(torch.float16).item() == 1.0
     assert cz.scale_keys(torch.tensor([1.0], dtype=torch.float16)).view(torch.float16).item() == 1.0
-    assert cz.fp8_bytes(torch.zeros(2, 3, dtype=torch.float8_e4m3fn), (2, 3)).dtype == torch.uint8
-    with pytest.raises(ValueError, match="FP8 numel mismatch"):
-        cz.fp8_bytes(torch.zeros(5, dtype=torch.uint8), (2, 3))
+    assert cz.scale_keys(torch.tensor([2], dtype=torch.int32)).dtype == torch.bfloat16
+    b = torch.tensor([1.5], dtype=torch.bfloat16)
+    assert cz.scale_keys(b) is b
+    assert cz.fp8_bytes(torch.zeros(2, 3, dtype=torch.float8_e4m3fn), 2, 3).dtype == torch.uint8
+    # 16-bit stores keep their bytes; float32 stores are rounded to bf16 byte pairs first
+    h = torch.tensor([[0x1234, 0xABCD]], dtype=torch.int32).to(torch.uint16).view(torch.bfloat16)
+    assert cz.fp8_bytes(h, 1, 4).tolist() == [[0x34, 0x12, 0xCD, 0xAB]]
+    f = torch.tensor([[1.0, -2.0]], dtype=torch.float32)
+    assert cz.fp8_bytes(f, 1, 4).tolist() == [[0x80, 0x3F, 0x00, 0xC0]]
+    with pytest.raises(ValueError, match="needs 6"):
+        cz.fp8_bytes(torch.zeros(5, dtype=torch.uint8), 2, 3)
 
 
 @pytest.mark.gpu
