@@ -92,10 +92,14 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
 typedef struct mps_fp8_plan mps_fp8_plan;
 int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stream, mps_fp8_plan **plan_out);
 int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream);
-/* A plan of one tensor, decoded into `out` (device, n*m BF16) instead of the
- * output it was created with. Its flags go to the device status word
- * (mps_fp8_read_status), as a single-tensor decode's do: this serves the
- * drop-in decode op's per-sidecar plan cache. */
+/* Decode the plan into a buffer laid out like the outputs it was created
+ * with, moved to `out`: every tensor's output moves by (out - the first
+ * tensor's output at creation), in BF16 elements. A plan of one tensor decodes
+ * into any n*m buffer; a plan whose tensors' outputs are row slices of one
+ * weight decodes into any buffer of that weight's size. The flags go to the
+ * device status word (mps_fp8_read_status), as a single-tensor decode's do.
+ * This serves the drop-in decode op's per-sidecar plan cache and the vLLM
+ * method's scratch slots. */
 int mps_fp8_plan_decode_into(mps_fp8_plan *plan, uint16_t *out, void *stream);
 /* The plan's work list (for profiling tools): work items (buckets, and the row
  * ranges of the buckets it split), bytes of LDS per workgroup. */

@@ -1283,11 +1283,11 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
   }
 }
 
-// out0: when not null, the output of every item (a plan of one tensor decoding
-// into a buffer other than the one it was created with).
+// out_delta: elements every tensor's output moves by (a plan decoding into a
+// buffer laid out like, but other than, the one it was created with).
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
                                                           const WorkItem *__restrict__ work, int64_t nwork,
-                                                          uint32_t *status, uint16_t *out0) {
+                                                          uint32_t *status, int64_t out_delta) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   if ((int64_t)blockIdx.x >= nwork) return;
   // The next bucket's record (scalar registers) is loaded with this bucket's
@@ -1297,7 +1297,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
     const int64_t inext = i + gridDim.x;
     const WorkItem wn = work[inext < nwork ? inext : i];
     const mps_fp8_tensor &T = tensors[w.tensor];
-    decode_bucket(T, out0 ? out0 : T.out, w, lds, status);
+    decode_bucket(T, T.out + out_delta, w, lds, status);
     end_bucket();
     w = wn;
   }
@@ -1569,6 +1569,7 @@ struct mps_fp8_plan {
   uint32_t *d_status = nullptr;
   mps_fp8_tensor *d_tensors = nullptr;
   WorkItem *d_work = nullptr;
+  uint16_t *first_out = nullptr;  // the first tensor's output at creation (decode_into moves all by one offset)
   int64_t count = 0;
   int64_t work_items = 0;
   int device = 0;
@@ -1712,6 +1713,7 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   if (!p) return fail(MPS_ERR_NO_MEMORY, "out of memory");
   p->count = count;
   p->device = device;
+  p->first_out = count > 0 ? tensors[0].out : nullptr;
   hipError_t e = hipMalloc(&p->d_block, bytes);
   if (e != hipSuccess) {
     delete p;
@@ -1788,13 +1790,13 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
 }
 
 namespace {
-int plan_launch(mps_fp8_plan *plan, uint16_t *out0, void *stream) {
+int plan_launch(mps_fp8_plan *plan, int64_t out_delta, uint32_t *status, void *stream) {
   if (plan->work_items == 0) return MPS_OK;
   unsigned grid = 0;
   const int rc = persistent_grid(plan->work_items, &grid);
   if (rc != MPS_OK) return rc;
   hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                     plan->d_tensors, plan->d_work, plan->work_items, plan->d_status, out0);
+                     plan->d_tensors, plan->d_work, plan->work_items, status, out_delta);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
@@ -1803,15 +1805,21 @@ int plan_launch(mps_fp8_plan *plan, uint16_t *out0, void *stream) {
 int mps_fp8_plan_decode(mps_fp8_plan *plan, void *stream) {
   last_error().clear();
   if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
-  return plan_launch(plan, nullptr, stream);
+  return plan_launch(plan, 0, plan->d_status, stream);
 }
 
 int mps_fp8_plan_decode_into(mps_fp8_plan *plan, uint16_t *out, void *stream) {
   last_error().clear();
   if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
   if (!out) return fail(MPS_ERR_INVALID_ARGUMENT, "out is NULL");
-  if (plan->count != 1) return fail(MPS_ERR_INVALID_ARGUMENT, "decode into another output needs a plan of one tensor");
-  return plan_launch(plan, out, stream);
+  if (plan->count == 0) return MPS_OK;
+  uint32_t *status = nullptr;
+  const int rc = status_word(plan->device, &status);
+  if (rc != MPS_OK) return rc;
+  const intptr_t delta = reinterpret_cast<intptr_t>(out) - reinterpret_cast<intptr_t>(plan->first_out);
+  if (delta % (intptr_t)sizeof(uint16_t) != 0)
+    return fail(MPS_ERR_INVALID_ARGUMENT, "out must be 2-byte aligned like the plan's outputs");
+  return plan_launch(plan, (int64_t)(delta / (intptr_t)sizeof(uint16_t)), status, stream);
 }
 
 int mps_fp8_plan_info(const mps_fp8_plan *plan, int64_t *work_items, int64_t *lds_bytes) {
@@ -1884,7 +1892,7 @@ int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, i
   rc = persistent_grid(total, &grid);
   if (rc != MPS_OK) return rc;
   hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, st, d_tensors, d_work, total, status,
-                     static_cast<uint16_t *>(nullptr));
+                     (int64_t)0);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }

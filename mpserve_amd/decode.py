@@ -101,6 +101,26 @@ class DecodePlan:
             _native.check(_native.lib().mps_fp8_plan_decode(self._plan, ctypes.c_void_p(h)))
         return self.outputs
 
+    def decode_into(self, out: torch.Tensor, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """Decode into ``out`` instead of the outputs given at creation: ``out`` is a
+        contiguous bfloat16 buffer laid out like them, every tensor's output moving by
+        the offset of ``out`` from the first one (a single tensor, or row slices of
+        one weight). Flags go to the device status word, as the op's do."""
+        first = self.outputs[0] if self.outputs else None
+        if first is not None:
+            lo = min(o.data_ptr() for o in self.outputs)
+            span = max(o.data_ptr() + 2 * o.numel() for o in self.outputs) - lo
+            if lo != first.data_ptr():
+                raise ValueError("decode_into needs the plan's first output to be its lowest")
+            if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.device != self.device \
+                    or 2 * out.numel() < span:
+                raise ValueError("out must be a contiguous bfloat16 buffer on the plan's device covering its outputs")
+            h = stream.cuda_stream if stream is not None else _stream_handle(self.device)
+            with torch.cuda.device(self.device):
+                _native.check(_native.lib().mps_fp8_plan_decode_into(self._plan, ctypes.c_void_p(out.data_ptr()),
+                                                                     ctypes.c_void_p(h)))
+        return out
+
     def read_status(self, stream: torch.cuda.Stream | None = None) -> int:
         """MPS_STATUS_* flags this plan's decodes recorded since the last read (synchronises)."""
         v = ctypes.c_uint32(0)

@@ -1,27 +1,34 @@
 """vLLM quantization method ``fp8_huffman`` on ROCm / MI355X.
 
-Keeps the reference plugin's surface (scripts/mpserve_vllm_fp8_huffman.py):
-the registration name ``"fp8_huffman"`` (:95), ``FP8HuffmanConfig`` with its
-``max_len`` / ``include_regex`` / ``ignore_regex`` keys and the
+The surface vLLM sees is the reference plugin's
+(scripts/mpserve_vllm_fp8_huffman.py): the registration name
+``"fp8_huffman"`` (:95), ``FP8HuffmanConfig`` with its ``max_len`` /
+``include_regex`` / ``ignore_regex`` keys and the
 ``MPSERVE_ENABLE_FP8_HUFFMAN=1`` gate (:98-148), and
 ``FP8HuffmanLinearMethod`` with the same thirteen ``huff_*`` parameters, the
 discarded ``weight`` / ``weight_scale_inv`` / ``weight_scale`` parameters, the
-three buffers and the shard-aware loaders (:155-360).
+three buffers and the shard map of merged layers (:155-360). ``apply()``
+returns what the reference's does (:389-665): ``x @ W.T`` (+ bias) for the BF16
+weight W rebuilt bit-exact from FP8 bytes + sidecar.
 
-``apply()`` keeps the reference's result (BF16 weight rebuilt from FP8 bytes +
-sidecar, then ``x @ W.T`` plus bias, :389-665) and changes how it gets there:
+How it gets there is this build's own:
 
-* every shard of a merged layer (qkv, gate_up) decodes straight into its row
-  slice of one BF16 scratch weight, all shards in one launch of a
-  ``DecodePlan`` (the reference decodes shard by shard into fresh tensors and
-  concatenates them, :526-543);
-* the scratch is a per-device pool keyed by weight size, shared by every layer
-  of that size (two slots, so a prefetch of the next layer can overlap the
-  current GEMM) instead of a fresh allocation per call;
-* ``prefetch(layer)`` enqueues a layer's decode on a side stream; ``apply()``
-  then waits on its event instead of decoding. Setting
-  ``MPSERVE_FP8_HUFFMAN_CACHE=1`` keeps each layer's decoded weight resident
-  (decode once, memory of a BF16 model).
+* Loading keeps each shard's sidecar tensors per shard index; at
+  ``process_weights_after_loading`` every layer gets a ``_LayerDecode``: the
+  sidecars in row order, their layer-pack rows (if any), and one
+  ``DecodePlan`` that decodes every shard straight into its row slice of one
+  BF16 weight buffer (one launch; the reference decodes shard by shard into
+  fresh tensors and concatenates them, :526-543). Plan creation happens there,
+  after loading: it synchronises the current stream once and allocates; a
+  forward pass then only launches.
+* The weight buffer is a scratch slot shared by every layer of the same size
+  (``ScratchPool``); plans are relocatable, so slot 1 serves ``prefetch()``,
+  which decodes the next layer on a side stream while the current GEMM runs.
+  ``MPSERVE_FP8_HUFFMAN_CACHE=1`` instead gives each layer its own buffer,
+  decoded once at load time (the memory of a BF16 model, no decode per step).
+* A layer of a packed attention/MLP block (non-empty
+  ``huff_attn_block_row_*``) multiplies by its row slice of its leader's
+  (the block's ``o_proj``) decoded weight, as the reference does (:559-655).
 
 Importing this module requires vLLM (as the reference's does); it registers
 the method as a side effect.
@@ -31,8 +38,8 @@ from __future__ import annotations
 import os
 import re
 import weakref
-from dataclasses import dataclass
-from typing import Any, Dict, List, Optional, Tuple, cast
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -45,8 +52,8 @@ from vllm.model_executor.layers.quantization.base_config import (  # noqa: E402
 )
 from vllm.model_executor.parameter import BasevLLMParameter  # noqa: E402
 
-# prefix -> layer, for the layer-pack path (a shard of a leader's packed weight)
-_PREFIX_TO_LAYER: "weakref.WeakValueDictionary[str, torch.nn.Module]" = weakref.WeakValueDictionary()
+ENV_ENABLE = "MPSERVE_ENABLE_FP8_HUFFMAN"
+ENV_CACHE = "MPSERVE_FP8_HUFFMAN_CACHE"
 
 # Parameters the compress script writes per module, with their stored dtypes
 # (scripts/compress_llm_fp8_huffman.py:284-306; safetensors has no unsigned
@@ -64,10 +71,14 @@ HUFF_PARAMS: Tuple[Tuple[str, torch.dtype], ...] = (
     ("huff_bucket_thread_startbit_u32", torch.int32),
     ("huff_bucket_bit_base_i64", torch.int64),
 )
-_PACK_PARAMS = ("huff_attn_block_row_start_i32", "huff_attn_block_row_len_i32")
+PACK_PARAMS = ("huff_attn_block_row_start_i32", "huff_attn_block_row_len_i32")
 # shard id -> row-block index of a merged layer (reference :176-184)
 SHARD_INDEX: Dict[object, int] = {0: 0, 1: 1, "q": 0, "k": 1, "v": 2, "gate": 0, "up": 1}
+# the reference's default ignore list (:105)
 DEFAULT_IGNORE = r"(^lm_head$|^model\.visual\.|.*\.mlp\.gate$|.*\.mlp\.shared_expert_gate$)"
+
+# prefix -> layer, so that a packed layer finds its block's leader
+_LAYERS_BY_PREFIX: "weakref.WeakValueDictionary[str, torch.nn.Module]" = weakref.WeakValueDictionary()
 
 
 @dataclass(frozen=True)
@@ -75,9 +86,26 @@ class FP8HuffmanParams:
     max_len: int = 7
 
 
+class _PrefixFilter:
+    """Which linear layers the method takes: none on the ignore list; of the
+    rest, all when there is no include pattern, else those it matches."""
+
+    def __init__(self, include: Optional[str], ignore: Optional[str]):
+        self._include = re.compile(include) if include else None
+        self._ignore = re.compile(ignore) if ignore else None
+
+    def accepts(self, prefix: str) -> bool:
+        if self._ignore is not None and self._ignore.search(prefix):
+            return False
+        return self._include is None or self._include.search(prefix) is not None
+
+
 @register_quantization_config("fp8_huffman")
 class FP8HuffmanConfig(QuantizationConfig):
     """Config of the ``fp8_huffman`` method (reference :95-148)."""
+
+    # config.json keys and their defaults (from_config)
+    _KEYS = (("max_len", 7), ("include_regex", None), ("ignore_regex", None))
 
     def __init__(self, *, max_len: int = 7, include_regex: str | None = None,
                  ignore_regex: str | None = DEFAULT_IGNORE) -> None:
@@ -86,10 +114,9 @@ class FP8HuffmanConfig(QuantizationConfig):
             raise ValueError("fp8_huffman currently requires max_len=7")
         self.params = FP8HuffmanParams(max_len=int(max_len))
         self.include_regex = include_regex
-        self._include_re = re.compile(include_regex) if include_regex else None
         self.ignore_regex = ignore_regex
-        self._ignore_re = re.compile(ignore_regex) if ignore_regex else None
-        self._enabled = os.environ.get("MPSERVE_ENABLE_FP8_HUFFMAN", "0") == "1"
+        self._filter = _PrefixFilter(include_regex, ignore_regex)
+        self._enabled = os.environ.get(ENV_ENABLE, "0") == "1"
 
     def get_name(self) -> str:
         return "fp8_huffman"
@@ -108,23 +135,25 @@ class FP8HuffmanConfig(QuantizationConfig):
 
     @classmethod
     def from_config(cls, config: dict) -> "FP8HuffmanConfig":
-        return cls(max_len=int(config.get("max_len", 7)), include_regex=config.get("include_regex", None),
-                   ignore_regex=config.get("ignore_regex", None))
+        kw = {k: config.get(k, d) for k, d in cls._KEYS}
+        kw["max_len"] = int(kw["max_len"])
+        return cls(**kw)
 
     def get_quant_method(self, layer: torch.nn.Module, prefix: str) -> Optional[QuantizeMethodBase]:
+        # gate off: every layer stays unquantized (the reference returns that for any layer)
         if not self._enabled:
             return UnquantizedLinearMethod()
-        if isinstance(layer, LinearBase):
-            if self._ignore_re is not None and self._ignore_re.search(prefix) is not None:
-                return UnquantizedLinearMethod()
-            if self._include_re is None or self._include_re.search(prefix) is not None:
-                return FP8HuffmanLinearMethod(self.params)
-            return UnquantizedLinearMethod()
-        return None
+        if not isinstance(layer, LinearBase):
+            return None
+        if self._filter.accepts(prefix):
+            return FP8HuffmanLinearMethod(self.params)
+        return UnquantizedLinearMethod()
 
 
-class _ScratchPool:
-    """BF16 scratch weights per (device, numel, slot), reused by every layer of that size."""
+class ScratchPool:
+    """BF16 weight buffers keyed by (device, elements, slot), shared by every
+    layer of that size: slot 0 is the weight apply() multiplies by, slot 1 the
+    one prefetch() fills for the next layer."""
 
     def __init__(self) -> None:
         self._bufs: Dict[Tuple[int, int, int], torch.Tensor] = {}
@@ -133,21 +162,78 @@ class _ScratchPool:
         key = (device.index if device.index is not None else torch.cuda.current_device(), int(numel), int(slot))
         buf = self._bufs.get(key)
         if buf is None:
-            buf = torch.empty(int(numel), dtype=torch.bfloat16, device=device)
-            self._bufs[key] = buf
+            buf = self._bufs[key] = torch.empty(int(numel), dtype=torch.bfloat16, device=device)
         return buf
 
     def clear(self) -> None:
         self._bufs.clear()
 
 
-SCRATCH = _ScratchPool()
+SCRATCH = ScratchPool()
 
 
-def _as_tensor(x: Any) -> torch.Tensor:
-    if isinstance(x, torch.Tensor):
-        return x
-    return cast(torch.Tensor, cast(Any, x)[:])
+class _HuffParamLoader:
+    """weight_loader of one ``huff_*`` parameter.
+
+    A lazily loaded tensor (one that materialises on ``[:]``) is read and moved
+    to the parameter's device. Without a shard id (or for an unmerged layer) it
+    replaces the parameter's data, unless it is smaller than the placeholder.
+    With one, it is kept as that shard's array in the layer's
+    ``_fp8_huff_shards[row block][name]``; the reference keeps the same arrays
+    per parameter name (:200-229).
+    """
+
+    def __init__(self, layer: torch.nn.Module, name: str, merged: bool):
+        self.layer_ref = weakref.ref(layer)
+        self.name = name
+        self.merged = merged
+
+    def __call__(self, param: torch.Tensor, loaded_weight, shard_id: object | None = None, *args, **kwargs) -> None:
+        src = loaded_weight if isinstance(loaded_weight, torch.Tensor) else loaded_weight[:]
+        t = src.to(device=param.device).contiguous()
+        if not self.merged or shard_id is None:
+            if t.numel() >= param.data.numel():
+                param.data = t
+            return
+        if shard_id not in SHARD_INDEX:
+            raise ValueError(f"Unknown shard_id for fp8_huffman: {shard_id!r}")
+        layer = self.layer_ref()
+        layer.__dict__.setdefault("_fp8_huff_shards", {}).setdefault(SHARD_INDEX[shard_id], {})[self.name] = t
+
+
+def _discard(param: torch.Tensor, loaded_weight, *args, **kwargs) -> None:
+    """weight_loader of the checkpoint's FP8 weight and scales: the sidecar carries them."""
+
+
+@dataclass
+class _LayerDecode:
+    """What a layer needs at apply(): set up once, by process_weights_after_loading."""
+    out_features: int
+    in_features: int
+    pack: Optional[Tuple[int, int]] = None           # (first row, rows) in the block leader's weight
+    plan: Optional[object] = None                    # DecodePlan into `weight`'s buffer
+    weight: Optional[torch.Tensor] = None            # BF16 [N, K] the plan decodes into
+    cached: bool = False                             # weight decoded once, kept
+    pending: Optional[Tuple[torch.cuda.Event, torch.Tensor]] = None  # a prefetch's (event, weight)
+    extra: Dict[str, object] = field(default_factory=dict)
+
+
+def _as_2d(fp8: torch.Tensor, k: int) -> torch.Tensor:
+    """A shard's FP8 bytes as [rows, k]: stored 2-D, or flat with a multiple of k bytes."""
+    if fp8.numel() == 0:
+        raise RuntimeError(f"fp8_huffman: a shard's huff_fp8_u8 is empty (shape {tuple(fp8.shape)}): "
+                           "its sidecar was not loaded (is the shard id mapped?)")
+    if fp8.dim() == 2:
+        return fp8
+    if fp8.dim() == 1 and k > 0 and fp8.numel() % k == 0:
+        return fp8.view(-1, k)
+    raise ValueError(f"fp8_huffman: huff_fp8_u8 of shape {tuple(fp8.shape)} does not hold rows of {k} bytes")
+
+
+def _first_int(t: Optional[torch.Tensor]) -> Optional[int]:
+    if isinstance(t, torch.Tensor) and t.numel() > 0:
+        return int(t.reshape(-1)[0].item())
+    return None
 
 
 class FP8HuffmanLinearMethod(LinearMethodBase):
@@ -160,143 +246,171 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
     def create_weights(self, layer: torch.nn.Module, input_size_per_partition: int,
                        output_partition_sizes: List[int], input_size: int, output_size: int,
                        params_dtype: torch.dtype, **extra_weight_attrs) -> None:
-        tp_rank = getattr(layer, "tp_rank", 0)
-        tp_size = getattr(layer, "tp_size", 1)
-        if int(tp_rank) != 0 or int(tp_size) != 1:
+        if int(getattr(layer, "tp_rank", 0)) != 0 or int(getattr(layer, "tp_size", 1)) != 1:
             raise NotImplementedError("fp8_huffman MVP only supports tp_size=1")
-        num_shards = int(len(output_partition_sizes))
         device = torch.device("cuda" if torch.cuda.is_available() else "cpu")
+        merged = len(output_partition_sizes) > 1
 
-        def _discard_loader(param: torch.Tensor, loaded_weight: torch.Tensor, *args, **kwargs) -> None:
-            return
-
-        def _make_loader(attr_name: str):
-            def _loader(param: torch.Tensor, loaded_weight: torch.Tensor, shard_id: object | None = None,
-                        *args, **kwargs) -> None:
-                tgt = _as_tensor(loaded_weight).to(device=param.device).contiguous()
-                if num_shards <= 1 or shard_id is None:
-                    if int(tgt.numel()) >= int(param.data.numel()):
-                        param.data = tgt
-                    return
-                idx = SHARD_INDEX.get(shard_id, None)
-                if idx is None:
-                    raise ValueError(f"Unknown shard_id for fp8_huffman: {shard_id!r}")
-                shards = getattr(layer, f"_{attr_name}_shards", None)
-                if shards is None:
-                    shards = {}
-                    setattr(layer, f"_{attr_name}_shards", shards)
-                shards[int(idx)] = tgt
-            return _loader
+        def param(data: torch.Tensor, loader) -> BasevLLMParameter:
+            return BasevLLMParameter(data=data, weight_loader=loader)
 
         for name, dtype in HUFF_PARAMS:
-            layer.register_parameter(name, BasevLLMParameter(data=torch.empty((1,), dtype=dtype, device=device),
-                                                             weight_loader=_make_loader(name)))
-        for name in _PACK_PARAMS:
-            layer.register_parameter(name, BasevLLMParameter(data=torch.zeros((0,), dtype=torch.int32, device=device),
-                                                             weight_loader=_make_loader(name)))
-        layer.register_parameter("weight", BasevLLMParameter(data=torch.empty((1,), dtype=torch.uint8, device=device),
-                                                             weight_loader=_discard_loader))
+            layer.register_parameter(name, param(torch.empty((1,), dtype=dtype, device=device),
+                                                 _HuffParamLoader(layer, name, merged)))
+        for name in PACK_PARAMS:
+            layer.register_parameter(name, param(torch.zeros((0,), dtype=torch.int32, device=device),
+                                                 _HuffParamLoader(layer, name, merged)))
+        layer.register_parameter("weight", param(torch.empty((1,), dtype=torch.uint8, device=device), _discard))
         for name in ("weight_scale_inv", "weight_scale"):
-            layer.register_parameter(name, BasevLLMParameter(
-                data=torch.empty((1,), dtype=torch.float16, device=device), weight_loader=_discard_loader))
-        layer.register_buffer("huff_max_len", torch.tensor(int(self.params.max_len), dtype=torch.int32, device=device),
-                              persistent=False)
-        layer.register_buffer("huff_in_features_i32", torch.tensor(int(input_size), dtype=torch.int32, device=device),
-                              persistent=False)
-        layer.register_buffer("huff_out_features_i32",
-                              torch.tensor(int(output_size), dtype=torch.int32, device=device), persistent=False)
+            layer.register_parameter(name, param(torch.empty((1,), dtype=torch.float16, device=device), _discard))
+        for name, value in (("huff_max_len", self.params.max_len), ("huff_in_features_i32", input_size),
+                            ("huff_out_features_i32", output_size)):
+            layer.register_buffer(name, torch.tensor(int(value), dtype=torch.int32, device=device), persistent=False)
+        layer._fp8_huff_sizes = (int(output_size), int(input_size))
+
+    # ------------------------------------------------------------------ after loading
+    @staticmethod
+    def _sidecars(layer: torch.nn.Module) -> List[Dict[str, torch.Tensor]]:
+        """The layer's sidecars in row order (one unless merged). When a shard's
+        FP8 bytes are empty the reference decodes only the largest shard
+        (:495-524); so does this."""
+        per = layer.__dict__.get("_fp8_huff_shards")
+        if not per:
+            return [{name: getattr(layer, name).data for name, _ in HUFF_PARAMS}]
+        shards = [per[i] for i in sorted(per)]
+        sizes = [int(s["huff_fp8_u8"].numel()) if "huff_fp8_u8" in s else 0 for s in shards]
+        if min(sizes) > 0:
+            return shards
+        if max(sizes) <= 0:
+            raise RuntimeError("fp8_huffman: all shard sidecars are empty")
+        return [shards[sizes.index(max(sizes))]]
+
+    @staticmethod
+    def _pack_rows(layer: torch.nn.Module) -> Optional[Tuple[int, int]]:
+        """The layer's rows (first, count) in its block leader's weight, when it is
+        part of a packed block: the span of its shards' row ranges, or its own."""
+        spans = []
+        for shard in (layer.__dict__.get("_fp8_huff_shards") or {}).values():
+            start = _first_int(shard.get(PACK_PARAMS[0]))
+            rows = _first_int(shard.get(PACK_PARAMS[1]))
+            if start is not None and rows is not None and rows > 0:
+                spans.append((start, start + rows))
+        if not spans:
+            start = _first_int(getattr(layer, PACK_PARAMS[0], None))
+            rows = _first_int(getattr(layer, PACK_PARAMS[1], None))
+            if start is not None and rows is not None and rows > 0:
+                spans.append((start, start + rows))
+        if not spans:
+            return None
+        lo, hi = min(a for a, _ in spans), max(b for _, b in spans)
+        return (lo, hi - lo) if hi > lo else None
 
     def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
-        for name in [n for n, _ in HUFF_PARAMS] + list(_PACK_PARAMS):
+        from .decode import DecodePlan
+
+        for name in [n for n, _ in HUFF_PARAMS] + list(PACK_PARAMS):
             p = getattr(layer, name)
             if not isinstance(p, torch.nn.Parameter):
                 setattr(layer, name, torch.nn.Parameter(p, requires_grad=False))
         prefix = getattr(layer, "prefix", None)
         if isinstance(prefix, str) and prefix:
-            _PREFIX_TO_LAYER[prefix] = layer
-        layer._fp8_huff_state = {}
-
-    # ------------------------------------------------------------------ decode
-    @staticmethod
-    def _shards(layer: torch.nn.Module) -> List[Dict[str, torch.Tensor]]:
-        """The layer's sidecars in row order: [{param name: tensor}] (one entry unless merged)."""
-        per = getattr(layer, "_huff_fp8_u8_shards", None)
-        if isinstance(per, dict) and per:
-            order = sorted(per.keys())
-            out = [{name: getattr(layer, f"_{name}_shards")[i] for name, _ in HUFF_PARAMS} for i in order]
-            if any(int(s["huff_fp8_u8"].numel()) == 0 for s in out):
-                # the reference falls back to the largest shard when one is empty (:495-524)
-                best = max(out, key=lambda s: int(s["huff_fp8_u8"].numel()))
-                if int(best["huff_fp8_u8"].numel()) <= 0:
-                    raise RuntimeError("fp8_huffman: all shard sidecars are empty")
-                return [best]
-            return out
-        return [{name: getattr(layer, name) for name, _ in HUFF_PARAMS}]
-
-    @staticmethod
-    def _fp8_2d(t: torch.Tensor, m_in: int) -> torch.Tensor:
-        if t.numel() == 0:
-            raise RuntimeError(f"fp8_huffman: encountered empty fp8_u8 tensor (shape={tuple(t.shape)}). "
-                               "This usually indicates missing/incorrect shard_id remapping during weight loading.")
-        if t.dim() == 2:
-            return t
-        if t.dim() == 1:
-            if m_in <= 0 or t.numel() % m_in != 0:
-                raise ValueError(f"fp8_huffman: invalid fp8_u8 flat shape={tuple(t.shape)} for m_in={m_in}")
-            return t.view(-1, m_in)
-        raise ValueError(f"fp8_huffman: invalid fp8_u8 dim={t.dim()} shape={tuple(t.shape)}")
-
-    def _plan(self, layer: torch.nn.Module, m_in: int, slot: int):
-        """(DecodePlan, BF16 [N, K] weight view) decoding every shard into its row slice."""
-        from .decode import DecodePlan
-
-        state = layer.__dict__.setdefault("_fp8_huff_state", {})
-        cached = state.get(("plan", slot))
-        if cached is not None:
-            return cached
-        shards = self._shards(layer)
-        fp8s = [self._fp8_2d(s["huff_fp8_u8"], m_in) for s in shards]
+            _LAYERS_BY_PREFIX[prefix] = layer
+        out_features, in_features = getattr(layer, "_fp8_huff_sizes", (0, 0))
+        st = _LayerDecode(out_features=out_features, in_features=in_features, pack=self._pack_rows(layer))
+        layer._fp8_huff = st
+        if st.pack is not None:
+            return  # decoded through its block leader
+        sidecars = self._sidecars(layer)
+        fp8s = [_as_2d(s["huff_fp8_u8"], in_features) for s in sidecars]
+        if not fp8s[0].is_cuda:
+            return  # no GPU: the layer loads, and apply() (CUDA only) reports it
         k = int(fp8s[0].shape[1])
         if any(int(f.shape[1]) != k for f in fp8s):
-            raise ValueError("fp8_huffman: shards of one layer must share the input dimension")
-        n_total = sum(int(f.shape[0]) for f in fp8s)
+            raise ValueError("fp8_huffman: the shards of one layer must share the input dimension")
+        rows = sum(int(f.shape[0]) for f in fp8s)
         device = fp8s[0].device
-        if os.environ.get("MPSERVE_FP8_HUFFMAN_CACHE", "0") == "1":
-            flat = torch.empty(n_total * k, dtype=torch.bfloat16, device=device)
-        else:
-            flat = SCRATCH.get(device, n_total * k, slot)
-        items = []
-        row = 0
-        for f, s in zip(fp8s, shards):
+        st.cached = os.environ.get(ENV_CACHE, "0") == "1"
+        flat = (torch.empty(rows * k, dtype=torch.bfloat16, device=device) if st.cached
+                else SCRATCH.get(device, rows * k, 0))
+        items, row = [], 0
+        for f, s in zip(fp8s, sidecars):
             n = int(f.shape[0])
             items.append((f.contiguous(), s, flat[row * k:(row + n) * k]))
             row += n
-        plan = DecodePlan(items)
-        weight = flat.view(n_total, k)
-        state[("plan", slot)] = (plan, weight)
-        return plan, weight
+        st.plan = DecodePlan(items)  # synchronises the current stream once; allocates the plan
+        st.weight = flat.view(rows, k)
+        if st.cached:
+            st.plan.decode()
 
-    def decoded_weight(self, layer: torch.nn.Module, m_in: int, slot: int = 0,
+    # ------------------------------------------------------------------ decode
+    @staticmethod
+    def _state(layer: torch.nn.Module) -> _LayerDecode:
+        st = layer.__dict__.get("_fp8_huff")
+        if st is None:
+            raise RuntimeError(f"fp8_huffman: process_weights_after_loading has not run for "
+                               f"{getattr(layer, 'prefix', type(layer).__name__)!r}")
+        return st
+
+    def decoded_weight(self, layer: torch.nn.Module, m_in: Optional[int] = None, slot: int = 0,
                        stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-        """Enqueue the layer's decode on ``stream`` (default: current) and return the BF16 [N, K] weight."""
-        plan, weight = self._plan(layer, m_in, slot)
-        state = layer.__dict__.setdefault("_fp8_huff_state", {})
-        if os.environ.get("MPSERVE_FP8_HUFFMAN_CACHE", "0") == "1" and state.get("decoded"):
-            return weight
-        plan.decode(stream)
-        state["decoded"] = True
-        return weight
+        """The layer's BF16 [N, K] weight, its decode enqueued on ``stream``
+        (default: current) into scratch ``slot`` (or the layer's own buffer in
+        cache mode, decoded once)."""
+        st = self._state(layer)
+        if st.pack is not None:
+            raise RuntimeError("fp8_huffman: a packed layer's weight is its leader's (see apply)")
+        if st.plan is None:
+            raise RuntimeError("fp8_huffman: the layer's sidecar is not on a GPU")
+        if st.cached:
+            return st.weight
+        if slot == 0:
+            st.plan.decode(stream)
+            return st.weight
+        buf = SCRATCH.get(st.weight.device, st.weight.numel(), slot)
+        st.plan.decode_into(buf, stream)
+        return buf.view(st.weight.shape)
 
-    def prefetch(self, layer: torch.nn.Module, m_in: int, stream: torch.cuda.Stream, slot: int = 1) -> None:
-        """Decode ``layer`` on ``stream`` into scratch ``slot``; its next ``apply()`` waits for it.
-
-        The caller keeps ``slot`` apart from the scratch a running GEMM reads (alternate
-        slots between consecutive layers of one size).
-        """
-        weight = self.decoded_weight(layer, m_in, slot=slot, stream=stream)
+    def prefetch(self, layer: torch.nn.Module, m_in: Optional[int] = None, stream: Optional[torch.cuda.Stream] = None,
+                 slot: int = 1) -> None:
+        """Decode ``layer`` on ``stream`` into scratch ``slot``; its next ``apply()``
+        waits for that decode instead of decoding. The caller keeps ``slot`` apart
+        from the scratch a running GEMM reads (alternate slots between consecutive
+        layers of one size). The first prefetch into a slot of a new size
+        allocates that slot."""
+        st = self._state(layer)
+        w = self.decoded_weight(layer, slot=slot, stream=stream)
         ev = torch.cuda.Event()
-        ev.record(stream)
-        layer.__dict__.setdefault("_fp8_huff_state", {})["pending"] = (ev, weight)
+        ev.record(stream if stream is not None else torch.cuda.current_stream(w.device))
+        st.pending = (ev, w)
+
+    def _leader_weight(self, layer: torch.nn.Module, st: _LayerDecode) -> torch.Tensor:
+        """A packed layer's rows of its block leader's (``<block>.self_attn.o_proj``) weight."""
+        prefix = getattr(layer, "prefix", "") or ""
+        for part in (".self_attn.", ".mlp."):
+            if part in prefix:
+                leader_prefix = prefix.split(part, 1)[0] + ".self_attn.o_proj"
+                break
+        else:
+            raise RuntimeError(f"fp8_huffman: {prefix!r} is packed but not in an attention or MLP block")
+        leader = _LAYERS_BY_PREFIX.get(leader_prefix)
+        if leader is None:
+            raise RuntimeError(f"fp8_huffman: cannot find layer-pack leader {leader_prefix!r} for {prefix!r}")
+        method = getattr(leader, "quant_method", None)
+        method = method if isinstance(method, FP8HuffmanLinearMethod) else self
+        w_full = method._weight_for_apply(leader)
+        start, rows = st.pack
+        return w_full[start:start + rows]
+
+    def _weight_for_apply(self, layer: torch.nn.Module) -> torch.Tensor:
+        st = self._state(layer)
+        if st.pack is not None:
+            return self._leader_weight(layer, st)
+        if st.pending is not None:
+            ev, w = st.pending
+            st.pending = None
+            torch.cuda.current_stream(w.device).wait_event(ev)
+            return w
+        return self.decoded_weight(layer)
 
     # ------------------------------------------------------------------ apply
     def apply(self, layer: torch.nn.Module, x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
@@ -304,82 +418,17 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
             raise ValueError("fp8_huffman requires CUDA tensors")
         if x.dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("fp8_huffman expects activations in bf16 or fp16")
+        st = self._state(layer)
         if x.numel() == 0:
-            out_features = 0
-            if hasattr(layer, "huff_out_features_i32"):
-                out_features = int(getattr(layer, "huff_out_features_i32").item())
-            if out_features <= 0 and hasattr(layer, "output_size"):
-                out_features = int(getattr(layer, "output_size"))
-            if out_features <= 0:
-                raise RuntimeError("fp8_huffman: cannot infer out_features for empty-token run "
-                                   f"(prefix={getattr(layer, 'prefix', None)!r}, "
-                                   f"layer_type={type(layer).__name__})")
-            out = torch.empty(x.shape[:-1] + (out_features,), dtype=x.dtype, device=x.device)
-            if bias is not None and out.numel() > 0:
-                out.add_(bias)
-            return out
-
-        x2d = x.reshape(-1, x.shape[-1])
-        m_in = int(x2d.shape[1])
-        w = self._packed_weight(layer, m_in)
-        if w is None:
-            state = layer.__dict__.setdefault("_fp8_huff_state", {})
-            pending = state.pop("pending", None)
-            if pending is not None:
-                ev, w = pending
-                torch.cuda.current_stream(x.device).wait_event(ev)
-            else:
-                w = self.decoded_weight(layer, m_in, slot=0)
-        if x.dtype == torch.float16 and w.dtype != torch.float16:
+            n_out = st.out_features or int(getattr(layer, "output_size", 0) or 0)
+            if n_out <= 0:
+                raise RuntimeError(f"fp8_huffman: no output size known for {getattr(layer, 'prefix', None)!r}")
+            y = torch.empty(x.shape[:-1] + (n_out,), dtype=x.dtype, device=x.device)
+            return y.add_(bias) if bias is not None and y.numel() > 0 else y
+        w = self._weight_for_apply(layer)
+        if x.dtype == torch.float16:
             w = w.to(torch.float16)
-        out = torch.matmul(x2d, w.t())
+        y = torch.matmul(x.reshape(-1, x.shape[-1]), w.t())
         if bias is not None:
-            out.add_(bias)
-        return out.reshape(x.shape[:-1] + (out.shape[-1],))
-
-    # The layer-pack path (reference :559-655): a layer whose huff_attn_block_*
-    # metadata is non-empty is a row slice of its layer's leader (o_proj).
-    @staticmethod
-    def _pack_meta(layer: torch.nn.Module) -> Optional[Tuple[int, int]]:
-        d_rs = getattr(layer, "_huff_attn_block_row_start_i32_shards", None)
-        d_rl = getattr(layer, "_huff_attn_block_row_len_i32_shards", None)
-        if isinstance(d_rs, dict) and isinstance(d_rl, dict) and d_rs:
-            spans = []
-            for si, rs in d_rs.items():
-                rl = d_rl.get(si)
-                if isinstance(rs, torch.Tensor) and isinstance(rl, torch.Tensor) and rs.numel() and rl.numel():
-                    s, ln = int(rs.reshape(-1)[0].item()), int(rl.reshape(-1)[0].item())
-                    if ln > 0:
-                        spans.append((s, s + ln))
-            if spans:
-                lo, hi = min(a for a, _ in spans), max(b for _, b in spans)
-                return (lo, hi - lo) if hi > lo else None
-        rs = getattr(layer, "huff_attn_block_row_start_i32", None)
-        rl = getattr(layer, "huff_attn_block_row_len_i32", None)
-        if isinstance(rs, torch.Tensor) and isinstance(rl, torch.Tensor) and rs.numel() and rl.numel():
-            s, ln = int(rs.reshape(-1)[0].item()), int(rl.reshape(-1)[0].item())
-            if ln > 0:
-                return s, ln
-        return None
-
-    def _packed_weight(self, layer: torch.nn.Module, m_in: int) -> Optional[torch.Tensor]:
-        meta = self._pack_meta(layer)
-        if meta is None:
-            return None
-        prefix = getattr(layer, "prefix", None)
-        if not isinstance(prefix, str) or not prefix:
-            return None
-        if ".self_attn." in prefix:
-            leader_prefix = prefix.split(".self_attn.", 1)[0] + ".self_attn.o_proj"
-        elif ".mlp." in prefix:
-            leader_prefix = prefix.split(".mlp.", 1)[0] + ".self_attn.o_proj"
-        else:
-            return None
-        leader = _PREFIX_TO_LAYER.get(leader_prefix, None)
-        if leader is None:
-            raise RuntimeError(f"fp8_huffman: cannot find layer-pack leader {leader_prefix!r} for {prefix!r}")
-        method = getattr(leader, "quant_method", None)
-        method = method if isinstance(method, FP8HuffmanLinearMethod) else self
-        w_full = method.decoded_weight(leader, m_in, slot=0)
-        row_start, row_len = meta
-        return w_full[row_start:row_start + row_len]
+            y.add_(bias)
+        return y.reshape(x.shape[:-1] + (y.shape[-1],))

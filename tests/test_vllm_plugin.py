@@ -126,12 +126,13 @@ def test_loaders_unsharded_and_sharded():
     merged, _ = make_layer("model.layers.0.self_attn.qkv_proj", [40, 8, 8], 64)
     for sid in ("q", "k", "v"):
         load(merged, t, sid)
-    assert sorted(merged._huff_fp8_u8_shards) == [0, 1, 2]
+    assert sorted(merged._fp8_huff_shards) == [0, 1, 2]
+    assert set(merged._fp8_huff_shards[1]) == set(t)  # every huff_* array of the k shard
     with pytest.raises(ValueError, match="Unknown shard_id"):
         merged.huff_fp8_u8.weight_loader(merged.huff_fp8_u8, t["huff_fp8_u8"], "o")
     method.process_weights_after_loading(layer)
     assert isinstance(layer.huff_fp8_u8, torch.nn.Parameter)
-    assert vfh._PREFIX_TO_LAYER["model.layers.0.self_attn.o_proj"] is layer
+    assert vfh._LAYERS_BY_PREFIX["model.layers.0.self_attn.o_proj"] is layer
 
 
 def test_apply_rejects_cpu_and_bad_dtypes():
@@ -191,3 +192,81 @@ def test_prefetch_on_side_stream():
     out = method.apply(layer, x)
     torch.cuda.synchronize()
     assert torch.allclose(out.float(), torch.matmul(x, w.t()).float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.gpu
+def test_plans_built_at_load_and_reused_by_apply(monkeypatch):
+    """process_weights_after_loading builds the layer's plan; apply() and
+    prefetch() (into the relocated slot 1) launch it without building another."""
+    k = 1024
+    parts = [synth(128, k, seed=220), synth(64, k, seed=221)]
+    layer, method = make_layer("model.layers.1.mlp.gate_up_proj", [128, 64], k)
+    for sid, (bf, q, sc) in zip(("gate", "up"), parts):
+        load(layer, _to(stored_sidecar(bf, q, sc), DEV), sid)
+    method.process_weights_after_loading(layer)
+    st = layer._fp8_huff
+    plan = st.plan
+    assert plan is not None and st.weight.shape == (192, k)
+    w = torch.from_numpy(np.concatenate([p[0] for p in parts])).view(torch.bfloat16).to(DEV)
+    x = torch.randn((4, k), device=DEV).to(torch.bfloat16)
+    for _ in range(2):
+        out = method.apply(layer, x)
+        assert layer._fp8_huff.plan is plan
+        assert torch.allclose(out.float(), torch.matmul(x, w.t()).float(), rtol=1e-2, atol=1e-2)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    method.prefetch(layer, k, side, slot=1)
+    slot1 = layer._fp8_huff.pending[1]
+    assert slot1.data_ptr() != st.weight.data_ptr()
+    out = method.apply(layer, x)
+    torch.cuda.synchronize()
+    assert torch.equal(slot1.view(torch.uint16), w.view(torch.uint16))
+    assert torch.allclose(out.float(), torch.matmul(x, w.t()).float(), rtol=1e-2, atol=1e-2)
+    from mpserve_amd.mpserve_cuda import read_status
+
+    assert read_status(torch.device(DEV)) == 0
+
+
+@pytest.mark.gpu
+def test_cache_mode_decodes_once_at_load(monkeypatch):
+    monkeypatch.setenv("MPSERVE_FP8_HUFFMAN_CACHE", "1")
+    k = 512
+    bf, q, sc = synth(96, k, seed=230)
+    layer, method = make_layer("model.layers.2.self_attn.o_proj", [96], k)
+    load(layer, _to(stored_sidecar(bf, q, sc), DEV))
+    method.process_weights_after_loading(layer)
+    torch.cuda.synchronize()
+    st = layer._fp8_huff
+    assert st.cached and torch.equal(st.weight.view(torch.uint16).cpu(), torch.from_numpy(bf))
+    st.weight.view(torch.int16)[0, 0] = 12345  # a marker: apply() must not decode again
+    x = torch.randn((2, k), device=DEV).to(torch.bfloat16)
+    method.apply(layer, x)
+    torch.cuda.synchronize()
+    assert int(st.weight.view(torch.int16)[0, 0]) == 12345
+
+
+@pytest.mark.gpu
+def test_packed_block_layers_use_the_leaders_rows():
+    """A layer with huff_attn_block_row_* multiplies by its rows of the block
+    leader's (o_proj) decoded weight (reference :559-655)."""
+    k = 1024
+    bf, q, sc = synth(384, k, seed=240)  # the leader's packed weight: qkv rows 0..255, gate rows 256..383
+    leader, lm = make_layer("model.layers.5.self_attn.o_proj", [384], k)
+    load(leader, _to(stored_sidecar(bf, q, sc), DEV))
+    leader.quant_method = lm
+    lm.process_weights_after_loading(leader)
+    w = torch.from_numpy(bf).view(torch.bfloat16).to(DEV)
+    packed = []
+    for prefix, start, rows in (("model.layers.5.self_attn.qkv_proj", 0, 256), ("model.layers.5.mlp.gate_proj", 256, 128)):
+        layer, method = make_layer(prefix, [rows], k)
+        t = {"huff_attn_block_row_start_i32": torch.tensor([start], dtype=torch.int32),
+             "huff_attn_block_row_len_i32": torch.tensor([rows], dtype=torch.int32)}
+        load(layer, _to(t, DEV))
+        method.process_weights_after_loading(layer)
+        assert layer._fp8_huff.pack == (start, rows) and layer._fp8_huff.plan is None
+        packed.append((layer, method, start, rows))
+    x = torch.randn((3, k), device=DEV).to(torch.bfloat16)
+    for layer, method, start, rows in packed:
+        out = method.apply(layer, x)
+        assert out.shape == (3, rows)
+        assert torch.allclose(out.float(), torch.matmul(x, w[start:start + rows].t()).float(), rtol=1e-2, atol=1e-2)
