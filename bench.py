@@ -84,6 +84,11 @@ def parse_args(argv=None):
     p.add_argument("--no-verify", action="store_true", help="skip the bit-exact check of the outputs")
     p.add_argument("--no-per-tensor", action="store_true",
                    help="layer workloads: skip the per-tensor timings (profiling runs that count one launch kind)")
+    p.add_argument("--compare-libs", nargs="+", default=None, metavar="LIB",
+                   help="instead of the benchmark: time the decode plan of --workload (default model8b) with each "
+                        "of these libmpserve_amd builds (python -m mpserve_amd.build --define ... --out LIB) in this "
+                        "one process, launches interleaved in rounds; prints one JSON line of medians")
+    p.add_argument("--compare-rounds", type=int, default=6, help="--compare-libs: rounds (20 launches per library each)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="after the timed steps, run 3 plain int32 elementwise copies of MIB MiB each "
                         "(reference kernel of known bytes for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -711,6 +716,78 @@ def run_single(args, dev) -> int:
     return 0
 
 
+def compare_libs(args, dev) -> int:
+    """Decode-plan launch time of one workload with several builds of the library,
+    measured in one process: the same inputs, one plan per library, 20 events-timed
+    launches per library per round, the order reversed every other round. Box-to-box
+    spread is several percent; within one process it is about 0.1%, which is what
+    tuning the kernel's compile-time knobs needs."""
+    import ctypes
+    import statistics
+
+    import torch
+
+    from mpserve_amd import _native
+    from mpserve_amd.decode import sidecar_decode_args
+    from mpserve_amd.mpserve_cuda import _descriptor
+    from mpserve_amd.synthetic import config_weights
+
+    workload = "model8b" if args.workload in ("all", "gemm8b", "awq8b") else args.workload
+    entries, _ = build_fp8_entries(config_weights(workload), dev)
+    outs = [torch.empty(src.shape, dtype=torch.bfloat16, device=dev) for _, _, _, src in entries]
+    descs = [_descriptor(*sidecar_decode_args(f, sc)[:13], o) for (_, f, sc, _), o in zip(entries, outs)]
+    arr = (_native.MpsFp8Tensor * len(descs))(*descs)
+    stream = torch.cuda.current_stream(dev)
+    h = ctypes.c_void_p(stream.cuda_stream)
+    libs = []
+    for path in args.compare_libs:
+        L = ctypes.CDLL(os.path.abspath(path))
+        vp = ctypes.c_void_p
+        L.mps_fp8_plan_create.argtypes = [ctypes.POINTER(_native.MpsFp8Tensor), ctypes.c_int64, vp,
+                                          ctypes.POINTER(vp)]
+        L.mps_fp8_plan_decode.argtypes = [vp, vp]
+        L.mps_fp8_plan_read_status.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
+        L.mps_fp8_plan_destroy.argtypes = [vp]
+        L.mps_last_error.restype = ctypes.c_char_p
+        plan = vp()
+        if L.mps_fp8_plan_create(arr, len(descs), h, ctypes.byref(plan)) != 0:
+            raise RuntimeError(f"{path}: plan creation failed: {L.mps_last_error().decode()}")
+        for o in outs:
+            o.zero_()
+        for _ in range(max(1, args.warmup // 3)):
+            if L.mps_fp8_plan_decode(plan, h) != 0:
+                raise RuntimeError(f"{path}: {L.mps_last_error().decode()}")
+        st = ctypes.c_uint32(0)
+        L.mps_fp8_plan_read_status(plan, h, ctypes.byref(st))
+        exact = None if args.no_verify else all(
+            torch.equal(o.view(torch.uint16), src.view(torch.uint16)) for o, (_, _, _, src) in zip(outs, entries))
+        log(f"{path}: status {st.value}, bit-exact {exact}")
+        libs.append({"path": path, "L": L, "plan": plan, "status": st.value, "bit_exact": exact, "ms": []})
+    for r in range(args.compare_rounds):
+        for lib in (libs if r % 2 == 0 else libs[::-1]):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+            for a, b in ev:
+                a.record(stream)
+                lib["L"].mps_fp8_plan_decode(lib["plan"], h)
+                b.record(stream)
+            torch.cuda.synchronize()
+            lib["ms"].append(statistics.mean(a.elapsed_time(b) for a, b in ev))
+        log(f"round {r}: " + " ".join(f"{x['ms'][-1]:.4f}" for x in libs))
+    base = statistics.median(libs[0]["ms"])
+    rows = []
+    for lib in libs:
+        med = statistics.median(lib["ms"])
+        rows.append({"lib": lib["path"], "median_ms": round(med, 4), "vs_first": round(med / base - 1, 4),
+                     "rounds_ms": [round(x, 4) for x in lib["ms"]], "status": lib["status"],
+                     "bit_exact": lib["bit_exact"]})
+        lib["L"].mps_fp8_plan_destroy(lib["plan"])
+    print(json.dumps({"metric": "decode plan launch ms per library build (one process, interleaved)",
+                      "workload": WORKLOADS[workload], "device": torch.cuda.get_device_name(dev),
+                      "arch": torch.cuda.get_device_properties(dev).gcnArchName, "libs": rows}),
+          flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -724,6 +801,8 @@ def main(argv=None) -> int:
         return 2
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.compare_libs:
+        return compare_libs(args, dev)
     if args.workload == "all":
         return run_all(args, dev)
     return run_single(args, dev)

@@ -2,6 +2,12 @@
 
 ``python -m mpserve_amd.build`` or ``mpserve_amd.build.build()``. The library is
 placed next to this file so it travels with the source tree.
+
+Tuning builds: ``python -m mpserve_amd.build --define MPS_SLAB_PREFETCH=12 --out
+/tmp/lib_df12.so`` compiles the same sources with the decode kernel's
+compile-time knobs set otherwise (``MPS_SLAB_PREFETCH``, ``MPS_PRIO_LEAD``,
+``MPS_SLAB_RESERVE_BLOCKS``, ``MPS_SLAB_ALIGN``, ``MPS_LUT_SPREAD``) into another file, for
+``bench.py --compare-libs``. The product library is never built with defines.
 """
 from __future__ import annotations
 
@@ -32,18 +38,38 @@ def _hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into libmpserve_amd.so (always recompiles)."""
+def build(verbose: bool = False, defines=(), out: str | None = None) -> str:
+    """Compile every HIP source into libmpserve_amd.so (always recompiles), or,
+    with ``defines`` (``NAME=VALUE`` strings), into the tuning library ``out``."""
+    if defines and (out is None or os.path.abspath(out) == LIB):
+        raise ValueError("a build with --define needs --out: the product library keeps the default knobs")
+    target = os.path.abspath(out) if out else LIB
     srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    tmp = LIB + ".tmp"
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, *srcs, "-o", tmp]
+    tmp = target + ".tmp"
+    cmd = [_hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+           *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, target)
+    return target
+
+
+def main(argv=None) -> int:
+    import argparse
+
+    p = argparse.ArgumentParser(description="compile libmpserve_amd.so for gfx950")
+    p.add_argument("-v", "--verbose", action="store_true")
+    p.add_argument("--define", action="append", default=[], metavar="NAME=VALUE",
+                   help="compile-time knob of a tuning build (needs --out)")
+    p.add_argument("--out", default=None, help="output path of a tuning build")
+    a = p.parse_args(argv)
+    try:
+        print(build(a.verbose, a.define, a.out))
+    except ValueError as e:
+        p.error(str(e))
+    return 0
 
 
 if __name__ == "__main__":
-    build(verbose="-v" in sys.argv)
-    print(LIB)
+    sys.exit(main())
