@@ -214,6 +214,40 @@ def cpu_baseline(decode_one, items, what: str, seconds: float, threads: int) -> 
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
+def cfg1_cpu(threads: int) -> dict:
+    """Config 1, the reference's CPU-runnable case: one 4096x4096 N(0, 0.02^2) BF16
+    weight (seed 0, torch's CPU generator), per-channel FP8; the oracle's CPU encode,
+    then its CPU decode on ``threads`` threads and on one, checked bit-exact."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from mpserve_amd.synthetic import make_weight
+
+    n = m = 4096
+    w = make_weight(n, m, sigma=0.02, seed=0, device="cpu")
+    bf = w.bf16.view(torch.uint16).numpy()
+    q = w.fp8_u8.numpy()
+    t0 = time.perf_counter()
+    sc = oracle.encode(bf, q, w.scale_u16.numpy(), 7, 1024)
+    enc_ms = (time.perf_counter() - t0) * 1e3
+    dec = {}
+    exact = True
+    for t in (threads, 1):
+        out = np.empty((n, m), dtype=np.uint16)
+        t0 = time.perf_counter()
+        oracle.decode(sc, q, n, m, 7, oracle.MODE_LOSSLESS, t, out)
+        dec[t] = (time.perf_counter() - t0) * 1e3
+        exact = exact and bool(np.array_equal(out, bf))
+    side = sum(v.nbytes for k, v in sc.items() if k not in _NOT_STORED)
+    return {"workload": "cfg1: one 4096x4096 weight, seed 0, sigma 0.02; CPU encode then CPU decode (no GPU)",
+            "encode_ms": round(enc_ms, 1), "decode_ms": round(dec[threads], 1), "decode_threads": threads,
+            "decode_ms_one_thread": round(dec[1], 1), "bit_exact": exact,
+            "buckets": int(sc["bucket_table_i32"].shape[0]), "sidecar_over_bf16": round(side / (2 * n * m), 4),
+            "implementation": "the parity oracle (oracle/fp8_huffman_oracle.c), the CPU restatement of the "
+                              "reference's builder and decoder", "cpu_model": cpu_model()}
+
+
 def fp8_host_sample(entries):
     """Host copies of FP8 entries for the CPU baseline: (name, n, m, decode args)."""
     import torch
@@ -650,6 +684,8 @@ def run_all(args, dev) -> int:
             host70, "oracle decode of the 70B layer's q/k/v weights (ESC codes in q)", args.cpu_seconds, threads)
         sub["awq8b_by_scale"]["cpu_baseline"] = awq_cpu_baseline(
             awq_host, "oracle AWQ by-scale decode of the 8B layer's q/k/v/o weights", args.cpu_seconds, threads)
+        log("config 1 on the CPU: oracle encode and decode of one 4096x4096 weight")
+        sub["cfg1_cpu"] = cfg1_cpu(threads)
     res["subresults"] = sub
     print(json.dumps(res), flush=True)
     return 0
