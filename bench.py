@@ -560,8 +560,13 @@ def awq_result(dev, args, layouts=(("by_scale", 128), ("row_buckets", None))):
         for name, _, _, w, _, _, out, st in items:
             if not torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)) and st["esc_collisions"] == 0:
                 raise RuntimeError(f"AWQ plan decode ({layout}) of {name} is not bit-exact")
-        if plan.read_status() != 0:
-            raise RuntimeError(f"AWQ plan decode ({layout}) flagged the sidecars")
+        # A collided element is a bare ESC code that the decoder reads as ESC + 16 raw bits,
+        # so its lane ends past the next lane's start: that (and only that) is expected then.
+        from mpserve_amd._native import MPS_STATUS_DESYNC
+        status = plan.read_status()
+        allowed = MPS_STATUS_DESYNC if any(it[7]["esc_collisions"] for it in items) else 0
+        if status & ~allowed:
+            raise RuntimeError(f"AWQ plan decode ({layout}) flagged the sidecars (0x{status:x})")
         log(f"awq {layout} layer: {tot_ms:.4f} ms as 7 op launches, {plan_ms:.4f} ms as one plan launch "
             f"({plan.info()['work_items']} work items)")
         results[layout] = {"steps": steps, "warmup": warmup, "layer_ms_op_launches": round(tot_ms, 4),

@@ -247,62 +247,128 @@ __global__ void table_list_kernel(const uint32_t *tcount, const uint32_t *tgid, 
 // 3. Code book of one key (one work-item per key)
 // ---------------------------------------------------------------------------
 // Items (count, sym) compare as the reference's std::pair<int, uint16_t>.
-__device__ __forceinline__ bool item_less(int32_t ca, uint32_t sa, int32_t cb, uint32_t sb) {
-  return ca != cb ? ca < cb : sa < sb;
+// Items are ordered by (count, symbol) with counts compared as int, as the
+// reference's item lists are: the sort key flips the count's sign bit so that
+// an unsigned 64-bit compare orders it as a signed one.
+__device__ __forceinline__ uint64_t item_key(uint32_t count, uint32_t sym) {
+  return ((uint64_t)(count ^ 0x80000000u) << 16) | (sym & 0xFFFFu);
+}
+__device__ __forceinline__ uint32_t key_count(uint64_t k) { return (uint32_t)(k >> 16) ^ 0x80000000u; }
+
+// Sorts n (key, value) pairs by key (distinct keys) with a bottom-up merge
+// sort over runs of 16 made by insertion; tk/tv are scratch of n each. The
+// result is in k/v.
+__device__ void sort_pairs(uint64_t *k, uint32_t *v, uint64_t *tk, uint32_t *tv, uint32_t n) {
+  constexpr uint32_t kRun = 16;
+  for (uint32_t lo = 0; lo < n; lo += kRun) {
+    const uint32_t hi = lo + kRun < n ? lo + kRun : n;
+    for (uint32_t i = lo + 1; i < hi; ++i) {
+      const uint64_t x = k[i];
+      const uint32_t y = v[i];
+      uint32_t j = i;
+      for (; j > lo && k[j - 1] > x; --j) {
+        k[j] = k[j - 1];
+        v[j] = v[j - 1];
+      }
+      k[j] = x;
+      v[j] = y;
+    }
+  }
+  uint64_t *sk = k, *dk = tk;
+  uint32_t *sv = v, *dv = tv;
+  for (uint32_t width = kRun; width < n; width *= 2) {
+    for (uint32_t lo = 0; lo < n; lo += 2 * width) {
+      const uint32_t mid = lo + width < n ? lo + width : n;
+      const uint32_t hi = lo + 2 * width < n ? lo + 2 * width : n;
+      uint32_t i = lo, j = mid, o = lo;
+      while (i < mid && j < hi) {
+        const bool right = sk[j] < sk[i];
+        dk[o] = right ? sk[j] : sk[i];
+        dv[o] = right ? sv[j] : sv[i];
+        i += right ? 0u : 1u;
+        j += right ? 1u : 0u;
+        ++o;
+      }
+      for (; i < mid; ++i, ++o) {
+        dk[o] = sk[i];
+        dv[o] = sv[i];
+      }
+      for (; j < hi; ++j, ++o) {
+        dk[o] = sk[j];
+        dv[o] = sv[j];
+      }
+    }
+    uint64_t *t64 = sk;
+    sk = dk;
+    dk = t64;
+    uint32_t *t32 = sv;
+    sv = dv;
+    dv = t32;
+  }
+  if (sk != k) {
+    for (uint32_t i = 0; i < n; ++i) {
+      k[i] = sk[i];
+      v[i] = sv[i];
+    }
+  }
 }
 
-// Leaf counts per level of the package-merge (build_huffman.cu:46-118), in the
-// equivalent form: with cur_0 = leaves and cur_j = merge(leaves, pairs of
-// cur_{j-1}) (leaf first on equal weight), the reference selects the first
-// 2(n-1) items of cur_{L-1} and, recursively, the first 2p items of cur_{j-1}
-// for the p packages selected in cur_j. A leaf's length is the number of
-// levels whose selected prefix contains it; leaves keep their sorted order in
-// every cur_j, so that prefix holds leaves 0..x_j-1. cur_j is rebuilt from
-// the leaves for each level (O(L^2 n) time, O(n) memory per key).
-__device__ void package_merge_lengths(const int32_t *w, int n, int L, int32_t *A, int32_t *Bv, uint8_t *Aleaf,
-                                      uint8_t *Bleaf, int32_t *lens) {
+// Code lengths of n ascending weights by the package-merge (build_huffman.cu:46-118),
+// in the level-count form: with cur_0 = the leaves and cur_j = merge(leaves,
+// pairs of cur_{j-1}) (leaf first on equal weight, at most 4(n-1) items), the
+// reference selects the first 2(n-1) items of cur_{L-1} and, recursively, the
+// first 2p items of cur_{j-1} for the p packages selected in cur_j. Leaves keep
+// their sorted order in every cur_j, so a level's selected prefix holds leaves
+// 0..x_j-1, and a leaf's length is the number of levels with x_j above its
+// index. The levels are built once, bottom-up (O(L n)); each keeps only a bit
+// per item saying whether it is a leaf (masks: L words per 32 items of 4(n-1)),
+// and the selection then walks them top-down. A and B hold 4(n-1) ints each.
+__device__ void package_merge_lengths(const int32_t *w, int n, int L, int32_t *A, int32_t *B, uint32_t *masks,
+                                      int32_t *lens) {
   for (int i = 0; i < n; ++i) lens[i] = 0;
   if (n == 1) {
     lens[0] = 1;
     return;
   }
   const int keep = 4 * (n - 1);
+  const int words = (keep + 31) / 32;
+  int na[16];
+  int cur = n < keep ? n : keep;
+  for (int i = 0; i < cur; ++i) A[i] = w[i];
+  for (int i = 0; i < words; ++i) {
+    const int b = cur - 32 * i;
+    masks[i] = b >= 32 ? 0xFFFFFFFFu : (b > 0 ? (1u << b) - 1u : 0u);
+  }
+  na[0] = cur;
+  for (int j = 1; j < L; ++j) {
+    uint32_t *mk = masks + j * words;
+    for (int i = 0; i < words; ++i) mk[i] = 0u;
+    const int np = cur / 2;  // packages: pairs (0,1), (2,3), ... of the previous level
+    int a = 0, b = 0, o = 0;
+    while (o < keep && (a < n || b < np)) {
+      const int32_t pw = b < np ? (int32_t)((uint32_t)A[2 * b] + (uint32_t)A[2 * b + 1]) : 0;
+      if (a < n && (b >= np || w[a] <= pw)) {
+        B[o] = w[a++];
+        mk[o >> 5] |= 1u << (o & 31);
+      } else {
+        B[o] = pw;
+        ++b;
+      }
+      ++o;
+    }
+    int32_t *t = A;
+    A = B;
+    B = t;
+    cur = o;
+    na[j] = o;
+  }
   int c = 2 * (n - 1);  // selected prefix at the top level
   for (int level = L - 1; level >= 0 && c > 0; --level) {
-    // build cur_level
-    int na = n < keep ? n : keep;
-    for (int i = 0; i < na; ++i) {
-      A[i] = w[i];
-      Aleaf[i] = 1;
-    }
-    for (int r = 0; r < level; ++r) {
-      const int t = na < keep ? na : keep;
-      // packages are pairs (0,1), (2,3), ... of A, in order (sorted, since A is sorted)
-      const int np = t / 2;
-      int a = 0, b = 0, o = 0;
-      while (o < keep && (a < n || b < np)) {
-        const bool take_leaf =
-            a < n && (b >= np || w[a] <= (int32_t)((uint32_t)A[2 * b] + (uint32_t)A[2 * b + 1]));
-        if (take_leaf) {
-          Bv[o] = w[a++];
-          Bleaf[o] = 1;
-        } else {
-          Bv[o] = (int32_t)((uint32_t)A[2 * b] + (uint32_t)A[2 * b + 1]);
-          ++b;
-          Bleaf[o] = 0;
-        }
-        ++o;
-      }
-      for (int i = 0; i < o; ++i) {
-        A[i] = Bv[i];
-        Aleaf[i] = Bleaf[i];
-      }
-      na = o;
-    }
-    // leaves among the first c items of cur_level
-    const int cc = c < na ? c : na;
+    const int cc = c < na[level] ? c : na[level];
+    const uint32_t *mk = masks + level * words;
     int x = 0;
-    for (int i = 0; i < cc; ++i) x += Aleaf[i];
+    for (int i = 0; i < cc / 32; ++i) x += __popc(mk[i]);
+    if (cc & 31) x += __popc(mk[cc / 32] & ((1u << (cc & 31)) - 1u));
     for (int i = 0; i < x; ++i) lens[i] += 1;
     c = 2 * (cc - x);
   }
@@ -326,7 +392,7 @@ struct CodebookArgs {
   uint16_t *seg_sym;  // sorted in place
   uint32_t *seg_cnt;
   uint32_t *seg_slot;  // hash slot of each entry; sorted along with seg_sym/seg_cnt
-  int32_t *ws;        // 6 ints per segment entry + 2^(L+2) per key headroom
+  int32_t *ws;        // per key: kWsSort ints per histogram entry + kWsPerItem per list item (ws_size_kernel)
   const uint32_t *ws_off;
   const uint16_t *scale_values;  // sidx -> scale u16
   uint32_t *cw_slot;             // hash slot -> code word
@@ -341,6 +407,18 @@ struct CodebookArgs {
   uint32_t *esc_stats;  // [0] keys with ESC, [1] collisions (elements)
 };
 
+// Workspace per key, in ints: sort scratch over the ni histogram entries
+// (two 64-bit keys and two 32-bit values each, later the entry -> list
+// position map), then per list item (nmax = min(ni, 2^L)): weights, symbols,
+// lengths, histogram index, code, two package-merge lists of 4 items, the
+// level masks (2, plus kWsFixed for the per-level rounding) and the sorted
+// weights.
+constexpr uint32_t kWsSort = 6;
+constexpr uint32_t kWsPerItem = 16;
+constexpr uint32_t kWsFixed = 20;
+
+// One work-item per key: ESC selection, package-merge lengths, canonical codes
+// in list order, the decode table and the code word of each histogram entry.
 __global__ void codebook_kernel(CodebookArgs a) {
   const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= a.G) return;
@@ -363,58 +441,54 @@ __global__ void codebook_kernel(CodebookArgs a) {
     a.cw_slot[slot[0]] = (1u << 16) | 0u;
     return;
   }
-  // (count asc, sym asc); counts are compared as int like the reference's items
-  for (uint32_t i = 1; i < ni; ++i) {
-    const uint16_t s = sym[i];
-    const uint32_t c = cnt[i], h = slot[i];
-    int64_t j = (int64_t)i - 1;
-    while (j >= 0 && item_less((int32_t)c, s, (int32_t)cnt[j], sym[j])) {
-      sym[j + 1] = sym[j];
-      cnt[j + 1] = cnt[j];
-      slot[j + 1] = slot[j];
-      --j;
-    }
-    sym[j + 1] = s;
-    cnt[j + 1] = c;
-    slot[j + 1] = h;
-  }
-  // workspace of kWsPerItem ints per list item (see ws_size_kernel)
-  const uint32_t nmax = ni < T ? ni : T;
   int32_t *ws = a.ws + a.ws_off[g];
-  int32_t *lw = ws;                 // weights of the coded list
-  int32_t *ls = ws + nmax;          // its symbols
-  int32_t *lens = ws + 2 * nmax;
-  int32_t *A = ws + 3 * nmax;       // two merge lists of <= 4 nmax items
+  uint64_t *sk = reinterpret_cast<uint64_t *>(ws);  // 8-byte aligned: every key's size is even
+  uint64_t *tk64 = sk + ni;
+  uint32_t *sv = reinterpret_cast<uint32_t *>(tk64 + ni);
+  uint32_t *tv = sv + ni;
+  const uint32_t nmax = ni < T ? ni : T;
+  int32_t *lw = ws + kWsSort * ni;  // weights of the coded list
+  int32_t *ls = lw + nmax;          // its symbols
+  int32_t *lens = ls + nmax;
+  int32_t *hidx = lens + nmax;      // histogram entry of each list item (-1: the ESC item)
+  uint32_t *code = reinterpret_cast<uint32_t *>(hidx + nmax);
+  int32_t *A = reinterpret_cast<int32_t *>(code + nmax);
   int32_t *Bv = A + 4 * nmax;
-  uint8_t *Al = reinterpret_cast<uint8_t *>(Bv + 4 * nmax);
-  uint8_t *Bl = Al + 4 * nmax;
-  int32_t *sw = reinterpret_cast<int32_t *>(Bl + 4 * nmax);  // sorted weights (kEscAwqByScale)
+  uint32_t *masks = reinterpret_cast<uint32_t *>(Bv + 4 * nmax);  // L * ceil(4(nmax-1)/32) <= 2 nmax + 16
+  int32_t *sw = reinterpret_cast<int32_t *>(masks + 2 * nmax + 16);  // sorted weights (kEscAwqByScale)
+
+  // (count asc, sym asc)
+  for (uint32_t i = 0; i < ni; ++i) {
+    sk[i] = item_key(cnt[i], sym[i]);
+    sv[i] = slot[i];
+  }
+  sort_pairs(sk, sv, tk64, tv, ni);
+  for (uint32_t i = 0; i < ni; ++i) {
+    sym[i] = (uint16_t)(sk[i] & 0xFFFFu);
+    cnt[i] = key_count(sk[i]);
+    slot[i] = sv[i];
+  }
+
   uint32_t nl = 0;
   bool use_esc = false;
   uint32_t esc_sym = 0;
   if (ni > T) {
     // ESC (build_huffman.cu:485-535): keep the 2^L-1 most frequent by (count
-    // desc, sym asc); ESC weight = sum of the rest; esc_sym = smallest u16 not kept.
+    // desc, sym asc); ESC weight = sum of the rest. In (count asc, sym asc)
+    // order, count groups are taken from the top, each from its smallest symbol.
     use_esc = true;
     const uint32_t keep = T - 1;
-    // the list is (count asc, sym asc): the kept items are the last `keep`
-    // in (count desc, sym asc) order, i.e. ties on count break toward the
-    // smaller symbol, which is the earlier one in this order. Select them by
-    // walking count groups from the top.
-    // Mark kept items in cnt's high bit-free copy: use lens[] as scratch flags over ni is not
-    // possible (ni > T), so select in place by moving kept items to the end.
     uint32_t taken = 0;
     int64_t i = (int64_t)ni - 1;
-    // walk groups of equal count from the largest count down
     while (taken < keep && i >= 0) {
       int64_t j = i;
       while (j > 0 && cnt[j - 1] == cnt[i]) --j;
-      // group [j, i] has equal count, syms ascending; take from the smallest sym
       const uint32_t gsize = (uint32_t)(i - j + 1);
       const uint32_t take = gsize < keep - taken ? gsize : keep - taken;
       for (uint32_t t = 0; t < take; ++t) {
         lw[nl] = (int32_t)cnt[j + t];
         ls[nl] = sym[j + t];
+        hidx[nl] = (int32_t)(j + t);
         ++nl;
       }
       taken += take;
@@ -438,70 +512,70 @@ __global__ void codebook_kernel(CodebookArgs a) {
         else hi = mid - 1;
       }
       esc_sym = lo > 0xFFFFu ? 0xFFFFu : lo;
-      lw[nl] = (int32_t)esc_w;  // last; the list keeps its (count desc, sym asc) order
+      // The list keeps its (count desc, sym asc) order with ESC last; the
+      // package-merge gets the same weights ascending: the kept ones reversed,
+      // the ESC weight merged in.
+      const int32_t ew = (int32_t)esc_w;
+      uint32_t o = 0;
+      bool placed = false;
+      for (int64_t t = (int64_t)nl - 1; t >= 0; --t) {
+        if (!placed && ew <= lw[t]) {
+          sw[o++] = ew;
+          placed = true;
+        }
+        sw[o++] = lw[t];
+      }
+      if (!placed) sw[o++] = ew;
+      lw[nl] = ew;
       ls[nl] = (int32_t)esc_sym;
+      hidx[nl] = -1;
       ++nl;
       atomicAdd(&a.esc_stats[0], 1u);
-      goto lengths;
-    }
-    // smallest u16 not among the kept: sort kept syms (insertion, <= 2^15 items)
-    for (uint32_t p = 1; p < nl; ++p) {
-      const int32_t v = ls[p], vw = lw[p];
-      int64_t q = (int64_t)p - 1;
-      while (q >= 0 && ls[q] > v) {
-        ls[q + 1] = ls[q];
-        lw[q + 1] = lw[q];
-        --q;
+    } else {
+      // smallest u16 not among the kept: their symbols sorted
+      for (uint32_t t = 0; t < nl; ++t) {
+        sk[t] = (uint64_t)(uint32_t)ls[t];
+        sv[t] = 0u;
       }
-      ls[q + 1] = v;
-      lw[q + 1] = vw;
-    }
-    uint32_t cand = 0;
-    for (uint32_t p = 0; p < nl; ++p) {
-      if ((uint32_t)ls[p] == cand) ++cand;
-      else if ((uint32_t)ls[p] > cand) break;
-    }
-    esc_sym = cand & 0xFFFF;
-    lw[nl] = (a.esc_mode == kEscAwqBucket && (int32_t)esc_w <= 0) ? 1 : (int32_t)esc_w;
-    ls[nl] = (int32_t)esc_sym;
-    ++nl;
-    // back to (count asc, sym asc)
-    for (uint32_t p = 1; p < nl; ++p) {
-      const int32_t v = ls[p], vw = lw[p];
-      int64_t q = (int64_t)p - 1;
-      while (q >= 0 && item_less(vw, (uint32_t)v, lw[q], (uint32_t)ls[q])) {
-        ls[q + 1] = ls[q];
-        lw[q + 1] = lw[q];
-        --q;
+      sort_pairs(sk, sv, tk64, tv, nl);
+      uint32_t cand = 0;
+      for (uint32_t p = 0; p < nl; ++p) {
+        if ((uint32_t)sk[p] == cand) ++cand;
+        else if ((uint32_t)sk[p] > cand) break;
       }
-      ls[q + 1] = v;
-      lw[q + 1] = vw;
+      esc_sym = cand & 0xFFFF;
+      lw[nl] = (a.esc_mode == kEscAwqBucket && (int32_t)esc_w <= 0) ? 1 : (int32_t)esc_w;
+      ls[nl] = (int32_t)esc_sym;
+      hidx[nl] = -1;
+      ++nl;
+      // the list in (count asc, sym asc) order, with each item's histogram entry
+      for (uint32_t t = 0; t < nl; ++t) {
+        sk[t] = item_key((uint32_t)lw[t], (uint32_t)ls[t]);
+        sv[t] = (uint32_t)hidx[t];
+      }
+      sort_pairs(sk, sv, tk64, tv, nl);
+      for (uint32_t t = 0; t < nl; ++t) {
+        lw[t] = (int32_t)key_count(sk[t]);
+        ls[t] = (int32_t)(sk[t] & 0xFFFFu);
+        hidx[t] = (int32_t)sv[t];
+      }
+      atomicAdd(&a.esc_stats[0], 1u);
     }
-    atomicAdd(&a.esc_stats[0], 1u);
   } else {
     for (uint32_t t = 0; t < ni; ++t) {
       lw[t] = (int32_t)cnt[t];
       ls[t] = sym[t];
+      hidx[t] = (int32_t)t;
     }
     nl = ni;
   }
-lengths:
   if (a.esc_mode == kEscAwqByScale && use_esc) {
     // package-merge sorts the weights and returns lengths by sorted position;
     // the reference applies them to its (unsorted) list position by position
-    for (uint32_t t = 0; t < nl; ++t) {
-      const int32_t v = lw[t];
-      int64_t q = (int64_t)t - 1;
-      while (q >= 0 && sw[q] > v) {
-        sw[q + 1] = sw[q];
-        --q;
-      }
-      sw[q + 1] = v;
-    }
-    package_merge_lengths(sw, (int)nl, L, A, Bv, Al, Bl, lens);
+    package_merge_lengths(sw, (int)nl, L, A, Bv, masks, lens);
   } else {
     // weights are ascending (as int); package-merge expects that order
-    package_merge_lengths(lw, (int)nl, L, A, Bv, Al, Bl, lens);
+    package_merge_lengths(lw, (int)nl, L, A, Bv, masks, lens);
   }
   // canonical codes (build_huffman.cu:171-203), handed out in list order
   uint32_t bl_count[16], next_code[16];
@@ -514,11 +588,11 @@ lengths:
     if (use_esc && a.esc_mode != kEscFp8 && (uint32_t)ls[t] == esc_sym) lens[t] = L;  // AWQ: ESC code has length L
     bl_count[lens[t]]++;
   }
-  uint32_t code = 0;
+  uint32_t cd = 0;
   next_code[0] = 0;
   for (int b = 1; b < 16; ++b) {
-    code = (code + bl_count[b - 1]) << 1;
-    next_code[b] = code;
+    cd = (cd + bl_count[b - 1]) << 1;
+    next_code[b] = cd;
   }
   for (uint32_t j = 0; j < T; ++j) dsyms[j] = 0;
   for (uint32_t j = 0; j < T / 2; ++j) dlens[j] = 0;
@@ -526,6 +600,7 @@ lengths:
   for (uint32_t t = 0; t < nl; ++t) {
     const int len = lens[t];
     const uint32_t c = next_code[len]++;
+    code[t] = c;
     const uint32_t fill = 1u << (L - len);
     const uint32_t base = c << (L - len);
     const bool is_esc = use_esc && (uint32_t)ls[t] == esc_sym;
@@ -535,51 +610,37 @@ lengths:
       dsyms[e] = (uint16_t)ls[t];
       if (T >= 2) dlens[e >> 1] |= (uint8_t)((nib & 0xF) << ((e & 1) * 4));
     }
-    const uint32_t cw = ((uint32_t)len << 16) | (c & 0xFFFF);
-    if (is_esc) esc_cw = cw;
+    if (is_esc) esc_cw = ((uint32_t)len << 16) | (c & 0xFFFF);
   }
-  // code word of every histogram entry of this key
+  // code word of every histogram entry: its list item's code; an entry outside
+  // the list is coded as ESC + 16 raw bits, except one whose symbol is esc_sym
+  // (the ESC code alone: a collision, as in the reference)
+  int32_t *pos_of = ws;  // the sort scratch is free again
+  for (uint32_t t = 0; t < ni; ++t) pos_of[t] = -1;
+  for (uint32_t p = 0; p < nl; ++p)
+    if (hidx[p] >= 0) pos_of[hidx[p]] = (int32_t)p;
   for (uint32_t t = 0; t < ni; ++t) {
-    const uint32_t s = sym[t];
-    // find s in the coded list (ls is sorted by (count, sym): linear scan)
-    uint32_t cw = 0;
-    bool found = false;
-    for (uint32_t p = 0; p < nl; ++p) {
-      if ((uint32_t)ls[p] == s) {
-        // recompute this item's code: codes were handed out in list order, so
-        // walk again per length (cheap: nl <= 2^L)
-        found = true;
-        uint32_t nc[16];
-        uint32_t cd = 0;
-        nc[0] = 0;
-        for (int b = 1; b < 16; ++b) {
-          cd = (cd + bl_count[b - 1]) << 1;
-          nc[b] = cd;
-        }
-        for (uint32_t r = 0; r <= p; ++r) {
-          const uint32_t cr = nc[lens[r]]++;
-          if (r == p) cw = ((uint32_t)lens[r] << 16) | (cr & 0xFFFF);
-        }
-        break;
-      }
-    }
-    if (!found) {
+    const int32_t p = pos_of[t];
+    uint32_t cw;
+    if (p >= 0) {
+      cw = ((uint32_t)lens[p] << 16) | (code[p] & 0xFFFF);
+    } else if (use_esc && sym[t] == esc_sym) {
+      cw = esc_cw;
+      atomicAdd(&a.esc_stats[1], cnt[t]);
+    } else {
       cw = esc_cw | kRaw;  // outside the map: ESC code + raw16
-    } else if (use_esc && s == esc_sym) {
-      atomicAdd(&a.esc_stats[1], cnt[t]);  // data symbol equal to esc_sym: ESC code, no raw bits
     }
     a.cw_slot[slot[t]] = cw;
   }
 }
-
-constexpr uint32_t kWsPerItem = 14;  // 3 list arrays + 2 x 4 merge ints + 2 x 4 merge bytes + sorted weights
 
 __global__ void ws_size_kernel(const uint32_t *gid_tkey, const uint32_t *tcount, uint32_t G, uint32_t T,
                                uint32_t *sz) {
   const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   const uint32_t ni = tcount[gid_tkey[g]];
-  sz[g] = kWsPerItem * (ni < T ? ni : T) + 4;
+  const uint32_t n = kWsSort * ni + kWsPerItem * (ni < T ? ni : T) + kWsFixed;
+  sz[g] = (n + 1u) & ~1u;  // even, so that every key's 64-bit sort keys are 8-byte aligned
 }
 
 // ---------------------------------------------------------------------------
