@@ -27,11 +27,13 @@
 // 512-work-item workgroups per bucket, each with its own copy of the tables.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <cstring>
 
 #include <algorithm>
 #include <cstdint>
 #include <new>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -314,8 +316,390 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
   awq_bucket<kSplit>(T, blockIdx.x / kSplit, (int)(blockIdx.x % kSplit), lut, s_base, status);
 }
 
+// ---------------------------------------------------------------------------
+// Slab path: by-scale buckets with k = 1024 substreams and groups of 128
+// columns (8 to 1024 groups). Element e of such a bucket is column e % 128 of
+// its group e / 128, and substream t codes e = t, t + 1024, ...: the i-th
+// element of every substream lies in *slab* i, the bucket's groups 8i .. 8i+7.
+// Lane l = 16R + v of wave w decodes substream t = 64w + 4v + R, four elements
+// (slabs 4g .. 4g+3) per step, in the register layout of the FP8 slab decode:
+//  - lane (R, v) loads one dword of int4 bytes, columns 64(w & 1) + 4v .. +3 of
+//    slab 4g+R's group 8(4g+R) + w/2, so each 16-lane row reads 64 contiguous
+//    bytes; a 4x4 byte transpose across lanes (0,v) .. (3,v) gives every lane
+//    its own four bytes;
+//  - the inverse transpose of the BF16 symbols gives lane (R, v) those columns'
+//    values for one 8-byte store (a 128-byte segment per 16-lane row);
+//  - the wave's group bases (row * m + column start + 64(w & 1)) for slabs
+//    l and l + 64 sit in lane l of two VGPRs and are fetched with ds_bpermute;
+//  - the bit supply is the FP8 slab path's: an 8-chunk LDS queue per lane fed
+//    from a register reserve that requests aligned 64-byte blocks.
+// Codes are up to 11 bits, so a step cuts two 32-bit windows, two codes each.
+// An ESC entry's low bits are 27 (its 11-bit code and the 16 raw bits), so bit
+// 4 flags it and the running shift steps over the raw bits; a step holding an
+// ESC code is decoded again code by code, reading the raw symbol.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kAwqEscBit = 1u << 4;
+constexpr uint32_t kAwqEscLow = 27u;          // 11 + 16: an ESC entry's low bits
+constexpr int kSlabQSlots = 8;                // LDS queue chunks per lane
+constexpr uint32_t kSlabBsPast = 0x80000000u; // bitstream offset beyond every bucket's range
+constexpr uint32_t kSlabOutPast = 0xFFFFFFF0u;  // BF16 byte offset beyond every output (2*n*m < 2^32)
+constexpr uint32_t kSlabInPast = 0x80000000u;   // int4 byte offset beyond every input (n*m < 2^31)
+constexpr int kSlabCacheNT = 2;               // buffer cache-policy bits: non-temporal
+constexpr int kSlabMinGroups = 8, kSlabMaxGroups = 1024;
+static_assert(kSlabQSlots * kAwqBlock <= kRowSlots, "the slab queue lives in the row-offset region");
+
+// Buffer resource over [base, base + bytes): raw buffer loads past the end
+// return 0 and stores past the end are dropped (gfx9 V# with stride 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t awq_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t awq_uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+
+template <bool kEsc>
+__device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const uint32_t *__restrict__ lut,
+                                                uint32_t *__restrict__ queue, uint32_t lane, uint32_t count,
+                                                uint32_t base_lo, uint32_t base_hi, uint64_t bucket_bit,
+                                                const uint2 (&first)[4], uint32_t pos, uint32_t pos_end,
+                                                uint32_t *status) {
+  constexpr int DF = 8;  // int4 prefetch distance (steps)
+  constexpr int RB = 4;  // 16-byte blocks per bitstream request
+  count = awq_uni(count);
+  bucket_bit = ((uint64_t)awq_uni((uint32_t)(bucket_bit >> 32)) << 32) | awq_uni((uint32_t)bucket_bit);
+  const uint32_t nfull = count >> 2;
+  const uint32_t tail = count & 3u;  // elements of the last, partial step
+  const uint32_t gall = nfull + (tail ? 1u : 0u);
+  const uint32_t nm = (uint32_t)(T.n * T.m);
+  const __amdgpu_buffer_rsrc_t r_q = awq_rsrc(T.int4, nm);
+  const __amdgpu_buffer_rsrc_t r_out = awq_rsrc(T.out, 2u * nm);
+  const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
+  const uint64_t base_byte = bucket_bit >> 3;
+  const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+  const __amdgpu_buffer_rsrc_t r_bs =
+      awq_rsrc(reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+
+  const uint32_t lane4 = lane << 2;
+  const uint32_t R = (lane >> 4) & 3u;
+  const uint32_t v4 = (lane & 15u) << 2;
+  const char *qbytes = reinterpret_cast<const char *>(queue);
+  const char *lbytes = reinterpret_cast<const char *>(lut);
+  // byte selectors of the int4-byte transpose (v_perm: 0-3 pick the second operand's bytes, 4-7 the first's)
+  const uint32_t selA = (R & 2u) ? 0x07060302u : 0x05040100u;
+  const uint32_t selB = (R & 1u) ? 0x07030501u : 0x06020400u;
+
+  // --- bitstream queue: chunk h (32 stream bits) of this lane in slot (~h) & 7 ---
+  auto chunk_mem = [&](uint32_t h) -> uint32_t {  // biased chunk h from memory (h < 2: zeros)
+    return __builtin_amdgcn_raw_buffer_load_b32(r_bs, ((h - 2u) ^ 1u) << 2, 0, 0);
+  };
+  auto put_pair = [&](uint32_t h, uint32_t hi, uint32_t lo) {  // chunks h (even) and h + 1
+    uint32_t *slot = queue + (((~h << 10) & 0x1800u) | lane);
+    slot[0] = lo;
+    slot[1024] = hi;
+  };
+  const uint32_t phase =
+      ((uint32_t)reinterpret_cast<uintptr_t>(T.bitstream) + (uint32_t)(bucket_bit >> 3)) & (16u * RB - 1u);
+  const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
+  const uint32_t nfirst = ((phase + 4u * (rq0 - 2u)) & 15u) ? 6u : 8u;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
+  if (nfirst == 8u) put_pair(rq0 + 6u, first[3].y, first[3].x);
+  uint32_t wqb = (rq0 + nfirst) << 5;  // 32 x (first chunk not yet written)
+  uint32_t rqb = wqb;                  // 32 x (first chunk not yet requested)
+  uint32_t np = 0u - (pos + 64u);      // negated biased position
+
+  auto window = [&](uint32_t npv) -> uint32_t {  // 32 stream bits at -npv
+    const uint32_t t7 = npv << 7;
+    const uint32_t c0 = *reinterpret_cast<const uint32_t *>(qbytes + ((t7 & 0x7000u) | lane4));
+    const uint32_t c1 = *reinterpret_cast<const uint32_t *>(qbytes + (((t7 - 4096u) & 0x7000u) | lane4));
+    uint32_t w = __builtin_amdgcn_alignbit(c0, c1, npv);
+    const bool dry = (int32_t)(wqb + npv) <= 31;
+    if (__builtin_amdgcn_ballot_w64(dry)) {
+      if (dry) {
+        const uint32_t h = (~npv) >> 5;
+        w = __builtin_amdgcn_alignbit(chunk_mem(h), chunk_mem(h + 1u), npv);
+        __asm__ volatile("" ::"v"(w));  // wait for the loads here, not at a later join
+      }
+    }
+    return w;
+  };
+  // Register reserve of up to RB 16-byte blocks after the queue's last chunk,
+  // refilled by aligned 64-byte requests that land in inb.
+  uint4 rv[RB], inb[RB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t rcnt = 0, ninb = 0;
+  bool ifl = false;
+  auto feed = [&]() {
+    const bool f = rcnt != 0u && (int32_t)(wqb + np) < 128;
+    if (f) {
+      const uint32_t h = wqb >> 5;
+      put_pair(h, rv[0].y, rv[0].x);
+      put_pair(h + 2u, rv[0].w, rv[0].z);
+#pragma unroll
+      for (int i = 0; i + 1 < RB; ++i) rv[i] = rv[i + 1];
+    }
+    wqb += f ? 128u : 0u;
+    rcnt -= f ? 1u : 0u;
+  };
+  auto reserve = [&]() {
+    const bool land = ifl && rcnt == 0u;
+    if (land) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) rv[i] = inb[i];
+    }
+    rcnt = land ? ninb : rcnt;
+    ifl = ifl && !land;
+    const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
+    const uint32_t off = (rqb >> 3) - 8u;
+    const uint32_t nreq = (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4;
+    if (req) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+            r_bs, (uint32_t)i < nreq ? off + 16u * (uint32_t)i : kSlabBsPast, 0, 0);
+        inb[i] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+      ninb = nreq;
+    }
+    ifl = ifl || req;
+    rqb += req ? nreq << 7 : 0u;
+  };
+  // every second step: a 16-byte feed covers the 2 x 44 bits two steps can take
+  auto bitstream_step = [&]() {
+    reserve();
+    feed();
+  };
+
+  // --- walker: the int4 load of step g; returns its BF16 store byte offset ---
+  uint32_t w_g = 0;
+  auto load_step = [&](uint32_t &F) -> uint32_t {
+    const uint32_t sl = 4u * w_g + R;  // this lane's slab
+    const bool hi = w_g >= 16u;        // slabs 4g .. 4g+3 are all below 64 or all above
+    const uint32_t src = hi ? base_hi : base_lo;
+    const uint32_t base = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((sl & 63u) << 2), (int)src);
+    const bool ok = sl < count;
+    const uint32_t off = base + v4;
+    F = __builtin_amdgcn_raw_buffer_load_b32(r_q, ok ? off : kSlabInPast, 0, 0);
+    w_g = awq_uni(w_g + (w_g + 1u < gall ? 1u : 0u));
+    return ok ? off << 1 : kSlabOutPast;
+  };
+
+  auto lookup = [&](uint32_t qb, uint32_t x) -> uint32_t {  // entry of int4 value qb at peek bits x[12:2]
+    return *reinterpret_cast<const uint32_t *>(lbytes + ((qb & 15u) << 13 | (x & 0x1FFCu)));
+  };
+  auto step = [&](auto is_tail, uint32_t F, uint32_t so) {
+    constexpr bool kTail = decltype(is_tail)::value;
+    const auto p1 = __builtin_amdgcn_permlane32_swap(F, F, false, false);
+    const uint32_t gq = __builtin_amdgcn_perm(p1[1], p1[0], selA);
+    const auto p2 = __builtin_amdgcn_permlane16_swap(gq, gq, false, false);
+    const uint32_t fq = __builtin_amdgcn_perm(p2[1], p2[0], selB);  // byte j = element j's int4 byte
+    const uint32_t np0 = np;
+    uint32_t e[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t win = window(np);
+      uint32_t s = 19u;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * h + jj;
+        if (!kTail || (uint32_t)j < tail) {
+          e[j] = lookup(fq >> (8 * j), __builtin_amdgcn_alignbit(win, win, s));
+          s -= e[j];
+        } else {
+          e[j] = 0u;
+        }
+      }
+      np += (uint32_t)((int32_t)(s << 16) >> 16) - 19u;  // minus the bits consumed
+    }
+    if constexpr (kEsc) {
+      const bool esc = ((e[0] | e[1] | e[2] | e[3]) & kAwqEscBit) != 0u;
+      if (__builtin_amdgcn_ballot_w64(esc)) {
+        if (esc) {
+          uint32_t p = np0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (!kTail || (uint32_t)j < tail) {
+              const uint32_t w = window(p);
+              uint32_t ent = lookup(fq >> (8 * j), w >> 19);
+              p -= ent & 15u;
+              if (ent & kAwqEscBit) {
+                ent = window(p) & 0xFFFF0000u;  // the symbol: the 16 raw bits after the code
+                p -= 16u;
+              }
+              e[j] = ent;
+            }
+          }
+          np = p;
+        }
+      }
+    }
+    const auto t0 = __builtin_amdgcn_permlane32_swap(e[0], e[2], false, false);
+    const auto t1 = __builtin_amdgcn_permlane32_swap(e[1], e[3], false, false);
+    const uint32_t a = __builtin_amdgcn_perm(t0[1], t0[0], 0x07060302u);
+    const uint32_t b = __builtin_amdgcn_perm(t1[1], t1[0], 0x07060302u);
+    const auto t2 = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+    const v2u o = {__builtin_amdgcn_perm(t2[1], t2[0], 0x05040100u), __builtin_amdgcn_perm(t2[1], t2[0], 0x07060302u)};
+    __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, kSlabCacheNT);
+  };
+
+  uint32_t Fr[DF], SOr[DF];
+#pragma unroll
+  for (int u = 0; u < DF; ++u) SOr[u] = load_step(Fr[u]);
+  uint32_t g = 0;
+  for (; g + (uint32_t)DF <= nfull; g += (uint32_t)DF) {
+#pragma unroll
+    for (int u = 0; u < DF; ++u) {
+      if (u % 2 == 0) bitstream_step();
+      const uint32_t F = Fr[u], so = SOr[u];
+      SOr[u] = load_step(Fr[u]);  // the step DF ahead
+      step(std::false_type{}, F, so);
+    }
+  }
+  // the last (fewer than DF) full steps and the partial one; their bytes are already loaded
+#pragma unroll
+  for (int u = 0; u < DF; ++u) {
+    if (g + (uint32_t)u < gall) {
+      if (u % 2 == 0) bitstream_step();
+      if (g + (uint32_t)u < nfull) step(std::false_type{}, Fr[u], SOr[u]);
+      else step(std::true_type{}, Fr[u], SOr[u]);
+    }
+  }
+  if (0u - np - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
+}
+
+// One slab-path bucket (checked by the plan: by-scale, k = 1024, 128-column
+// groups, 8 .. 1024 groups). Set-up in two levels of loads, each issued in full
+// before any result is used: (1) the table ids, the wave's group rows and
+// column starts, the lane's start and end bits; (2) the tables' slices and the
+// lane's first bitstream words. Thread tid expands entries 32c .. 32c+31 of the
+// table of int4 value tid / 64 (c = tid % 64).
+__device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t b, uint32_t *__restrict__ lut,
+                                                uint32_t *__restrict__ region, uint32_t *status) {
+  int tid;
+  __asm__ volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+  const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
+  const int32_t groups = rb - ra;
+  if (groups < kSlabMinGroups || groups > kSlabMaxGroups || ra < 0 || (int64_t)rb > T.num_row_indices ||
+      T.k != kAwqBlock || T.group_size != 128) {
+    if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
+    return;
+  }
+  const uint32_t w = (uint32_t)tid >> 6, wl = (uint32_t)tid & 63u;
+  const uint32_t t = (w << 6) | (((uint32_t)tid & 15u) << 2) | (((uint32_t)tid >> 4) & 3u);  // substream
+  const int q = tid >> 6, c = tid & 63;
+  // level 1
+  const __amdgpu_buffer_rsrc_t r_tab = awq_rsrc(T.bucket_table + b * 16, 64u);
+  const int32_t gq = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_tab, (uint32_t)q * 4u, 0, 0);
+  const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra, (uint32_t)groups * 4u);
+  const __amdgpu_buffer_rsrc_t r_gcol = awq_rsrc(T.group_col_start + ra, (uint32_t)groups * 4u);
+  const uint32_t gi0 = 8u * wl + (w >> 1), gi1 = 8u * (wl + 64u) + (w >> 1);
+  const int32_t row0 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi0 * 4u, 0, 0);
+  const int32_t col0 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi0 * 4u, 0, 0);
+  const int32_t row1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi1 * 4u, 0, 0);
+  const int32_t col1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi1 * 4u, 0, 0);
+  const __amdgpu_buffer_rsrc_t r_sb = awq_rsrc(T.bucket_thread_startbit + b * (kAwqBlock + 1), (kAwqBlock + 1) * 4u);
+  const uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(r_sb, t * 4u, 0, 0);
+  const uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_sb, (t + 1u) * 4u, 0, 0);
+  const uint64_t bucket_bit = (uint64_t)T.bucket_bit_base[b];
+  // level 2
+  const bool tab_ok = gq >= 0 && gq < T.num_tables;
+  const uint32_t G = (uint32_t)(T.num_tables > 0 ? T.num_tables : 0);
+  const __amdgpu_buffer_rsrc_t r_syms = awq_rsrc(T.decode_syms, G * (uint32_t)(kAwqTable * 2));
+  const __amdgpu_buffer_rsrc_t r_lens = awq_rsrc(T.decode_lens, G * (uint32_t)kAwqPacked);
+  uint4 sv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(
+        r_syms, tab_ok ? (uint32_t)gq * (uint32_t)(kAwqTable * 2) + (uint32_t)c * 64u + 16u * (uint32_t)i : kSlabBsPast,
+        0, 0);
+    sv[i] = make_uint4(x[0], x[1], x[2], x[3]);
+  }
+  const auto ln = __builtin_amdgcn_raw_buffer_load_b128(
+      r_lens, tab_ok ? (uint32_t)gq * (uint32_t)kAwqPacked + (uint32_t)c * 16u : kSlabBsPast, 0, 0);
+  uint2 first[4];
+  {
+    const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
+    const uint64_t base_byte = bucket_bit >> 3;
+    const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+    const __amdgpu_buffer_rsrc_t r_bs = awq_rsrc(
+        reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+    const uint32_t off0 = ((pos >> 5) & ~1u) * 4u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off0 + 16u * (uint32_t)i, 0, 0);
+      first[2 * i] = make_uint2(x[0], x[1]);
+      first[2 * i + 1] = make_uint2(x[2], x[3]);
+    }
+  }
+  if (tid == 0) {
+    bool bad = false;
+#pragma unroll
+    for (int qq = 0; qq < 16; ++qq) {
+      const int32_t id = T.bucket_table[b * 16 + qq];
+      bad |= id < -1 || id >= T.num_tables;
+    }
+    if (bad) flag(status, MPS_STATUS_BAD_TABLE);
+  }
+  // expansion: entry p of value q = sym << 16 | (nibble 15 ? 27 : nibble); a
+  // missing table is all ESC entries, as the reference decodes it
+  uint32_t esc_seen = tab_ok ? 0u : 1u;
+  {
+    const uint32_t nib32[4] = {ln[0], ln[1], ln[2], ln[3]};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t s8[8] = {sv[i].x & 0xFFFFu, sv[i].x >> 16, sv[i].y & 0xFFFFu, sv[i].y >> 16,
+                              sv[i].z & 0xFFFFu, sv[i].z >> 16, sv[i].w & 0xFFFFu, sv[i].w >> 16};
+      uint32_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t nib = (nib32[i] >> (4 * j)) & 15u;  // entry 8i + j: byte (8i + j) / 2, low nibble first
+        esc_seen |= nib == 15u ? 1u : 0u;
+        e[j] = tab_ok ? ((s8[j] << 16) | (nib == 15u ? kAwqEscLow : nib)) : kAwqEscLow;
+      }
+      uint4 *dst = reinterpret_cast<uint4 *>(lut + (q << kAwqL) + 32 * c + 8 * i);
+      dst[0] = make_uint4(e[0], e[1], e[2], e[3]);
+      dst[1] = make_uint4(e[4], e[5], e[6], e[7]);
+    }
+  }
+  // group bases of this wave for slabs wl and wl + 64
+  const uint32_t m = (uint32_t)T.m;
+  auto gbase = [&](uint32_t gi, int32_t row, int32_t col, bool &bad) -> uint32_t {
+    if (gi >= (uint32_t)groups) return 0u;
+    bad |= row < 0 || (int64_t)row >= T.n || col < 0 || (int64_t)col + 128 > T.m;
+    return (uint32_t)row * m + (uint32_t)col + ((w & 1u) << 6);
+  };
+  bool bad_row = false;
+  const uint32_t base_lo = gbase(gi0, row0, col0, bad_row);
+  const uint32_t base_hi = gbase(gi1, row1, col1, bad_row);
+  uint32_t *s_wflag = region + 5 * kAwqBlock;  // queue slot 5 until the decode starts
+  {
+    const uint32_t wf = (__builtin_amdgcn_ballot_w64(bad_row) ? 1u : 0u) |
+                        (__builtin_amdgcn_ballot_w64(esc_seen != 0u) ? 2u : 0u);
+    if (wl == 0) s_wflag[w] = wf;
+  }
+  __syncthreads();
+  uint32_t bflags = 0;
+#pragma unroll
+  for (int i = 0; i < kAwqBlock / 64; ++i) bflags |= s_wflag[i];
+  __syncthreads();  // the flag words belong to the queue from here on
+  if (bflags & 1u) {
+    if (tid == 0) flag(status, MPS_STATUS_BAD_ROW);
+    return;
+  }
+  // this wave's elements per lane: every full slab, and the partial last one
+  // when its group w/2 exists
+  const uint32_t count = (uint32_t)groups / 8u + ((w >> 1) < ((uint32_t)groups & 7u) ? 1u : 0u);
+  if (bflags & 2u)
+    awq_slab_decode<true>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, bucket_bit, first, pos, pos_end,
+                          status);
+  else
+    awq_slab_decode<false>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, bucket_bit, first, pos, pos_end,
+                           status);
+}
+
 // Plan launch: workgroup i decodes buckets work[i].y .. work[i].y + work[i].z - 1
-// of tensor work[i].x. A record's buckets have identical table ids (one scale),
+// of tensor work[i].x; work[i].w = 1 marks one slab-path bucket (above). A
+// record's buckets have identical table ids (one scale),
 // so they share the tables in LDS; each gets kAwqBlock / nsub work-items (its k
 // lanes) and a kRowSlots / nsub slice of the row offsets. With k = 256 four
 // buckets run in one workgroup instead of one (the tables allow one
@@ -326,6 +710,10 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tenso
   __shared__ uint32_t s_base[kRowSlots];
   const int4 w = work[blockIdx.x];
   const mps_awq_tensor T = tensors[w.x];
+  if (w.w == 1) {
+    awq_slab_bucket(T, w.y, lut, s_base, status);
+    return;
+  }
   const int nsub = w.z;
   const int per = kAwqBlock / nsub;
   const int slots = kRowSlots / nsub;
@@ -478,7 +866,9 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   // they can share a workgroup's tables; ordered by elements, largest first,
   // so the launch's last workgroups are its smallest.
   std::vector<std::pair<int64_t, int4>> items;
-  std::vector<int32_t> roff, clen, btab;
+  std::vector<int32_t> roff, clen, btab, gcol;
+  const char *slab_env = std::getenv("MPSERVE_AWQ_SLAB");
+  const bool slab_on = !(slab_env && slab_env[0] == '0');
   for (int64_t i = 0; i < count; ++i) {
     const mps_awq_tensor &T = tensors[i];
     int rc = check_awq(&T);
@@ -493,6 +883,16 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
       clen.resize((size_t)B);
       MPS_HIP_CHECK(hipMemcpy(clen.data(), T.bucket_col_len, sizeof(int32_t) * B, hipMemcpyDefault));
     }
+    // The slab path (by-scale, k = 1024, 128-column groups) loads int4 bytes as
+    // dwords and stores 8 bytes a lane: every group must start on a 4-element
+    // boundary and the buffers must be aligned to match.
+    bool slab_tensor = slab_on && T.group_col_start && T.k == kAwqBlock && T.group_size == 128 && T.m % 4 == 0 &&
+                       (reinterpret_cast<uintptr_t>(T.int4) & 3u) == 0 && (reinterpret_cast<uintptr_t>(T.out) & 7u) == 0;
+    if (slab_tensor && T.num_row_indices > 0) {
+      gcol.resize((size_t)T.num_row_indices);
+      MPS_HIP_CHECK(hipMemcpy(gcol.data(), T.group_col_start, sizeof(int32_t) * T.num_row_indices, hipMemcpyDefault));
+      slab_tensor = std::all_of(gcol.begin(), gcol.end(), [](int32_t c) { return (c & 3) == 0; });
+    }
     auto rows_of = [&](int64_t b) { return std::max<int64_t>(0, (int64_t)roff[(size_t)b + 1] - roff[(size_t)b]); };
     auto elems_of = [&](int64_t b) {
       const int64_t cols = T.group_col_start ? T.group_size : (int64_t)clen[(size_t)b];
@@ -502,6 +902,12 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     const int64_t row_cap = kRowSlots / 4;
     int64_t b = 0;
     while (b < B) {
+      if (slab_tensor && rows_of(b) >= kSlabMinGroups && rows_of(b) <= kSlabMaxGroups &&
+          roff[(size_t)b] >= 0 && roff[(size_t)b + 1] <= T.num_row_indices) {
+        items.push_back({elems_of(b), make_int4((int)i, (int)b, 1, 1)});
+        ++b;
+        continue;
+      }
       int64_t nsub = 1, elems = elems_of(b);
       if (rows_of(b) <= row_cap) {
         while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap &&

@@ -283,3 +283,46 @@ def test_truncated_bitstream_and_wild_start_bits_flag_desync_without_faults():
         torch.cuda.synchronize()
         assert out.shape == (64, 512)
         assert read_status(torch.device(DEV)) & MPS_STATUS_DESYNC, what
+
+
+def _slab_buckets(sc):
+    """Group counts of the buckets the plan sends down the slab path (8..1024 groups)."""
+    off = sc["bucket_group_offsets_i32"].cpu().numpy().astype(np.int64)
+    g = np.diff(off)
+    return g[(g >= 8) & (g <= 1024)]
+
+
+@pytest.mark.parametrize("n,m,cap,seed", [(4096, 4096, 1024, 700), (1024, 4096, 1024, 701), (2048, 4096, 12, 702),
+                                          (14336, 4096, 1024, 703)],
+                         ids=["q_4096", "kv_1024x4096", "cap12_partial_slabs", "gate_14336x4096"])
+def test_plan_slab_path_matches_input_and_the_lane_path(n, m, cap, seed, monkeypatch):
+    """By-scale sidecars with k = 1024 and 128-column groups decode on the slab path
+    (dword int4 loads, register transposes, 8-byte stores): bit-exact to the input,
+    equal to the per-lane path's output, status clean. The cases hold ESC keys,
+    buckets whose group count is not a multiple of 8 (a partial last slab) and
+    waves whose step count is not a multiple of 4 (a partial last step)."""
+    print(f"[awq] slab path {n}x{m} cap {cap}", flush=True)
+    w = make_awq_weight(n, m, 128, seed=seed, device=DEV)
+    sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, 1024, cap, True, with_stats=True)
+    groups = _slab_buckets(sc)
+    assert groups.size > 0
+    assert (groups % 8 != 0).any()
+    counts = np.concatenate([groups // 8 + (np.arange(8)[None, :] < (groups % 8)[:, None])[:, j] for j in range(8)])
+    assert (counts % 4 != 0).any()
+    if n * m >= 4096 * 4096:
+        assert st["esc_keys"] > 0
+    outs = {}
+    for slab in ("1", "0"):
+        monkeypatch.setenv("MPSERVE_AWQ_SLAB", slab)
+        out = torch.empty((n, m), dtype=torch.bfloat16, device=DEV)
+        plan = awq.AwqDecodePlan([(w.int4_u8, sc, out)])
+        plan.read_status()
+        for _ in range(2):
+            out.zero_()
+            plan.decode()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)), slab
+        assert plan.read_status() == 0
+        plan.close()
+        outs[slab] = out
+    assert torch.equal(outs["1"].view(torch.uint16), outs["0"].view(torch.uint16))
