@@ -85,7 +85,8 @@ def parse_args(argv=None):
     p.add_argument("--no-per-tensor", action="store_true",
                    help="layer workloads: skip the per-tensor timings (profiling runs that count one launch kind)")
     p.add_argument("--compare-libs", nargs="+", default=None, metavar="LIB",
-                   help="instead of the benchmark: time the decode plan of --workload (default model8b) with each "
+                   help="instead of the benchmark: time the decode plan of --workload (model8b by default; awq8b: the "
+                        "AWQ by-scale layer) with each "
                         "of these libmpserve_amd builds (python -m mpserve_amd.build --define ... --out LIB) in this "
                         "one process, launches interleaved in rounds; prints one JSON line of medians")
     p.add_argument("--compare-rounds", type=int, default=6, help="--compare-libs: rounds (20 launches per library each)")
@@ -758,58 +759,78 @@ def run_single(args, dev) -> int:
 
 
 def compare_libs(args, dev) -> int:
-    """Decode-plan launch time of one workload with several builds of the library,
+    """Plan launch time of one workload with several builds of the library,
     measured in one process: the same inputs, one plan per library, 20 events-timed
     launches per library per round, the order reversed every other round. Box-to-box
     spread is several percent; within one process it is about 0.1%, which is what
-    tuning the kernel's compile-time knobs needs."""
+    tuning the kernels' compile-time knobs needs. ``--workload awq8b`` compares the
+    AWQ by-scale layer's plan (group 128, k = --awq-k); otherwise an FP8 workload's."""
     import ctypes
     import statistics
 
     import torch
 
     from mpserve_amd import _native
-    from mpserve_amd.decode import sidecar_decode_args
-    from mpserve_amd.mpserve_cuda import _descriptor
     from mpserve_amd.synthetic import config_weights
 
-    workload = "model8b" if args.workload in ("all", "gemm8b", "awq8b") else args.workload
-    entries, _ = build_fp8_entries(config_weights(workload), dev)
-    outs = [torch.empty(src.shape, dtype=torch.bfloat16, device=dev) for _, _, _, src in entries]
-    descs = [_descriptor(*sidecar_decode_args(f, sc)[:13], o) for (_, f, sc, _), o in zip(entries, outs)]
-    arr = (_native.MpsFp8Tensor * len(descs))(*descs)
     stream = torch.cuda.current_stream(dev)
     h = ctypes.c_void_p(stream.cuda_stream)
+    entries, outs, descs = [], [], []
+    if args.workload == "awq8b":
+        from mpserve_amd import awq
+        from mpserve_amd.awq import _sidecar_descriptor
+        from mpserve_amd.synthetic import make_awq_weight
+
+        workload, kind, tensor_t = "awq8b", "awq", _native.MpsAwqTensor
+        for j, (name, n, m, _, _, _) in enumerate(config_weights("layer8b")):
+            w = make_awq_weight(n, m, 128, seed=300 + j, device=dev)
+            sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, args.awq_k, 1024, True)
+            o = torch.empty((n, m), dtype=torch.bfloat16, device=dev)
+            entries.append((name, w.int4_u8, sc, w.bf16))
+            outs.append(o)
+            descs.append(_sidecar_descriptor(w.int4_u8, sc, o))
+    else:
+        from mpserve_amd.decode import sidecar_decode_args
+        from mpserve_amd.mpserve_cuda import _descriptor
+
+        workload = "model8b" if args.workload in ("all", "gemm8b") else args.workload
+        kind, tensor_t = "fp8", _native.MpsFp8Tensor
+        entries, _ = build_fp8_entries(config_weights(workload), dev)
+        outs = [torch.empty(src.shape, dtype=torch.bfloat16, device=dev) for _, _, _, src in entries]
+        descs = [_descriptor(*sidecar_decode_args(f, sc)[:13], o) for (_, f, sc, _), o in zip(entries, outs)]
+    arr = (tensor_t * len(descs))(*descs)
     libs = []
     for path in args.compare_libs:
         L = ctypes.CDLL(os.path.abspath(path))
         vp = ctypes.c_void_p
-        L.mps_fp8_plan_create.argtypes = [ctypes.POINTER(_native.MpsFp8Tensor), ctypes.c_int64, vp,
-                                          ctypes.POINTER(vp)]
-        L.mps_fp8_plan_decode.argtypes = [vp, vp]
-        L.mps_fp8_plan_read_status.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
-        L.mps_fp8_plan_destroy.argtypes = [vp]
+        create, decode, read_status, destroy = (getattr(L, f"mps_{kind}_plan_{x}")
+                                                for x in ("create", "decode", "read_status", "destroy"))
+        create.argtypes = [ctypes.POINTER(tensor_t), ctypes.c_int64, vp, ctypes.POINTER(vp)]
+        decode.argtypes = [vp, vp]
+        read_status.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
+        destroy.argtypes = [vp]
         L.mps_last_error.restype = ctypes.c_char_p
         plan = vp()
-        if L.mps_fp8_plan_create(arr, len(descs), h, ctypes.byref(plan)) != 0:
+        if create(arr, len(descs), h, ctypes.byref(plan)) != 0:
             raise RuntimeError(f"{path}: plan creation failed: {L.mps_last_error().decode()}")
         for o in outs:
             o.zero_()
         for _ in range(max(1, args.warmup // 3)):
-            if L.mps_fp8_plan_decode(plan, h) != 0:
+            if decode(plan, h) != 0:
                 raise RuntimeError(f"{path}: {L.mps_last_error().decode()}")
         st = ctypes.c_uint32(0)
-        L.mps_fp8_plan_read_status(plan, h, ctypes.byref(st))
+        read_status(plan, h, ctypes.byref(st))
         exact = None if args.no_verify else all(
             torch.equal(o.view(torch.uint16), src.view(torch.uint16)) for o, (_, _, _, src) in zip(outs, entries))
         log(f"{path}: status {st.value}, bit-exact {exact}")
-        libs.append({"path": path, "L": L, "plan": plan, "status": st.value, "bit_exact": exact, "ms": []})
+        libs.append({"path": path, "plan": plan, "decode": decode, "destroy": destroy, "status": st.value,
+                     "bit_exact": exact, "ms": []})
     for r in range(args.compare_rounds):
         for lib in (libs if r % 2 == 0 else libs[::-1]):
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
             for a, b in ev:
                 a.record(stream)
-                lib["L"].mps_fp8_plan_decode(lib["plan"], h)
+                lib["decode"](lib["plan"], h)
                 b.record(stream)
             torch.cuda.synchronize()
             lib["ms"].append(statistics.mean(a.elapsed_time(b) for a, b in ev))
@@ -821,11 +842,10 @@ def compare_libs(args, dev) -> int:
         rows.append({"lib": lib["path"], "median_ms": round(med, 4), "vs_first": round(med / base - 1, 4),
                      "rounds_ms": [round(x, 4) for x in lib["ms"]], "status": lib["status"],
                      "bit_exact": lib["bit_exact"]})
-        lib["L"].mps_fp8_plan_destroy(lib["plan"])
-    print(json.dumps({"metric": "decode plan launch ms per library build (one process, interleaved)",
+        lib["destroy"](lib["plan"])
+    print(json.dumps({"metric": "plan launch ms per library build (one process, interleaved)",
                       "workload": WORKLOADS[workload], "device": torch.cuda.get_device_name(dev),
-                      "arch": torch.cuda.get_device_properties(dev).gcnArchName, "libs": rows}),
-          flush=True)
+                      "arch": torch.cuda.get_device_properties(dev).gcnArchName, "libs": rows}), flush=True)
     return 0
 
 

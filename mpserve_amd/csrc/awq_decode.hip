@@ -361,7 +361,15 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
                                                 uint32_t base_lo, uint32_t base_hi, uint64_t bucket_bit,
                                                 const uint2 (&first)[4], uint32_t pos, uint32_t pos_end,
                                                 uint32_t *status) {
-  constexpr int DF = 8;  // int4 prefetch distance (steps)
+#ifndef MPS_AWQ_SLAB_PREFETCH
+#define MPS_AWQ_SLAB_PREFETCH 8
+#endif
+#ifndef MPS_AWQ_FEED_EVERY
+#define MPS_AWQ_FEED_EVERY 2
+#endif
+  constexpr int DF = MPS_AWQ_SLAB_PREFETCH;  // int4 prefetch distance (steps)
+  constexpr int FE = MPS_AWQ_FEED_EVERY;     // steps per bitstream feed (16 bytes: 2 x 44 bits fit)
+  static_assert(DF % FE == 0 && (FE == 1 || FE == 2), "a feed every one or two steps");
   constexpr int RB = 4;  // 16-byte blocks per bitstream request
   count = awq_uni(count);
   bucket_bit = ((uint64_t)awq_uni((uint32_t)(bucket_bit >> 32)) << 32) | awq_uni((uint32_t)bucket_bit);
@@ -545,21 +553,48 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   uint32_t Fr[DF], SOr[DF];
 #pragma unroll
   for (int u = 0; u < DF; ++u) SOr[u] = load_step(Fr[u]);
+  // Wave priorities, as in the FP8 slab decode: the issue arbiter favours the
+  // oldest ready wave, so a wave lowers its priority by one level per quarter
+  // of its steps, counted from a head start that grows with its age.
+#ifndef MPS_AWQ_PRIO
+#define MPS_AWQ_PRIO 1
+#endif
+#ifndef MPS_AWQ_PRIO_LEAD
+#define MPS_AWQ_PRIO_LEAD 16
+#endif
+  const uint32_t quarter = awq_uni(nfull / 4u > 0u ? nfull / 4u : 1u);
+  const uint32_t lead = (3u - (awq_uni(lane) >> 8)) * (quarter * MPS_AWQ_PRIO_LEAD / 16u);  // head start (steps)
+  uint32_t prio = 3u - (lead / quarter < 3u ? lead / quarter : 3u);
+  uint32_t prio_at = (lead / quarter + 1u) * quarter - lead;  // steps done when the priority next drops
+  if (MPS_AWQ_PRIO) {
+    if (prio == 3u) __builtin_amdgcn_s_setprio(3);
+    else if (prio == 2u) __builtin_amdgcn_s_setprio(2);
+    else if (prio == 1u) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+  }
   uint32_t g = 0;
   for (; g + (uint32_t)DF <= nfull; g += (uint32_t)DF) {
+    if (MPS_AWQ_PRIO && g >= prio_at) {
+      prio_at += quarter;
+      --prio;
+      if (prio == 2u) __builtin_amdgcn_s_setprio(2);
+      else if (prio == 1u) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
 #pragma unroll
     for (int u = 0; u < DF; ++u) {
-      if (u % 2 == 0) bitstream_step();
+      if (u % FE == 0) bitstream_step();
       const uint32_t F = Fr[u], so = SOr[u];
       SOr[u] = load_step(Fr[u]);  // the step DF ahead
       step(std::false_type{}, F, so);
     }
   }
+  if (MPS_AWQ_PRIO) __builtin_amdgcn_s_setprio(0);
   // the last (fewer than DF) full steps and the partial one; their bytes are already loaded
 #pragma unroll
   for (int u = 0; u < DF; ++u) {
     if (g + (uint32_t)u < gall) {
-      if (u % 2 == 0) bitstream_step();
+      if (u % FE == 0) bitstream_step();
       if (g + (uint32_t)u < nfull) step(std::false_type{}, Fr[u], SOr[u]);
       else step(std::true_type{}, Fr[u], SOr[u]);
     }
