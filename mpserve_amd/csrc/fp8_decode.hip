@@ -311,6 +311,18 @@ constexpr uint32_t kPast = 0x40000000u;    // offset beyond every fast-path buff
 constexpr uint32_t kBsPast = 0x80000000u;  // bitstream offset beyond every bucket's range
 constexpr uint32_t kSlabPast = 0xFFFFFFF0u;  // BF16 byte offset beyond every k = 1024 output (2*n*m < 2^32 - 16)
 constexpr int kCacheNT = 2;                  // buffer cache-policy bits: non-temporal (gfx950 NT)
+// Cache-policy bits of the slab path's streams (tuning builds only; gfx950
+// encodes sc0 = 1, nt = 2, sc1 = 16): the BF16 stores, the FP8 loads and the
+// bitstream reserve loads.
+#ifndef MPS_SLAB_OUT_CPOL
+#define MPS_SLAB_OUT_CPOL kCacheNT
+#endif
+#ifndef MPS_SLAB_FP8_CPOL
+#define MPS_SLAB_FP8_CPOL 0
+#endif
+#ifndef MPS_SLAB_BS_CPOL
+#define MPS_SLAB_BS_CPOL 0
+#endif
 
 // LDS: the queue (kQSlots x kBlock u32) at offset 0, then 256 tables x 128 u32
 // entries. During set-up the queue region also holds the fp8 -> table map; the
@@ -874,7 +886,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, (uint32_t)i < nreq ? off + 16u * (uint32_t)i : kBsPast,
-                                                             0, 0);
+                                                             0, MPS_SLAB_BS_CPOL);
         inb[i] = make_uint4(v[0], v[1], v[2], v[3]);
       }
       ninb = nreq;
@@ -904,14 +916,14 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
     uint32_t ret;
     if constexpr (!kWrap) {
       const uint32_t so = uni(w_off + (w_blk << 10));
-      F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, vf_al, so, 0);
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, vf_al, so, MPS_SLAB_FP8_CPOL);
       ret = so;
     } else {
       const uint32_t b = w_blk + R;
       const bool wrap = b >= P;
       const bool ok = !wrap || w_row + 1u < rows;
       const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << 10) + colw;
-      F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, ok ? off : 0u, 0, 0);
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, ok ? off : 0u, 0, MPS_SLAB_FP8_CPOL);
       ret = ok ? off << 1 : kSlabPast;
     }
     // advance (branch-free; past the last group the walk stays on it)
@@ -990,8 +1002,8 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
     const v2u o = {__builtin_amdgcn_perm(t2[1], t2[0], 0x05040100u), __builtin_amdgcn_perm(t2[1], t2[0], 0x07060302u)};
     // Non-temporal: the output is written once, and L2 is better spent on the
     // lanes' bitstream lines and the FP8 lines that wave pairs share.
-    if constexpr (!kWrap) __builtin_amdgcn_raw_buffer_store_b64(o, r_out, vf_al << 1, uni(so) << 1, kCacheNT);
-    else __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, kCacheNT);
+    if constexpr (!kWrap) __builtin_amdgcn_raw_buffer_store_b64(o, r_out, vf_al << 1, uni(so) << 1, MPS_SLAB_OUT_CPOL);
+    else __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, MPS_SLAB_OUT_CPOL);
   };
 
   uint32_t Fr[DF], SOr[DF];
