@@ -199,6 +199,11 @@ int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream);
 typedef struct mps_awq_plan mps_awq_plan;
 int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stream, mps_awq_plan **plan_out);
 int mps_awq_plan_decode(mps_awq_plan *plan, void *stream);
+/* Decode the plan into a buffer laid out like its outputs, moved to `out`, as
+ * mps_fp8_plan_decode_into does (the move must keep 8-byte alignment); the
+ * flags go to the device status word. No counterpart in the reference: it
+ * serves the AWQ decode ops' per-sidecar plan cache. */
+int mps_awq_plan_decode_into(mps_awq_plan *plan, uint16_t *out, void *stream);
 int mps_awq_plan_info(const mps_awq_plan *plan, int64_t *work_items);
 int mps_awq_plan_read_status(mps_awq_plan *plan, void *stream, uint32_t *status_out);
 int mps_awq_plan_destroy(mps_awq_plan *plan);

@@ -110,6 +110,7 @@ def lib():
     L.mps_awq_encode.argtypes = [ctypes.POINTER(MpsAwqEncodeIn), _p, ctypes.POINTER(_p)]
     L.mps_awq_plan_create.argtypes = [ctypes.POINTER(MpsAwqTensor), _i64, _p, ctypes.POINTER(_p)]
     L.mps_awq_plan_decode.argtypes = [_p, _p]
+    L.mps_awq_plan_decode_into.argtypes = [_p, _p, _p]
     L.mps_awq_plan_info.argtypes = [_p, ctypes.POINTER(_i64)]
     L.mps_awq_plan_read_status.argtypes = [_p, _p, ctypes.POINTER(ctypes.c_uint32)]
     L.mps_awq_plan_destroy.argtypes = [_p]
@@ -117,7 +118,7 @@ def lib():
                  "mps_fp8_plan_decode_into", "mps_fp8_plan_info", "mps_fp8_plan_read_status",
                  "mps_fp8_plan_destroy", "mps_fp8_read_status", "mps_fp8_decode_batch_noalloc",
                  "mps_awq_decode", "mps_awq_encode",
-                 "mps_awq_plan_create", "mps_awq_plan_decode", "mps_awq_plan_info", "mps_awq_plan_read_status",
+                 "mps_awq_plan_create", "mps_awq_plan_decode", "mps_awq_plan_decode_into", "mps_awq_plan_info", "mps_awq_plan_read_status",
                  "mps_awq_plan_destroy"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L

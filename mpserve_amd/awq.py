@@ -144,6 +144,40 @@ def _dt(t: torch.Tensor, dtype, dim: int | None, msg: str) -> None:
         raise ValueError(msg)
 
 
+class _AwqTensorPlan:
+    """A device plan of one AWQ tensor that holds no reference to its tensors (the
+    cache entry that owns it checks they are alive before every use)."""
+
+    def __init__(self, desc: "_native.MpsAwqTensor", stream: int):
+        arr = (_native.MpsAwqTensor * 1)(desc)
+        self.handle = ctypes.c_void_p()
+        _native.check(_native.lib().mps_awq_plan_create(arr, 1, ctypes.c_void_p(stream), ctypes.byref(self.handle)))
+
+    def decode_into(self, out: torch.Tensor, stream: int) -> None:
+        _native.check(_native.lib().mps_awq_plan_decode_into(self.handle, ctypes.c_void_p(out.data_ptr()),
+                                                             ctypes.c_void_p(stream)))
+
+    def close(self) -> None:
+        if self.handle:
+            _native.lib().mps_awq_plan_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+
+_AWQ_PLANS = None
+
+
+def _plan_cache():
+    """The AWQ decoders' per-sidecar plan cache (the FP8 op's rules: a plan from the
+    second call on a sidecar, dropped when a tensor is freed or written through torch;
+    MPSERVE_DECODE_PLANS=0 turns it off; clear_decode_plans() empties it)."""
+    global _AWQ_PLANS
+    if _AWQ_PLANS is None:
+        from .mpserve_cuda import _SidecarPlans
+
+        _AWQ_PLANS = _SidecarPlans(factory=_AwqTensorPlan)
+    return _AWQ_PLANS
+
+
 def _launch(int4, bitstream, syms, lens, table, col_start, col_len, offsets, rows, group_col, group_size,
             startbit, bit_base, n, m, max_len, out) -> torch.Tensor:
     dev = int4.device
@@ -167,9 +201,23 @@ def _launch(int4, bitstream, syms, lens, table, col_start, col_len, offsets, row
     d.n, d.m, d.out = n, m, out.data_ptr()
     if n * m >= (1 << 31):
         raise ValueError("tensor too large for the AWQ decode kernel (n*m >= 2^31)")
+    # From its second call on a by-scale sidecar that the slab path can take (k = 1024,
+    # 128-column groups) the op launches the sidecar's cached plan; other sidecars, and
+    # the first call, decode over whole buckets as the reference does (a tensor with
+    # fewer buckets than CUs then splits each bucket over two workgroups, which a plan
+    # does not).
+    key_tensors = tuple(t for t in (int4, bitstream, syms, lens, table, col_start, col_len, offsets, rows, group_col,
+                                    startbit, bit_base) if t is not None)
+    slab = group_col is not None and startbit.size(1) - 1 == 1024 and int(group_size) == 128
     with torch.cuda.device(dev):
-        _native.check(_native.lib().mps_awq_decode(ctypes.byref(d), int(max_len),
-                                                   ctypes.c_void_p(_stream_handle(dev))))
+        stream = _stream_handle(dev)
+        plan = None
+        if slab and table.size(0) > 0 and out.data_ptr() % 8 == 0:
+            plan = _plan_cache().get(key_tensors, n, m, d, dev, stream, extra=(int(group_size),))
+        if plan is not None:
+            plan.decode_into(out, stream)
+        else:
+            _native.check(_native.lib().mps_awq_decode(ctypes.byref(d), int(max_len), ctypes.c_void_p(stream)))
     _maybe_check_status(dev, "AWQ int4 decode")
     return out
 

@@ -739,12 +739,16 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
 // lanes) and a kRowSlots / nsub slice of the row offsets. With k = 256 four
 // buckets run in one workgroup instead of one (the tables allow one
 // workgroup per CU).
+// out_delta: elements every tensor's output moves by (a plan decoding into a
+// buffer laid out like, but other than, the one it was created with).
 __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
-                                                             const int4 *__restrict__ work, uint32_t *status) {
+                                                             const int4 *__restrict__ work, uint32_t *status,
+                                                             int64_t out_delta) {
   __shared__ uint32_t lut[kLutEntries];
   __shared__ uint32_t s_base[kRowSlots];
   const int4 w = work[blockIdx.x];
-  const mps_awq_tensor T = tensors[w.x];
+  mps_awq_tensor T = tensors[w.x];
+  T.out += out_delta;
   if (w.w == 1) {
     awq_slab_bucket(T, w.y, lut, s_base, status);
     return;
@@ -855,6 +859,7 @@ using namespace mps;
 struct mps_awq_plan {
   int device = 0;
   int64_t count = 0, nwork = 0;
+  uint16_t *first_out = nullptr;  // the first tensor's output at creation (decode_into moves from it)
   void *d_block = nullptr;
   uint32_t *d_status = nullptr;
   mps_awq_tensor *d_tensors = nullptr;
@@ -962,6 +967,7 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   MPS_HIP_CHECK(hipGetDevice(&plan->device));
   plan->count = count;
   plan->nwork = (int64_t)items.size();
+  plan->first_out = count > 0 ? tensors[0].out : nullptr;
   // status word (zero) | descriptors | work records: one allocation, one copy
   const size_t o_tensors = 256;
   const size_t o_work = o_tensors + ((sizeof(mps_awq_tensor) * (size_t)count + 255) & ~(size_t)255);
@@ -986,14 +992,32 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   return MPS_OK;
 }
 
+static int awq_plan_launch(mps_awq_plan *plan, int64_t out_delta, uint32_t *status, void *stream) {
+  if (plan->nwork == 0) return MPS_OK;
+  hipLaunchKernelGGL(awq_decode_plan, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
+                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, status, out_delta);
+  MPS_HIP_CHECK(hipGetLastError());
+  return MPS_OK;
+}
+
 int mps_awq_plan_decode(mps_awq_plan *plan, void *stream) {
   last_error().clear();
   if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
-  if (plan->nwork == 0) return MPS_OK;
-  hipLaunchKernelGGL(awq_decode_plan, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_status);
-  MPS_HIP_CHECK(hipGetLastError());
-  return MPS_OK;
+  return awq_plan_launch(plan, 0, plan->d_status, stream);
+}
+
+int mps_awq_plan_decode_into(mps_awq_plan *plan, uint16_t *out, void *stream) {
+  last_error().clear();
+  if (!plan) return fail(MPS_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (!out) return fail(MPS_ERR_INVALID_ARGUMENT, "out is NULL");
+  if (plan->count == 0) return MPS_OK;
+  uint32_t *status = nullptr;
+  const int rc = status_word(plan->device, &status);
+  if (rc != MPS_OK) return rc;
+  const intptr_t delta = reinterpret_cast<intptr_t>(out) - reinterpret_cast<intptr_t>(plan->first_out);
+  // the slab path stores 8 bytes a lane: the moved outputs keep its alignment
+  if (delta % 8 != 0) return fail(MPS_ERR_INVALID_ARGUMENT, "out must be aligned like the plan's outputs (8 bytes)");
+  return awq_plan_launch(plan, (int64_t)(delta / (intptr_t)sizeof(uint16_t)), status, stream);
 }
 
 int mps_awq_plan_info(const mps_awq_plan *plan, int64_t *work_items) {

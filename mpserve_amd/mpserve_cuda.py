@@ -161,6 +161,9 @@ class _TensorPlan:
             self.handle = ctypes.c_void_p()
 
 
+_CACHES: list = []  # every per-sidecar plan cache, for clear_decode_plans()
+
+
 class _SidecarPlans:
     """Single-tensor decode plans behind huffman_decode_fp8, one per sidecar.
 
@@ -186,10 +189,12 @@ class _SidecarPlans:
     MPSERVE_DECODE_PLANS=0 turns the cache off.
     """
 
-    def __init__(self, capacity: int = 256):
+    def __init__(self, capacity: int = 256, factory=None):
         self.capacity = capacity
+        self.factory = factory if factory is not None else _TensorPlan  # (descriptor, stream) -> plan
         self._entries: "collections.OrderedDict[tuple, list]" = collections.OrderedDict()
         self._lock = threading.Lock()
+        _CACHES.append(self)
 
     @staticmethod
     def _valid(entry, tensors: Sequence[torch.Tensor]) -> bool:
@@ -199,12 +204,13 @@ class _SidecarPlans:
                 return False
         return True
 
-    def get(self, tensors: Sequence[torch.Tensor], n: int, m: int, desc: _native.MpsFp8Tensor,
-            device: torch.device, stream: int) -> Optional[_TensorPlan]:
-        """The sidecar's plan, building it on its second sighting; None: decode over whole buckets."""
+    def get(self, tensors: Sequence[torch.Tensor], n: int, m: int, desc, device: torch.device, stream: int,
+            extra: tuple = ()) -> Optional[_TensorPlan]:
+        """The sidecar's plan, building it on its second sighting; None: decode over whole buckets.
+        ``extra``: further key parts (an AWQ group size)."""
         if self.capacity <= 0 or os.environ.get("MPSERVE_DECODE_PLANS", "1") == "0":
             return None
-        key = (device.index, n, m) + tuple(t.data_ptr() for t in tensors)
+        key = (device.index, n, m) + tuple(extra) + tuple(t.data_ptr() for t in tensors)
         dropped = []
         try:
             with self._lock:
@@ -222,7 +228,7 @@ class _SidecarPlans:
                 if entry[2] is None:
                     if torch.cuda.is_current_stream_capturing():
                         return None
-                    entry[2] = _TensorPlan(desc, stream)
+                    entry[2] = self.factory(desc, stream)
                 return entry[2]
         finally:
             for e in dropped:
@@ -245,8 +251,10 @@ _PLANS = _SidecarPlans()
 
 
 def clear_decode_plans() -> None:
-    """Drop every cached per-sidecar plan of huffman_decode_fp8 (see _SidecarPlans)."""
-    _PLANS.clear()
+    """Drop every cached per-sidecar plan of the decode ops (huffman_decode_fp8 and the
+    AWQ int4 decoders; see _SidecarPlans)."""
+    for c in list(_CACHES):
+        c.clear()
 
 
 def huffman_decode_fp8(fp8_params_u8: torch.Tensor, bitstream_u64: torch.Tensor, decode_syms_u16: torch.Tensor,

@@ -326,3 +326,56 @@ def test_plan_slab_path_matches_input_and_the_lane_path(n, m, cap, seed, monkeyp
         plan.close()
         outs[slab] = out
     assert torch.equal(outs["1"].view(torch.uint16), outs["0"].view(torch.uint16))
+
+
+def _op_call(sc, w, n, m, group, out=None):
+    if "bucket_group_offsets_i32" in sc:
+        return MPServe_cuda.huffman_decode_awq_int4_bucket_by_scale(
+            w.int4_u8, sc["bitstream_u64"], sc["decode_syms_u16"], sc["decode_lens_u8"], sc["bucket_table_i32"],
+            sc["bucket_group_offsets_i32"], sc["group_rows_i32"], sc["group_col_start_i32"],
+            sc["bucket_thread_startbit_u32"], sc["bucket_bit_base_i64"], n, m, 11, group, out=out)
+    return MPServe_cuda.huffman_decode_awq_int4_bucket(
+        w.int4_u8, sc["bitstream_u64"], sc["decode_syms_u16"], sc["decode_lens_u8"], sc["bucket_table_i32"],
+        sc["bucket_col_start_i32"], sc["bucket_col_len_i32"], sc["bucket_row_offsets_i32"], sc["row_indices_i32"],
+        sc["bucket_thread_startbit_u32"], sc["bucket_bit_base_i64"], n, m, 11, out=out)
+
+
+def test_op_plan_cache_alternating_sidecars():
+    """The AWQ decode ops keep one plan per by-scale sidecar (k = 1024, 128-column
+    groups) from their second call on, so its buckets take the slab path: sidecars of both layouts
+    alternated through the ops decode bit-exact on every call; an output that is
+    not 8-byte aligned takes the direct kernel; an in-place rewrite of a tensor
+    drops its sidecar's plan until it is seen twice again."""
+    from mpserve_amd import awq as awq_mod
+    from mpserve_amd import mpserve_cuda as mc
+
+    print("[awq] op plan cache", flush=True)
+    mc.clear_decode_plans()
+    cases = []
+    for n, m, group, by_scale, seed in ((2048, 4096, 128, True, 710), (512, 4096, None, False, 711)):
+        w = make_awq_weight(n, m, group, seed=seed, device=DEV)
+        sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, 1024, 1024, by_scale)
+        cases.append((sc, w, n, m, group or m))
+    read_status(torch.device(DEV))
+    for call in range(4):
+        for sc, w, n, m, group in cases:
+            out = _op_call(sc, w, n, m, group)
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)), f"call {call}"
+        assert read_status(torch.device(DEV)) == 0
+    cache = awq_mod._plan_cache()
+    # only the by-scale sidecar (k = 1024, 128-column groups) is cached
+    assert len(cache) == 1 and all(e[2] is not None for e in cache._entries.values())
+    sc, w, n, m, group = cases[0]
+    buf = torch.zeros(n * m + 1, dtype=torch.bfloat16, device=DEV)
+    out = _op_call(sc, w, n, m, group, out=buf[1:])  # 2-byte offset: the direct kernel
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16).reshape(-1))
+    w.int4_u8.copy_(w.int4_u8.clone())  # same bytes, new version
+    out = _op_call(sc, w, n, m, group)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16))
+    assert sum(e[2] is None for e in cache._entries.values()) == 1
+    assert read_status(torch.device(DEV)) == 0
+    mc.clear_decode_plans()
+    assert len(cache) == 0
