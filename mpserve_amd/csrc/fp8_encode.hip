@@ -17,6 +17,8 @@
 // The reference is single-threaded; here every O(N) pass runs on the GPU.
 #include <hip/hip_runtime.h>
 
+#include <rocprim/device/device_segmented_radix_sort.hpp>
+
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
@@ -634,6 +636,433 @@ __global__ void codebook_kernel(CodebookArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Codebooks with a wave per key (L <= 11). The keys' histogram entries are
+// sorted for all keys at once beforehand (a segmented radix sort of the
+// (count, symbol) keys), so a key's entries arrive in (count asc, sym asc)
+// order; one 64-lane workgroup then builds its codebook in LDS, with the same
+// results as codebook_kernel:
+//  - the ESC keep set from the sorted counts: the entry at ni - (2^L - 1) fixes
+//    the boundary count c; every entry above c's run is kept, and the run's
+//    first ones (smallest symbols) fill the rest;
+//  - esc_sym from a 65536-bit set of the symbols in LDS;
+//  - the package-merge levels built once, bottom-up, each level's outputs split
+//    over the lanes by merge path (a lane finds how many leaves precede its
+//    first output by binary search, then merges its run), keeping a leaf bit
+//    per item; the selection then counts leaf bits top-down;
+//  - canonical codes in list order, ranked within each length by ballots;
+//  - the decode table, and each histogram entry's code word from its list
+//    position, which follows from its sorted index.
+// NMAX bounds the coded list (min(ni, 2^L)); keys outside (lo, hi] of it are
+// left to another launch.
+// ---------------------------------------------------------------------------
+constexpr int kCbLanes = 64;
+
+__device__ __forceinline__ uint32_t cb_count(uint64_t k) { return key_count(k); }
+__device__ __forceinline__ uint32_t cb_sym(uint64_t k) { return (uint32_t)(k & 0xFFFFu); }
+
+template <int NMAX>
+struct CbShared {
+  int32_t lw[NMAX];   // list weights
+  int32_t sw[NMAX];   // ascending weights for the package-merge (kEscAwqByScale ESC lists)
+  int32_t hidx[NMAX];
+  uint16_t ls[NMAX];  // list symbols
+  uint16_t code[NMAX];
+  uint8_t lens[NMAX];
+  union {
+    struct {
+      int32_t A[4 * NMAX];
+      int32_t B[4 * NMAX];
+      uint32_t masks[11 * (NMAX / 8) + 16];
+    } pm;
+    uint32_t symset[65536 / 32];
+    uint8_t nibs[2048];
+  } u;
+  int32_t na[16];
+  int32_t xs[16];
+  uint32_t blc[16], ncode[16], run[16];
+  uint32_t acc, acc2, flag;
+};
+
+// Sum over the workgroup's 64 lanes (one wave), returned to every lane.
+__device__ __forceinline__ uint32_t cb_sum(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);
+  return v;
+}
+__device__ __forceinline__ uint32_t cb_min(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t w = (uint32_t)__shfl_xor((int)v, o);
+    v = w < v ? w : v;
+  }
+  return v;
+}
+
+// First index in [lo, hi) of the sorted keys whose count is >= c (lower) or > c (upper).
+__device__ __forceinline__ uint32_t cb_bound(const uint64_t *k, uint32_t lo, uint32_t hi, uint32_t c, bool upper) {
+  const int32_t ci = (int32_t)c;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    const int32_t x = (int32_t)cb_count(k[mid]);
+    if (upper ? x <= ci : x < ci) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+template <int NMAX>
+__global__ __launch_bounds__(kCbLanes) void codebook_wave_kernel(CodebookArgs a, const uint64_t *__restrict__ skeys,
+                                                                 const uint32_t *__restrict__ sslots, uint32_t lo_n,
+                                                                 uint32_t hi_n) {
+  __shared__ CbShared<NMAX> S;
+  const uint32_t g = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int L = a.L;
+  const uint32_t T = 1u << L;
+  const uint32_t tk = a.gid_tkey[g];
+  const uint32_t off = a.toff[tk];
+  const uint32_t ni = a.tcount[tk];
+  const uint32_t nmax = ni < T ? ni : T;
+  if (nmax <= lo_n || nmax > hi_n) return;
+  const uint64_t *keys = skeys + off;
+  const uint32_t *slots = sslots + off;
+  uint16_t *dsyms = a.decode_syms + (uint64_t)g * T;
+  uint8_t *dlens = a.decode_lens + (uint64_t)g * (T / 2 > 0 ? T / 2 : 1);
+  if (lane == 0) {
+    a.table_scale[g] = a.scale_values[tk >> 8];
+    a.table_fp8[g] = (uint16_t)(tk & 0xFF);
+  }
+  if (ni == 1) {
+    for (uint32_t j = lane; j < T; j += kCbLanes) dsyms[j] = (uint16_t)cb_sym(keys[0]);
+    for (uint32_t j = lane; j < T / 2; j += kCbLanes) dlens[j] = 0x11;  // len 1 in both nibbles
+    if (lane == 0) a.cw_slot[slots[0]] = (1u << 16) | 0u;
+    return;
+  }
+
+  // --- the coded list ---
+  const bool use_esc = ni > T;
+  const uint32_t keep = T - 1;
+  uint32_t nl, s0 = 0, s1 = 0, r = 0, esc_sym = 0, esc_pos = 0;
+  int32_t esc_w = 0;
+  if (!use_esc) {
+    for (uint32_t p = lane; p < ni; p += kCbLanes) {
+      const uint64_t k = keys[p];
+      S.lw[p] = (int32_t)cb_count(k);
+      S.ls[p] = (uint16_t)cb_sym(k);
+      S.hidx[p] = (int32_t)p;
+    }
+    nl = ni;
+  } else {
+    // kept: [s0, s0 + r) and [s1, ni), the top 2^L - 1 by (count desc, sym asc)
+    const uint32_t c = cb_count(keys[ni - keep]);
+    s0 = cb_bound(keys, 0, ni, c, false);
+    s1 = cb_bound(keys, s0, ni, c, true);
+    r = keep - (ni - s1);
+    uint32_t tot = 0, kept = 0;
+    for (uint32_t t = lane; t < ni; t += kCbLanes) {
+      const uint32_t cnt = cb_count(keys[t]);
+      tot += cnt;
+      kept += (t >= s1 || (t >= s0 && t < s0 + r)) ? cnt : 0u;
+    }
+    tot = cb_sum(tot);
+    kept = cb_sum(kept);
+    const uint32_t ew = tot - kept;  // int sums as in the reference
+    // esc_sym: the smallest u16 absent from the key's symbols (kEscAwqByScale) or
+    // from the kept ones (the other builders)
+    for (uint32_t i = lane; i < 65536 / 32; i += kCbLanes) S.u.symset[i] = 0u;
+    __syncthreads();
+    for (uint32_t t = lane; t < ni; t += kCbLanes) {
+      const bool in = a.esc_mode == kEscAwqByScale || t >= s1 || (t >= s0 && t < s0 + r);
+      if (in) {
+        const uint32_t sy = cb_sym(keys[t]);
+        atomicOr(&S.u.symset[sy >> 5], 1u << (sy & 31));
+      }
+    }
+    __syncthreads();
+    uint32_t cand = 0xFFFFFFFFu;
+    for (uint32_t i = lane; i < 65536 / 32; i += kCbLanes) {
+      const uint32_t wv = ~S.u.symset[i];
+      if (wv != 0u && cand == 0xFFFFFFFFu) cand = 32u * i + (uint32_t)__builtin_ctz(wv);
+    }
+    cand = cb_min(cand);
+    __syncthreads();
+    if (a.esc_mode == kEscAwqByScale) {
+      esc_sym = cand == 0xFFFFFFFFu ? 0xFFFFu : cand;
+      esc_w = (int32_t)ew;
+      // (count desc, sym asc), ESC last: an entry of a run [g0, g1) above c sits
+      // at (ni - g1) + (t - g0); the boundary run's first r follow them
+      for (uint32_t t = lane; t < ni; t += kCbLanes) {
+        uint32_t pos;
+        if (t >= s1) {
+          const uint32_t cc = cb_count(keys[t]);
+          const uint32_t g0 = cb_bound(keys, s1, t + 1, cc, false);
+          const uint32_t g1 = cb_bound(keys, t, ni, cc, true);
+          pos = (ni - g1) + (t - g0);
+        } else if (t >= s0 && t < s0 + r) {
+          pos = (ni - s1) + (t - s0);
+        } else {
+          continue;
+        }
+        const uint64_t k = keys[t];
+        S.lw[pos] = (int32_t)cb_count(k);
+        S.ls[pos] = (uint16_t)cb_sym(k);
+        S.hidx[pos] = (int32_t)t;
+      }
+      // the package-merge's weights, ascending: the kept counts in sorted order
+      // with the ESC weight merged in (ties: any order gives the same list)
+      uint32_t e_pos = 0;
+      {
+        uint32_t below = 0;  // kept counts < the ESC weight (as int)
+        for (uint32_t j = lane; j < keep; j += kCbLanes) {
+          const uint32_t t = j < r ? s0 + j : s1 + (j - r);
+          below += (int32_t)cb_count(keys[t]) < esc_w ? 1u : 0u;
+        }
+        e_pos = cb_sum(below);
+      }
+      for (uint32_t j = lane; j < keep; j += kCbLanes) {
+        const uint32_t t = j < r ? s0 + j : s1 + (j - r);
+        S.sw[j + (j >= e_pos ? 1u : 0u)] = (int32_t)cb_count(keys[t]);
+      }
+      if (lane == 0) {
+        S.sw[e_pos] = esc_w;
+        S.lw[keep] = esc_w;
+        S.ls[keep] = (uint16_t)esc_sym;
+        S.hidx[keep] = -1;
+      }
+      esc_pos = keep;
+    } else {
+      esc_sym = cand & 0xFFFFu;
+      esc_w = (a.esc_mode == kEscAwqBucket && (int32_t)ew <= 0) ? 1 : (int32_t)ew;
+      // (count asc, sym asc): the kept entries in sorted order with the ESC item
+      // inserted at its key's place
+      const uint64_t ek = item_key((uint32_t)esc_w, esc_sym);
+      uint32_t below = 0;
+      for (uint32_t j = lane; j < keep; j += kCbLanes) {
+        const uint32_t t = j < r ? s0 + j : s1 + (j - r);
+        below += item_key(cb_count(keys[t]), cb_sym(keys[t])) < ek ? 1u : 0u;
+      }
+      esc_pos = cb_sum(below);
+      for (uint32_t j = lane; j < keep; j += kCbLanes) {
+        const uint32_t t = j < r ? s0 + j : s1 + (j - r);
+        const uint32_t p = j + (j >= esc_pos ? 1u : 0u);
+        const uint64_t k = keys[t];
+        S.lw[p] = (int32_t)cb_count(k);
+        S.ls[p] = (uint16_t)cb_sym(k);
+        S.hidx[p] = (int32_t)t;
+      }
+      if (lane == 0) {
+        S.lw[esc_pos] = esc_w;
+        S.ls[esc_pos] = (uint16_t)esc_sym;
+        S.hidx[esc_pos] = -1;
+      }
+    }
+    nl = T;
+    if (lane == 0) atomicAdd(&a.esc_stats[0], 1u);
+  }
+  __syncthreads();
+
+  // --- package-merge lengths (see package_merge_lengths) ---
+  {
+    const int32_t *W = (use_esc && a.esc_mode == kEscAwqByScale) ? S.sw : S.lw;
+    const int n = (int)nl;
+    const int keep_pm = 4 * (n - 1);
+    const int words = (keep_pm + 31) / 32;
+    int32_t *A = S.u.pm.A, *B = S.u.pm.B;
+    int cur = n < keep_pm ? n : keep_pm;
+    for (int i = lane; i < cur; i += kCbLanes) A[i] = W[i];
+    for (int i = lane; i < words; i += kCbLanes) {
+      const int b = cur - 32 * i;
+      S.u.pm.masks[i] = b >= 32 ? 0xFFFFFFFFu : (b > 0 ? (1u << b) - 1u : 0u);
+    }
+    if (lane == 0) S.na[0] = cur;
+    __syncthreads();
+    for (int j = 1; j < L; ++j) {
+      const int np = cur / 2;
+      const int o = keep_pm < n + np ? keep_pm : n + np;
+      const int chunk = (((o + kCbLanes - 1) / kCbLanes) + 31) & ~31;  // whole mask words per lane
+      const int k0 = lane * chunk;
+      const int k1 = k0 + chunk < o ? k0 + chunk : o;
+      uint32_t *mk = S.u.pm.masks + j * words;
+      if (k0 < k1) {
+        // leaves among the first k0 outputs: the largest a with leaf a-1 before package k0-a
+        int lo = k0 - np > 0 ? k0 - np : 0, hi = k0 < n ? k0 : n;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          const int b = k0 - mid;
+          const bool ok = b >= np || W[mid - 1] <= (int32_t)((uint32_t)A[2 * b] + (uint32_t)A[2 * b + 1]);
+          if (ok) lo = mid;
+          else hi = mid - 1;
+        }
+        int ai = lo, bi = k0 - lo;
+        uint32_t bits = 0;
+        for (int k = k0; k < k1; ++k) {
+          const int32_t pw = bi < np ? (int32_t)((uint32_t)A[2 * bi] + (uint32_t)A[2 * bi + 1]) : 0;
+          const bool leaf = ai < n && (bi >= np || W[ai] <= pw);
+          B[k] = leaf ? W[ai] : pw;
+          ai += leaf ? 1 : 0;
+          bi += leaf ? 0 : 1;
+          bits |= (leaf ? 1u : 0u) << (k & 31);
+          if ((k & 31) == 31 || k + 1 == k1) {
+            mk[k >> 5] = bits;
+            bits = 0;
+          }
+        }
+      }
+      __syncthreads();
+      int32_t *t = A;
+      A = B;
+      B = t;
+      cur = o;
+      if (lane == 0) S.na[j] = o;
+    }
+    __syncthreads();
+    // top-down: leaves among each level's selected prefix
+    int c = 2 * (n - 1);
+    int nx = 0;
+    for (int level = L - 1; level >= 0 && c > 0; --level) {
+      const int cc = c < S.na[level] ? c : S.na[level];
+      const uint32_t *mk = S.u.pm.masks + level * words;
+      uint32_t x = 0;
+      for (int i = lane; i < (cc + 31) / 32; i += kCbLanes) {
+        const uint32_t wv = mk[i];
+        const int rem = cc - 32 * i;
+        x += __popc(rem >= 32 ? wv : (wv & ((1u << rem) - 1u)));
+      }
+      x = cb_sum(x);
+      if (lane == 0) S.xs[nx] = (int32_t)x;
+      ++nx;
+      c = 2 * (cc - (int)x);
+    }
+    __syncthreads();
+    for (int i = lane; i < n; i += kCbLanes) {
+      int len = 0;
+      for (int q = 0; q < nx; ++q) len += i < S.xs[q] ? 1 : 0;
+      S.lens[i] = (uint8_t)len;
+    }
+    if (lane < 16) {
+      S.blc[lane] = 0;
+      S.run[lane] = 0;
+    }
+    if (lane == 0) S.flag = 0;
+    __syncthreads();
+  }
+
+  // --- canonical codes (build_huffman.cu:171-203), handed out in list order ---
+  for (uint32_t p = lane; p < nl; p += kCbLanes) {
+    int len = S.lens[p];
+    if (len <= 0 || len > L) {
+      S.flag = 1;
+      continue;
+    }
+    if (use_esc && a.esc_mode != kEscFp8 && (uint32_t)S.ls[p] == esc_sym) {  // AWQ: ESC code has length L
+      len = L;
+      S.lens[p] = (uint8_t)L;
+    }
+    atomicAdd(&S.blc[len], 1u);
+  }
+  __syncthreads();
+  if (S.flag) {
+    if (lane == 0) atomicOr(a.err, 2u);
+    return;
+  }
+  if (lane == 0) {
+    uint32_t cd = 0;
+    S.ncode[0] = 0;
+    for (int b = 1; b < 16; ++b) {
+      cd = (cd + S.blc[b - 1]) << 1;
+      S.ncode[b] = cd;
+    }
+  }
+  __syncthreads();
+  for (uint32_t base = 0; base < nl; base += kCbLanes) {
+    const uint32_t p = base + lane;
+    const int len = p < nl ? S.lens[p] : 0;
+    uint32_t rank = 0, mine = 0;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int v = 1; v <= L; ++v) {
+      const uint64_t m = __ballot(len == v);
+      if (len == v) rank = (uint32_t)__popcll(m & below);
+      if (lane == v) mine = (uint32_t)__popcll(m);  // lane v keeps length v's count of this chunk
+    }
+    if (p < nl) S.code[p] = (uint16_t)(S.ncode[len] + S.run[len] + rank);
+    __syncthreads();
+    if (lane >= 1 && lane <= L) S.run[lane] += mine;
+    __syncthreads();
+  }
+
+  // --- decode table ---
+  for (uint32_t j = lane; j < T; j += kCbLanes) {
+    dsyms[j] = 0;
+    S.u.nibs[j] = 0;
+  }
+  __syncthreads();
+  uint32_t esc_cw = 0;
+  for (uint32_t p = lane; p < nl; p += kCbLanes) {
+    const uint32_t len = S.lens[p];
+    const uint32_t c = S.code[p];
+    const bool is_esc = use_esc && (uint32_t)S.ls[p] == esc_sym;
+    const uint32_t nib = is_esc ? (a.esc_mode == kEscFp8 ? (len | 0x8u) : 15u) : len;
+    const uint32_t fill = 1u << (L - len);
+    const uint32_t base = c << (L - len);
+    for (uint32_t f = 0; f < fill; ++f) {
+      dsyms[base + f] = S.ls[p];
+      S.u.nibs[base + f] = (uint8_t)nib;
+    }
+  }
+  if (use_esc) esc_cw = ((uint32_t)S.lens[esc_pos] << 16) | (S.code[esc_pos] & 0xFFFFu);
+  __syncthreads();
+  for (uint32_t j = lane; j < (T / 2 > 0 ? T / 2 : 1); j += kCbLanes)
+    dlens[j] = T >= 2 ? (uint8_t)((S.u.nibs[2 * j] & 0xF) | ((S.u.nibs[2 * j + 1] & 0xF) << 4)) : 0;
+
+  // --- code word of every histogram entry, from its list position ---
+  for (uint32_t t = lane; t < ni; t += kCbLanes) {
+    int32_t p = -1;
+    if (!use_esc) {
+      p = (int32_t)t;
+    } else if (a.esc_mode == kEscAwqByScale) {
+      if (t >= s1) {
+        const uint32_t cc = cb_count(keys[t]);
+        const uint32_t g0 = cb_bound(keys, s1, t + 1, cc, false);
+        const uint32_t g1 = cb_bound(keys, t, ni, cc, true);
+        p = (int32_t)((ni - g1) + (t - g0));
+      } else if (t >= s0 && t < s0 + r) {
+        p = (int32_t)((ni - s1) + (t - s0));
+      }
+    } else {
+      int32_t j = -1;
+      if (t >= s0 && t < s0 + r) j = (int32_t)(t - s0);
+      else if (t >= s1) j = (int32_t)(r + (t - s1));
+      if (j >= 0) p = j + (j >= (int32_t)esc_pos ? 1 : 0);
+    }
+    uint32_t cw;
+    if (p >= 0) {
+      cw = ((uint32_t)S.lens[p] << 16) | (S.code[p] & 0xFFFFu);
+    } else if (cb_sym(keys[t]) == esc_sym) {
+      cw = esc_cw;  // a data symbol equal to esc_sym: the ESC code alone
+      atomicAdd(&a.esc_stats[1], cb_count(keys[t]));
+    } else {
+      cw = esc_cw | kRaw;  // outside the map: ESC code + raw16
+    }
+    a.cw_slot[slots[t]] = cw;
+  }
+}
+
+__global__ void item_keys_kernel(const uint16_t *__restrict__ sym, const uint32_t *__restrict__ cnt, uint64_t n,
+                                 uint64_t *__restrict__ keys) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) keys[i] = item_key(cnt[i], sym[i]);
+}
+
+__global__ void segment_bounds_kernel(const uint32_t *gid_tkey, const uint32_t *toff, const uint32_t *tcount,
+                                      uint32_t G, uint32_t *beg, uint32_t *end) {
+  const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  const uint32_t tk = gid_tkey[g];
+  beg[g] = toff[tk];
+  end[g] = toff[tk] + tcount[tk];
+}
+
 __global__ void ws_size_kernel(const uint32_t *gid_tkey, const uint32_t *tcount, uint32_t G, uint32_t T,
                                uint32_t *sz) {
   const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1146,12 +1575,40 @@ int encode_impl(const EncodeSpec &sp, hipStream_t s, mps_fp8_sidecar **out) {
   HC(sc->table_scale.alloc(G));
   HC(sc->table_fp8.alloc(G));
   HC(cw_slot.alloc(cap));
-  // per-key workspace, sized by each key's list length
+  // Codebooks. L <= 11 (the FP8 and AWQ formats): the keys' histogram entries
+  // are sorted for all keys at once, then a wave per key builds each codebook in
+  // LDS (codebook_wave_kernel; one launch for lists of up to 512 items, one for
+  // the larger). Longer codes (L up to 15, reachable through the op's max_len)
+  // keep the work-item-per-key kernel and its global workspace.
+  const bool wave_cb = L <= 11;
+  DevBuf<uint64_t> keys_in, keys_sorted;
+  DevBuf<uint32_t> slots_sorted, seg_beg, seg_end;
+  DevBuf<char> sort_tmp;
+  if (wave_cb && G) {
+    HC(keys_in.alloc(D));
+    HC(keys_sorted.alloc(D));
+    HC(slots_sorted.alloc(D));
+    HC(seg_beg.alloc(G));
+    HC(seg_end.alloc(G));
+    if (D)
+      hipLaunchKernelGGL(item_keys_kernel, dim3((D + 255) / 256), dim3(256), 0, s, seg_sym.p, seg_cnt.p, (uint64_t)D,
+                         keys_in.p);
+    hipLaunchKernelGGL(segment_bounds_kernel, dim3((G + 255) / 256), dim3(256), 0, s, gid_tkey.p, toff.p, tcount.p, G,
+                       seg_beg.p, seg_end.p);
+    HC(hipGetLastError());
+    size_t tmp_bytes = 0;
+    HC(rocprim::segmented_radix_sort_pairs(nullptr, tmp_bytes, keys_in.p, keys_sorted.p, seg_slot.p, slots_sorted.p,
+                                           D, G, seg_beg.p, seg_end.p, 0, 48, s));
+    HC(sort_tmp.alloc(tmp_bytes));
+    HC(rocprim::segmented_radix_sort_pairs(sort_tmp.p, tmp_bytes, keys_in.p, keys_sorted.p, seg_slot.p,
+                                           slots_sorted.p, D, G, seg_beg.p, seg_end.p, 0, 48, s));
+  }
+  // per-key workspace of the work-item-per-key kernel, sized by each key's list length
   DevBuf<uint32_t> ws_sz;
   HC(ws_sz.alloc(G));
   HC(ws_off.alloc(G));
   uint32_t ws_total = 0;
-  if (G) {
+  if (G && !wave_cb) {
     hipLaunchKernelGGL(ws_size_kernel, dim3((G + 255) / 256), dim3(256), 0, s, gid_tkey.p, tcount.p, G, Tsz,
                        ws_sz.p);
     HC(hipGetLastError());
@@ -1179,7 +1636,14 @@ int encode_impl(const EncodeSpec &sp, hipStream_t s, mps_fp8_sidecar **out) {
   cba.esc_mode = sp.format;
   cba.err = flags.p + 1;
   cba.esc_stats = flags.p + 2;
-  if (G) hipLaunchKernelGGL(codebook_kernel, dim3((G + 63) / 64), dim3(64), 0, s, cba);
+  if (G && wave_cb) {
+    hipLaunchKernelGGL(codebook_wave_kernel<512>, dim3(G), dim3(kCbLanes), 0, s, cba, keys_sorted.p, slots_sorted.p,
+                       0u, 512u);
+    hipLaunchKernelGGL(codebook_wave_kernel<2048>, dim3(G), dim3(kCbLanes), 0, s, cba, keys_sorted.p,
+                       slots_sorted.p, 512u, 2048u);
+  } else if (G) {
+    hipLaunchKernelGGL(codebook_kernel, dim3((G + 63) / 64), dim3(64), 0, s, cba);
+  }
   HC(hipGetLastError());
 
   // --- 4. bucket tables ---
