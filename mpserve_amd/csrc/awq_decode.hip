@@ -355,12 +355,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t awq_rsrc(const void *base, uin
 }
 __device__ __forceinline__ uint32_t awq_uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 
-template <bool kEsc>
+// Slab layouts: by-scale groups, or row buckets whose column range is P blocks
+// of 1024 (P >= 4) with P % 4 == 0 (a step's four slabs in one row) or not (a
+// step can straddle two rows; each lane picks its row's offset).
+enum : int { kLayGroups = 0, kLayRows = 1, kLayRowsWrap = 2 };
+
+// base_lo / base_hi: lane l holds slab l's and l + 64's base (groups), or row
+// l's and l + 64's offset (rows, column start included); rows and P describe a
+// row bucket (rows x P elements per lane).
+template <bool kEsc, int kLay>
 __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const uint32_t *__restrict__ lut,
                                                 uint32_t *__restrict__ queue, uint32_t lane, uint32_t count,
-                                                uint32_t base_lo, uint32_t base_hi, uint64_t bucket_bit,
-                                                const uint2 (&first)[4], uint32_t pos, uint32_t pos_end,
-                                                uint32_t *status) {
+                                                uint32_t base_lo, uint32_t base_hi, uint32_t rows, uint32_t P,
+                                                uint64_t bucket_bit, const uint2 (&first)[4], uint32_t pos,
+                                                uint32_t pos_end, uint32_t *status) {
 #ifndef MPS_AWQ_SLAB_PREFETCH
 #define MPS_AWQ_SLAB_PREFETCH 8
 #endif
@@ -477,18 +485,61 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     feed();
   };
 
-  // --- walker: the int4 load of step g; returns its BF16 store byte offset ---
-  uint32_t w_g = 0;
+  // --- walker: the int4 load of step g; returns its BF16 store byte offset
+  // (kLayRows: the step's uniform element offset; the lane adds its own) ---
+  rows = awq_uni(rows);
+  P = awq_uni(P);
+  uint32_t w_g = 0, w_row = 0, w_blk = 0;
+  auto row_offset = [&](uint32_t r) -> uint32_t {
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)base_lo, (int)(r & 63u));
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)base_hi, (int)(r & 63u));
+    return r < 64u ? a : b;
+  };
+  uint32_t w_off = 0, w_next = 0;
+  if constexpr (kLay != kLayGroups) {
+    w_off = row_offset(0);
+    w_next = row_offset(rows > 1u ? 1u : 0u);  // offset of row w_row + 1 (kLayRowsWrap)
+  }
+  const uint32_t colw = (lane & ~63u) | v4;  // 64w + 4v: the lane's columns within a 1024-block
+  const uint32_t vf_al = R * 1024u + colw;   // ... and its block within an aligned step
   auto load_step = [&](uint32_t &F) -> uint32_t {
-    const uint32_t sl = 4u * w_g + R;  // this lane's slab
-    const bool hi = w_g >= 16u;        // slabs 4g .. 4g+3 are all below 64 or all above
-    const uint32_t src = hi ? base_hi : base_lo;
-    const uint32_t base = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((sl & 63u) << 2), (int)src);
-    const bool ok = sl < count;
-    const uint32_t off = base + v4;
-    F = __builtin_amdgcn_raw_buffer_load_b32(r_q, ok ? off : kSlabInPast, 0, 0);
-    w_g = awq_uni(w_g + (w_g + 1u < gall ? 1u : 0u));
-    return ok ? off << 1 : kSlabOutPast;
+    uint32_t ret;
+    if constexpr (kLay == kLayGroups) {
+      const uint32_t sl = 4u * w_g + R;  // this lane's slab
+      const bool hi = w_g >= 16u;        // slabs 4g .. 4g+3 are all below 64 or all above
+      const uint32_t src = hi ? base_hi : base_lo;
+      const uint32_t base = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((sl & 63u) << 2), (int)src);
+      const bool ok = sl < count;
+      const uint32_t off = base + v4;
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_q, ok ? off : kSlabInPast, 0, 0);
+      ret = ok ? off << 1 : kSlabOutPast;
+    } else if constexpr (kLay == kLayRows) {
+      const uint32_t so = awq_uni(w_off + (w_blk << 10));
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_q, vf_al, so, 0);
+      ret = so;
+    } else {
+      const uint32_t b = w_blk + R;
+      const bool wrap = b >= P;
+      const bool ok = !wrap || w_row + 1u < rows;
+      const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << 10) + colw;
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_q, ok ? off : kSlabInPast, 0, 0);
+      ret = ok ? off << 1 : kSlabOutPast;
+    }
+    const bool more = w_g + 1u < gall;
+    if constexpr (kLay != kLayGroups) {
+      // advance the row walk (past the last step it stays there)
+      const uint32_t nb = w_blk + 4u;
+      const bool wr = nb >= P;
+      const uint32_t nrow = w_row + ((more && wr) ? 1u : 0u);
+      const uint32_t noff = row_offset(nrow);
+      const uint32_t nnext = row_offset(nrow + 1u < rows ? nrow + 1u : nrow);
+      w_blk = awq_uni(more ? (wr ? nb - P : nb) : w_blk);
+      w_off = awq_uni(nrow != w_row ? noff : w_off);
+      w_next = awq_uni(nrow != w_row ? nnext : w_next);
+      w_row = awq_uni(nrow);
+    }
+    w_g = awq_uni(w_g + (more ? 1u : 0u));
+    return ret;
   };
 
   auto lookup = [&](uint32_t qb, uint32_t x) -> uint32_t {  // entry of int4 value qb at peek bits x[12:2]
@@ -547,7 +598,8 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     const auto t2 = __builtin_amdgcn_permlane16_swap(a, b, false, false);
     typedef unsigned v2u __attribute__((ext_vector_type(2)));
     const v2u o = {__builtin_amdgcn_perm(t2[1], t2[0], 0x05040100u), __builtin_amdgcn_perm(t2[1], t2[0], 0x07060302u)};
-    __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, kSlabCacheNT);
+    if constexpr (kLay == kLayRows) __builtin_amdgcn_raw_buffer_store_b64(o, r_out, vf_al << 1, awq_uni(so) << 1, kSlabCacheNT);
+    else __builtin_amdgcn_raw_buffer_store_b64(o, r_out, so, 0, kSlabCacheNT);
   };
 
   uint32_t Fr[DF], SOr[DF];
@@ -602,23 +654,32 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   if (0u - np - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
 }
 
-// One slab-path bucket (checked by the plan: by-scale, k = 1024, 128-column
-// groups, 8 .. 1024 groups). Set-up in two levels of loads, each issued in full
-// before any result is used: (1) the table ids, the wave's group rows and
-// column starts, the lane's start and end bits; (2) the tables' slices and the
-// lane's first bitstream words. Thread tid expands entries 32c .. 32c+31 of the
-// table of int4 value tid / 64 (c = tid % 64).
+// One slab-path bucket, checked by the plan: k = 1024 and either by-scale
+// with 128-column groups and 8 .. 1024 groups, or a row bucket of 1 .. 128 rows
+// whose column range is P >= 4 blocks of 1024. Set-up in two levels of loads,
+// each issued in full before any result is used: (1) the table ids, the
+// wave's group rows and column starts (or the bucket's rows), the lane's start
+// and end bits; (2) the tables' slices and the lane's first bitstream words.
+// Thread tid expands entries 32c .. 32c+31 of the table of int4 value tid / 64
+// (c = tid % 64).
 __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t b, uint32_t *__restrict__ lut,
                                                 uint32_t *__restrict__ region, uint32_t *status) {
   int tid;
   __asm__ volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+  const bool by_scale = T.group_col_start != nullptr;
   const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
-  const int32_t groups = rb - ra;
-  if (groups < kSlabMinGroups || groups > kSlabMaxGroups || ra < 0 || (int64_t)rb > T.num_row_indices ||
-      T.k != kAwqBlock || T.group_size != 128) {
+  const int32_t groups = rb - ra;  // groups (by-scale) or rows
+  const int32_t c0 = by_scale ? 0 : T.bucket_col_start[b];
+  const int32_t cl = by_scale ? 128 : T.bucket_col_len[b];
+  const bool shape_ok =
+      by_scale ? (groups >= kSlabMinGroups && groups <= kSlabMaxGroups && T.group_size == 128)
+               : (groups >= 1 && groups <= 128 && cl >= 4 * kAwqBlock && cl % kAwqBlock == 0 && c0 >= 0 &&
+                  (int64_t)c0 + cl <= T.m);
+  if (!shape_ok || ra < 0 || (int64_t)rb > T.num_row_indices || T.k != kAwqBlock) {
     if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
     return;
   }
+  const uint32_t P = by_scale ? 0u : (uint32_t)cl / (uint32_t)kAwqBlock;
   const uint32_t w = (uint32_t)tid >> 6, wl = (uint32_t)tid & 63u;
   const uint32_t t = (w << 6) | (((uint32_t)tid & 15u) << 2) | (((uint32_t)tid >> 4) & 3u);  // substream
   const int q = tid >> 6, c = tid & 63;
@@ -626,12 +687,13 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
   const __amdgpu_buffer_rsrc_t r_tab = awq_rsrc(T.bucket_table + b * 16, 64u);
   const int32_t gq = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_tab, (uint32_t)q * 4u, 0, 0);
   const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra, (uint32_t)groups * 4u);
-  const __amdgpu_buffer_rsrc_t r_gcol = awq_rsrc(T.group_col_start + ra, (uint32_t)groups * 4u);
-  const uint32_t gi0 = 8u * wl + (w >> 1), gi1 = 8u * (wl + 64u) + (w >> 1);
+  const __amdgpu_buffer_rsrc_t r_gcol = awq_rsrc(by_scale ? T.group_col_start + ra : nullptr, by_scale ? (uint32_t)groups * 4u : 0u);
+  // by-scale: groups 8 wl + w/2 and 8 (wl + 64) + w/2 (slabs wl and wl + 64); rows: rows wl and wl + 64
+  const uint32_t gi0 = by_scale ? 8u * wl + (w >> 1) : wl, gi1 = by_scale ? 8u * (wl + 64u) + (w >> 1) : wl + 64u;
   const int32_t row0 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi0 * 4u, 0, 0);
-  const int32_t col0 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi0 * 4u, 0, 0);
+  const int32_t col0 = by_scale ? (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi0 * 4u, 0, 0) : c0;
   const int32_t row1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi1 * 4u, 0, 0);
-  const int32_t col1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi1 * 4u, 0, 0);
+  const int32_t col1 = by_scale ? (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi1 * 4u, 0, 0) : c0;
   const __amdgpu_buffer_rsrc_t r_sb = awq_rsrc(T.bucket_thread_startbit + b * (kAwqBlock + 1), (kAwqBlock + 1) * 4u);
   const uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(r_sb, t * 4u, 0, 0);
   const uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_sb, (t + 1u) * 4u, 0, 0);
@@ -696,12 +758,13 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
       dst[1] = make_uint4(e[4], e[5], e[6], e[7]);
     }
   }
-  // group bases of this wave for slabs wl and wl + 64
+  // group bases of this wave for slabs wl and wl + 64 (by-scale), or the
+  // offsets of rows wl and wl + 64 with the column start (rows)
   const uint32_t m = (uint32_t)T.m;
   auto gbase = [&](uint32_t gi, int32_t row, int32_t col, bool &bad) -> uint32_t {
     if (gi >= (uint32_t)groups) return 0u;
-    bad |= row < 0 || (int64_t)row >= T.n || col < 0 || (int64_t)col + 128 > T.m;
-    return (uint32_t)row * m + (uint32_t)col + ((w & 1u) << 6);
+    bad |= row < 0 || (int64_t)row >= T.n || col < 0 || (int64_t)col + cl > T.m;
+    return (uint32_t)row * m + (uint32_t)col + (by_scale ? ((w & 1u) << 6) : 0u);
   };
   bool bad_row = false;
   const uint32_t base_lo = gbase(gi0, row0, col0, bad_row);
@@ -721,15 +784,25 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
     if (tid == 0) flag(status, MPS_STATUS_BAD_ROW);
     return;
   }
-  // this wave's elements per lane: every full slab, and the partial last one
-  // when its group w/2 exists
-  const uint32_t count = (uint32_t)groups / 8u + ((w >> 1) < ((uint32_t)groups & 7u) ? 1u : 0u);
-  if (bflags & 2u)
-    awq_slab_decode<true>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, bucket_bit, first, pos, pos_end,
-                          status);
-  else
-    awq_slab_decode<false>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, bucket_bit, first, pos, pos_end,
-                           status);
+  // this wave's elements per lane: by-scale, every full slab and the partial
+  // last one when its group w/2 exists; rows, rows x P
+  const uint32_t count = by_scale ? (uint32_t)groups / 8u + ((w >> 1) < ((uint32_t)groups & 7u) ? 1u : 0u)
+                                  : (uint32_t)groups * P;
+  const bool esc = (bflags & 2u) != 0u;
+#define MPS_AWQ_SLAB(ESC, LAY)                                                                                   \
+  awq_slab_decode<ESC, LAY>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)groups, P, bucket_bit, \
+                            first, pos, pos_end, status)
+  if (by_scale) {
+    if (esc) MPS_AWQ_SLAB(true, kLayGroups);
+    else MPS_AWQ_SLAB(false, kLayGroups);
+  } else if (P % 4u == 0u) {
+    if (esc) MPS_AWQ_SLAB(true, kLayRows);
+    else MPS_AWQ_SLAB(false, kLayRows);
+  } else {
+    if (esc) MPS_AWQ_SLAB(true, kLayRowsWrap);
+    else MPS_AWQ_SLAB(false, kLayRowsWrap);
+  }
+#undef MPS_AWQ_SLAB
 }
 
 // Plan launch: workgroup i decodes buckets work[i].y .. work[i].y + work[i].z - 1
@@ -906,7 +979,7 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   // they can share a workgroup's tables; ordered by elements, largest first,
   // so the launch's last workgroups are its smallest.
   std::vector<std::pair<int64_t, int4>> items;
-  std::vector<int32_t> roff, clen, btab, gcol;
+  std::vector<int32_t> roff, clen, cst, btab, gcol;
   const char *slab_env = std::getenv("MPSERVE_AWQ_SLAB");
   const bool slab_on = !(slab_env && slab_env[0] == '0');
   for (int64_t i = 0; i < count; ++i) {
@@ -923,15 +996,20 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
       clen.resize((size_t)B);
       MPS_HIP_CHECK(hipMemcpy(clen.data(), T.bucket_col_len, sizeof(int32_t) * B, hipMemcpyDefault));
     }
-    // The slab path (by-scale, k = 1024, 128-column groups) loads int4 bytes as
-    // dwords and stores 8 bytes a lane: every group must start on a 4-element
-    // boundary and the buffers must be aligned to match.
-    bool slab_tensor = slab_on && T.group_col_start && T.k == kAwqBlock && T.group_size == 128 && T.m % 4 == 0 &&
+    // The slab path (k = 1024: by-scale with 128-column groups, or row buckets of
+    // 1..128 rows over P >= 4 blocks of 1024 columns) loads int4 bytes as dwords
+    // and stores 8 bytes a lane: every group or column range must start on a
+    // 4-element boundary and the buffers must be aligned to match.
+    bool slab_tensor = slab_on && T.k == kAwqBlock && (!T.group_col_start || T.group_size == 128) && T.m % 4 == 0 &&
                        (reinterpret_cast<uintptr_t>(T.int4) & 3u) == 0 && (reinterpret_cast<uintptr_t>(T.out) & 7u) == 0;
-    if (slab_tensor && T.num_row_indices > 0) {
+    if (slab_tensor && T.group_col_start && T.num_row_indices > 0) {
       gcol.resize((size_t)T.num_row_indices);
       MPS_HIP_CHECK(hipMemcpy(gcol.data(), T.group_col_start, sizeof(int32_t) * T.num_row_indices, hipMemcpyDefault));
       slab_tensor = std::all_of(gcol.begin(), gcol.end(), [](int32_t c) { return (c & 3) == 0; });
+    }
+    if (slab_tensor && !T.group_col_start) {
+      cst.resize((size_t)B);
+      MPS_HIP_CHECK(hipMemcpy(cst.data(), T.bucket_col_start, sizeof(int32_t) * B, hipMemcpyDefault));
     }
     auto rows_of = [&](int64_t b) { return std::max<int64_t>(0, (int64_t)roff[(size_t)b + 1] - roff[(size_t)b]); };
     auto elems_of = [&](int64_t b) {
@@ -942,8 +1020,15 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     const int64_t row_cap = kRowSlots / 4;
     int64_t b = 0;
     while (b < B) {
-      if (slab_tensor && rows_of(b) >= kSlabMinGroups && rows_of(b) <= kSlabMaxGroups &&
-          roff[(size_t)b] >= 0 && roff[(size_t)b + 1] <= T.num_row_indices) {
+      // (cst holds the column starts only for a slab-eligible row-layout tensor)
+      const bool slab_shape =
+          slab_tensor &&
+          (T.group_col_start
+               ? rows_of(b) >= kSlabMinGroups && rows_of(b) <= kSlabMaxGroups
+               : rows_of(b) >= 1 && rows_of(b) <= 128 && clen[(size_t)b] >= 4 * kAwqBlock &&
+                     clen[(size_t)b] % kAwqBlock == 0 && cst[(size_t)b] >= 0 && (cst[(size_t)b] & 3) == 0 &&
+                     (int64_t)cst[(size_t)b] + clen[(size_t)b] <= T.m);
+      if (slab_shape && roff[(size_t)b] >= 0 && roff[(size_t)b + 1] <= T.num_row_indices) {
         items.push_back({elems_of(b), make_int4((int)i, (int)b, 1, 1)});
         ++b;
         continue;

@@ -285,31 +285,45 @@ def test_truncated_bitstream_and_wild_start_bits_flag_desync_without_faults():
         assert read_status(torch.device(DEV)) & MPS_STATUS_DESYNC, what
 
 
-def _slab_buckets(sc):
-    """Group counts of the buckets the plan sends down the slab path (8..1024 groups)."""
-    off = sc["bucket_group_offsets_i32"].cpu().numpy().astype(np.int64)
-    g = np.diff(off)
-    return g[(g >= 8) & (g <= 1024)]
+def _slab_counts(sc):
+    """Per-lane element counts of the buckets the plan sends down the slab path:
+    by-scale buckets of 8..1024 groups (one count per wave pair), row buckets of
+    1..128 rows over P >= 4 blocks of 1024 columns (rows x P)."""
+    if "bucket_group_offsets_i32" in sc:
+        g = np.diff(sc["bucket_group_offsets_i32"].cpu().numpy().astype(np.int64))
+        g = g[(g >= 8) & (g <= 1024)]
+        return np.concatenate([g // 8 + (j < g % 8) for j in range(8)]) if g.size else g
+    rows = np.diff(sc["bucket_row_offsets_i32"].cpu().numpy().astype(np.int64))
+    cl = sc["bucket_col_len_i32"].cpu().numpy().astype(np.int64)
+    ok = (rows >= 1) & (rows <= 128) & (cl % 1024 == 0) & (cl >= 4096)
+    return (rows * (cl // 1024))[ok]
 
 
-@pytest.mark.parametrize("n,m,cap,seed", [(4096, 4096, 1024, 700), (1024, 4096, 1024, 701), (2048, 4096, 12, 702),
-                                          (14336, 4096, 1024, 703)],
-                         ids=["q_4096", "kv_1024x4096", "cap12_partial_slabs", "gate_14336x4096"])
-def test_plan_slab_path_matches_input_and_the_lane_path(n, m, cap, seed, monkeypatch):
-    """By-scale sidecars with k = 1024 and 128-column groups decode on the slab path
-    (dword int4 loads, register transposes, 8-byte stores): bit-exact to the input,
-    equal to the per-lane path's output, status clean. The cases hold ESC keys,
-    buckets whose group count is not a multiple of 8 (a partial last slab) and
-    waves whose step count is not a multiple of 4 (a partial last step)."""
-    print(f"[awq] slab path {n}x{m} cap {cap}", flush=True)
-    w = make_awq_weight(n, m, 128, seed=seed, device=DEV)
-    sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, 1024, cap, True, with_stats=True)
-    groups = _slab_buckets(sc)
-    assert groups.size > 0
-    assert (groups % 8 != 0).any()
-    counts = np.concatenate([groups // 8 + (np.arange(8)[None, :] < (groups % 8)[:, None])[:, j] for j in range(8)])
-    assert (counts % 4 != 0).any()
-    if n * m >= 4096 * 4096:
+@pytest.mark.parametrize(
+    "by_scale,n,m,cap,seed",
+    [(True, 4096, 4096, 1024, 700), (True, 1024, 4096, 1024, 701), (True, 2048, 4096, 12, 702),
+     (True, 14336, 4096, 1024, 703), (False, 2048, 4096, 1024, 721), (False, 512, 14336, 1024, 722),
+     (False, 1024, 14336, 1024, 724)],
+    ids=["q_4096", "kv_1024x4096", "cap12_partial_slabs", "gate_14336x4096", "rows_p4", "rows_p14_wrap",
+         "rows_p14_1024"])
+def test_plan_slab_path_matches_input_and_the_lane_path(by_scale, n, m, cap, seed, monkeypatch):
+    """Sidecars with k = 1024 decode on the slab path (dword int4 loads, register
+    transposes, 8-byte stores): by-scale with 128-column groups, and row buckets
+    over P >= 4 blocks of 1024 columns (P % 4 == 0, or a step straddling two rows).
+    Bit-exact to the input, equal to the per-lane path's output, status clean. The
+    cases hold ESC keys, partial last slabs (by-scale group counts not a multiple
+    of 8) and partial last steps (per-lane counts not a multiple of 4)."""
+    print(f"[awq] slab path {'by-scale' if by_scale else 'rows'} {n}x{m} cap {cap}", flush=True)
+    w = make_awq_weight(n, m, 128 if by_scale else None, seed=seed, device=DEV)
+    sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, 1024, cap, by_scale, with_stats=True)
+    assert st["esc_collisions"] == 0
+    counts = _slab_counts(sc)
+    assert counts.size > 0
+    if by_scale and cap == 12:
+        assert (counts % 4 != 0).any()
+    if not by_scale and m % 4096 != 0:
+        assert (counts % 4 != 0).any()  # rows x 14: partial last steps
+    if not by_scale or n * m >= 4096 * 4096:  # every row case here has ESC keys (6, 10 and 23)
         assert st["esc_keys"] > 0
     outs = {}
     for slab in ("1", "0"):
