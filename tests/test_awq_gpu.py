@@ -355,8 +355,9 @@ def _op_call(sc, w, n, m, group, out=None):
 
 
 def test_op_plan_cache_alternating_sidecars():
-    """The AWQ decode ops keep one plan per by-scale sidecar (k = 1024, 128-column
-    groups) from their second call on, so its buckets take the slab path: sidecars of both layouts
+    """The AWQ decode ops keep one plan per sidecar with k = 1024 (by-scale with
+    128-column groups, or row buckets) from their second call on, so its buckets take
+    the slab path: sidecars of both layouts
     alternated through the ops decode bit-exact on every call; an output that is
     not 8-byte aligned takes the direct kernel; an in-place rewrite of a tensor
     drops its sidecar's plan until it is seen twice again."""
@@ -378,8 +379,7 @@ def test_op_plan_cache_alternating_sidecars():
             assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)), f"call {call}"
         assert read_status(torch.device(DEV)) == 0
     cache = awq_mod._plan_cache()
-    # only the by-scale sidecar (k = 1024, 128-column groups) is cached
-    assert len(cache) == 1 and all(e[2] is not None for e in cache._entries.values())
+    assert len(cache) == 2 and all(e[2] is not None for e in cache._entries.values())
     sc, w, n, m, group = cases[0]
     buf = torch.zeros(n * m + 1, dtype=torch.bfloat16, device=DEV)
     out = _op_call(sc, w, n, m, group, out=buf[1:])  # 2-byte offset: the direct kernel
