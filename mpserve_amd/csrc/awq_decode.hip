@@ -338,6 +338,20 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
 // 4 flags it and the running shift steps over the raw bits; a step holding an
 // ESC code is decoded again code by code, reading the raw symbol.
 // ---------------------------------------------------------------------------
+// A plan's work record: one record per workgroup.
+//  kind 0: buckets bucket .. bucket + nsub - 1 on the per-lane path (one scale, shared tables);
+//  kind 1: one slab-path bucket;
+//  kind 2: rows [range * range_rows, +range_rows) of a slab-path row bucket split into
+//          `ranges` ranges, starting from the lane checkpoints at ckpt + (range - 1) * 1024
+//          and ending at ckpt + range * 1024 (the bucket's own start and end bits at its ends).
+struct AwqWork {
+  int32_t tensor, bucket, nsub, kind;
+  int32_t range, range_rows, ranges, pad;
+  int64_t ckpt;
+  int64_t elems;  // (the plan's ordering key)
+};
+static_assert(sizeof(AwqWork) == 48, "work record layout");
+
 constexpr uint32_t kAwqEscBit = 1u << 4;
 constexpr uint32_t kAwqEscLow = 27u;          // 11 + 16: an ESC entry's low bits
 constexpr int kSlabQSlots = 8;                // LDS queue chunks per lane
@@ -662,10 +676,12 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
 // and end bits; (2) the tables' slices and the lane's first bitstream words.
 // Thread tid expands entries 32c .. 32c+31 of the table of int4 value tid / 64
 // (c = tid % 64).
-__device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t b, uint32_t *__restrict__ lut,
+__device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const AwqWork &wk,
+                                                const uint32_t *__restrict__ ckpt, uint32_t *__restrict__ lut,
                                                 uint32_t *__restrict__ region, uint32_t *status) {
   int tid;
   __asm__ volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+  const int64_t b = wk.bucket;
   const bool by_scale = T.group_col_start != nullptr;
   const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
   const int32_t groups = rb - ra;  // groups (by-scale) or rows
@@ -680,13 +696,21 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
     return;
   }
   const uint32_t P = by_scale ? 0u : (uint32_t)cl / (uint32_t)kAwqBlock;
+  // a row range (kind 2): its first row and row count; its lanes start and end at checkpoints
+  const bool ranged = wk.kind == 2 && !by_scale;
+  const int32_t first_row = ranged ? wk.range * wk.range_rows : 0;
+  const int32_t nr = ranged ? (groups - first_row < wk.range_rows ? groups - first_row : wk.range_rows) : groups;
+  if (nr <= 0) {
+    if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
+    return;
+  }
   const uint32_t w = (uint32_t)tid >> 6, wl = (uint32_t)tid & 63u;
   const uint32_t t = (w << 6) | (((uint32_t)tid & 15u) << 2) | (((uint32_t)tid >> 4) & 3u);  // substream
   const int q = tid >> 6, c = tid & 63;
   // level 1
   const __amdgpu_buffer_rsrc_t r_tab = awq_rsrc(T.bucket_table + b * 16, 64u);
   const int32_t gq = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_tab, (uint32_t)q * 4u, 0, 0);
-  const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra, (uint32_t)groups * 4u);
+  const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra + first_row, (uint32_t)nr * 4u);
   const __amdgpu_buffer_rsrc_t r_gcol = awq_rsrc(by_scale ? T.group_col_start + ra : nullptr, by_scale ? (uint32_t)groups * 4u : 0u);
   // by-scale: groups 8 wl + w/2 and 8 (wl + 64) + w/2 (slabs wl and wl + 64); rows: rows wl and wl + 64
   const uint32_t gi0 = by_scale ? 8u * wl + (w >> 1) : wl, gi1 = by_scale ? 8u * (wl + 64u) + (w >> 1) : wl + 64u;
@@ -695,8 +719,15 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
   const int32_t row1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi1 * 4u, 0, 0);
   const int32_t col1 = by_scale ? (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi1 * 4u, 0, 0) : c0;
   const __amdgpu_buffer_rsrc_t r_sb = awq_rsrc(T.bucket_thread_startbit + b * (kAwqBlock + 1), (kAwqBlock + 1) * 4u);
-  const uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(r_sb, t * 4u, 0, 0);
-  const uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_sb, (t + 1u) * 4u, 0, 0);
+  const __amdgpu_buffer_rsrc_t r_ck =
+      awq_rsrc(ranged ? ckpt + wk.ckpt : nullptr, ranged ? (uint32_t)(wk.ranges - 1) * (uint32_t)kAwqBlock * 4u : 0u);
+  const bool from_ck = ranged && wk.range > 0, to_ck = ranged && wk.range + 1 < wk.ranges;
+  const uint32_t pos = from_ck ? __builtin_amdgcn_raw_buffer_load_b32(
+                                     r_ck, ((uint32_t)(wk.range - 1) * (uint32_t)kAwqBlock + t) * 4u, 0, 0)
+                               : __builtin_amdgcn_raw_buffer_load_b32(r_sb, t * 4u, 0, 0);
+  const uint32_t pos_end = to_ck ? __builtin_amdgcn_raw_buffer_load_b32(
+                                       r_ck, ((uint32_t)wk.range * (uint32_t)kAwqBlock + t) * 4u, 0, 0)
+                                 : __builtin_amdgcn_raw_buffer_load_b32(r_sb, (t + 1u) * 4u, 0, 0);
   const uint64_t bucket_bit = (uint64_t)T.bucket_bit_base[b];
   // level 2
   const bool tab_ok = gq >= 0 && gq < T.num_tables;
@@ -762,7 +793,7 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
   // offsets of rows wl and wl + 64 with the column start (rows)
   const uint32_t m = (uint32_t)T.m;
   auto gbase = [&](uint32_t gi, int32_t row, int32_t col, bool &bad) -> uint32_t {
-    if (gi >= (uint32_t)groups) return 0u;
+    if (gi >= (uint32_t)nr) return 0u;
     bad |= row < 0 || (int64_t)row >= T.n || col < 0 || (int64_t)col + cl > T.m;
     return (uint32_t)row * m + (uint32_t)col + (by_scale ? ((w & 1u) << 6) : 0u);
   };
@@ -787,10 +818,10 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
   // this wave's elements per lane: by-scale, every full slab and the partial
   // last one when its group w/2 exists; rows, rows x P
   const uint32_t count = by_scale ? (uint32_t)groups / 8u + ((w >> 1) < ((uint32_t)groups & 7u) ? 1u : 0u)
-                                  : (uint32_t)groups * P;
+                                  : (uint32_t)nr * P;
   const bool esc = (bflags & 2u) != 0u;
 #define MPS_AWQ_SLAB(ESC, LAY)                                                                                   \
-  awq_slab_decode<ESC, LAY>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)groups, P, bucket_bit, \
+  awq_slab_decode<ESC, LAY>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)nr, P, bucket_bit, \
                             first, pos, pos_end, status)
   if (by_scale) {
     if (esc) MPS_AWQ_SLAB(true, kLayGroups);
@@ -805,6 +836,76 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
 #undef MPS_AWQ_SLAB
 }
 
+// Lane checkpoints of a slab-path row bucket split into row ranges: where each
+// substream stands at the first row of every range after the first, found by
+// walking it through the code lengths once (the int4 value picks the table, the
+// next 11 bits the length nibble; a nibble of 15 is an 11-bit ESC code and 16
+// raw bits). One workgroup per bucket to split; lane t walks substream t, whose
+// element (row r, block p) is column c0 + t + 1024 p of the bucket's row r. A row
+// index or table id out of range stops the walk and marks the job failed (the
+// plan then keeps the bucket whole, and its decode reports them).
+struct AwqSplitJob {
+  int32_t tensor, bucket, P, rows;
+  int32_t c0, range_rows, ranges, pad;
+  int64_t out;  // first u32 of the job's checkpoints: [ranges - 1][1024]
+};
+
+__global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tensor *__restrict__ tensors,
+                                                             const AwqSplitJob *__restrict__ jobs,
+                                                             uint32_t *__restrict__ ckpt,
+                                                             uint32_t *__restrict__ failed) {
+  __shared__ int32_t s_gid[16];
+  __shared__ uint8_t s_lens[16 * kAwqPacked];  // packed length nibbles of each int4 value's table
+  const AwqSplitJob J = jobs[blockIdx.x];
+  const mps_awq_tensor &T = tensors[J.tensor];
+  const int tid = threadIdx.x;
+  if (tid < 16) {
+    int32_t g = T.bucket_table[(int64_t)J.bucket * 16 + tid];
+    if (g < -1 || g >= T.num_tables) {
+      failed[blockIdx.x] = 1u;
+      g = -1;
+    }
+    s_gid[tid] = g;
+  }
+  __syncthreads();
+  for (int i = tid; i < 16 * kAwqPacked; i += kAwqBlock) {
+    const int32_t g = s_gid[i / kAwqPacked];
+    s_lens[i] = g >= 0 ? T.decode_lens[(int64_t)g * kAwqPacked + i % kAwqPacked] : 0xFFu;  // missing: all ESC
+  }
+  __syncthreads();
+  const bool empty = T.bitstream_words <= 0;
+  const uint32_t *__restrict__ bs32 = empty ? g_awq_zero_chunks : reinterpret_cast<const uint32_t *>(T.bitstream);
+  const uint64_t nchunks = empty ? 2u : (uint64_t)T.bitstream_words * 2u;
+  const uint64_t bit_base = (uint64_t)T.bucket_bit_base[J.bucket];
+  const int32_t ra = T.bucket_row_offsets[J.bucket];
+  uint64_t pos = bit_base + T.bucket_thread_startbit[(int64_t)J.bucket * (kAwqBlock + 1) + tid];
+  uint64_t cidx = ~0ull;
+  uint32_t ca = 0, cb = 0;
+  for (int j = 1; j < J.ranges; ++j) {
+    for (int32_t r = (j - 1) * J.range_rows; r < j * J.range_rows; ++r) {
+      const int32_t row = T.row_indices[ra + r];
+      if (row < 0 || row >= T.n) {
+        failed[blockIdx.x] = 1u;
+        return;
+      }
+      const uint8_t *qrow = T.int4 + (int64_t)row * T.m + J.c0 + tid;
+      for (int32_t p = 0; p < J.P; ++p) {
+        const uint32_t q = qrow[(int64_t)p * kAwqBlock] & 15u;
+        const uint64_t c = pos >> 5;
+        if (c != cidx) {
+          cidx = c;
+          ca = chunk_at(bs32, nchunks, c);
+          cb = chunk_at(bs32, nchunks, c + 1);
+        }
+        const uint32_t peek = (uint32_t)(((((uint64_t)ca << 32) | cb) << (pos & 31u)) >> (64 - kAwqL));
+        const uint32_t nib = (s_lens[q * kAwqPacked + (peek >> 1)] >> ((peek & 1u) * 4u)) & 0xFu;
+        pos += nib == 15u ? (uint64_t)kAwqEscLow : (uint64_t)nib;
+      }
+    }
+    ckpt[J.out + (int64_t)(j - 1) * kAwqBlock + tid] = (uint32_t)(pos - bit_base);
+  }
+}
+
 // Plan launch: workgroup i decodes buckets work[i].y .. work[i].y + work[i].z - 1
 // of tensor work[i].x; work[i].w = 1 marks one slab-path bucket (above). A
 // record's buckets have identical table ids (one scale),
@@ -815,15 +916,17 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, int64_t
 // out_delta: elements every tensor's output moves by (a plan decoding into a
 // buffer laid out like, but other than, the one it was created with).
 __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
-                                                             const int4 *__restrict__ work, uint32_t *status,
+                                                             const AwqWork *__restrict__ work,
+                                                             const uint32_t *__restrict__ ckpt, uint32_t *status,
                                                              int64_t out_delta) {
   __shared__ uint32_t lut[kLutEntries];
   __shared__ uint32_t s_base[kRowSlots];
-  const int4 w = work[blockIdx.x];
+  const AwqWork wk = work[blockIdx.x];
+  const int4 w = make_int4(wk.tensor, wk.bucket, wk.nsub, wk.kind);
   mps_awq_tensor T = tensors[w.x];
   T.out += out_delta;
-  if (w.w == 1) {
-    awq_slab_bucket(T, w.y, lut, s_base, status);
+  if (wk.kind != 0) {
+    awq_slab_bucket(T, wk, ckpt, lut, s_base, status);
     return;
   }
   const int nsub = w.z;
@@ -927,8 +1030,8 @@ int check_awq(const mps_awq_tensor *t) {
 
 using namespace mps;
 
-// A plan owns one device allocation: its status word, the tensor descriptors
-// and the work records {tensor, first bucket, buckets, 0}.
+// A plan owns one device allocation: its status word, the tensor descriptors,
+// the work records, and the split jobs and lane checkpoints of its row ranges.
 struct mps_awq_plan {
   int device = 0;
   int64_t count = 0, nwork = 0;
@@ -936,7 +1039,9 @@ struct mps_awq_plan {
   void *d_block = nullptr;
   uint32_t *d_status = nullptr;
   mps_awq_tensor *d_tensors = nullptr;
-  int4 *d_work = nullptr;
+  AwqWork *d_work = nullptr;
+  uint32_t *d_ckpt = nullptr;  // lane checkpoints of the row buckets split into ranges
+  int64_t splits = 0;          // row buckets split into ranges
 };
 
 extern "C" {
@@ -974,14 +1079,19 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // The sidecars may still be being written by work on the caller's stream.
   MPS_HIP_CHECK(hipStreamSynchronize(st));
-  // Work records: runs of up to 1024 / k consecutive buckets of one tensor with
-  // identical table ids (one scale) and at most kRowSlots / 4 rows each, so
-  // they can share a workgroup's tables; ordered by elements, largest first,
-  // so the launch's last workgroups are its smallest.
-  std::vector<std::pair<int64_t, int4>> items;
+  int dev = 0, cus = 0;
+  MPS_HIP_CHECK(hipGetDevice(&dev));
+  MPS_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  // Work records (AwqWork). Slab-eligible buckets get one record each (kind 1);
+  // the others run in runs of up to 1024 / k consecutive buckets of one tensor
+  // with identical table ids (one scale) and at most kRowSlots / 4 rows each, so
+  // they can share a workgroup's tables (kind 0).
+  std::vector<AwqWork> base;
   std::vector<int32_t> roff, clen, cst, btab, gcol;
+  std::vector<int32_t> rows_of_rec, p_of_rec, c0_of_rec;  // row-layout slab records: rows, P, column start
   const char *slab_env = std::getenv("MPSERVE_AWQ_SLAB");
   const bool slab_on = !(slab_env && slab_env[0] == '0');
+  int64_t total = 0;
   for (int64_t i = 0; i < count; ++i) {
     const mps_awq_tensor &T = tensors[i];
     int rc = check_awq(&T);
@@ -1020,6 +1130,7 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     const int64_t row_cap = kRowSlots / 4;
     int64_t b = 0;
     while (b < B) {
+      total += elems_of(b);
       // (cst holds the column starts only for a slab-eligible row-layout tensor)
       const bool slab_shape =
           slab_tensor &&
@@ -1029,7 +1140,10 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
                      clen[(size_t)b] % kAwqBlock == 0 && cst[(size_t)b] >= 0 && (cst[(size_t)b] & 3) == 0 &&
                      (int64_t)cst[(size_t)b] + clen[(size_t)b] <= T.m);
       if (slab_shape && roff[(size_t)b] >= 0 && roff[(size_t)b + 1] <= T.num_row_indices) {
-        items.push_back({elems_of(b), make_int4((int)i, (int)b, 1, 1)});
+        base.push_back(AwqWork{(int32_t)i, (int32_t)b, 1, 1, 0, 0, 1, 0, 0, elems_of(b)});
+        rows_of_rec.push_back(T.group_col_start ? 0 : (int32_t)rows_of(b));
+        p_of_rec.push_back(T.group_col_start ? 0 : clen[(size_t)b] / kAwqBlock);
+        c0_of_rec.push_back(T.group_col_start ? 0 : cst[(size_t)b]);
         ++b;
         continue;
       }
@@ -1038,41 +1152,107 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
         while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap &&
                std::equal(btab.begin() + b * 16, btab.begin() + b * 16 + 16, btab.begin() + (b + nsub) * 16)) {
           elems += elems_of(b + nsub);
+          total += elems_of(b + nsub);
           ++nsub;
         }
       }
-      items.push_back({elems, make_int4((int)i, (int)b, (int)nsub, 0)});
+      base.push_back(AwqWork{(int32_t)i, (int32_t)b, (int32_t)nsub, 0, 0, 0, 1, 0, 0, elems});
+      rows_of_rec.push_back(0);
+      p_of_rec.push_back(0);
+      c0_of_rec.push_back(0);
       b += nsub;
     }
   }
-  std::stable_sort(items.begin(), items.end(),
-                   [](const std::pair<int64_t, int4> &x, const std::pair<int64_t, int4> &y) { return x.first > y.first; });
+  // Row ranges: a slab-path row bucket with more than total / (2 * CUs) elements
+  // is split into row ranges of at least 64 elements a lane, each started from
+  // lane checkpoints that one walk over the bucket's substreams finds.
+  const int64_t target = std::max<int64_t>(1, total / (2 * (int64_t)std::max(cus, 1)));
+  std::vector<AwqSplitJob> jobs;
+  std::vector<size_t> job_rec;  // the base record each job splits
+  int64_t ck_words = 0;
+  for (size_t r = 0; r < base.size(); ++r) {
+    const AwqWork &w = base[r];
+    const int32_t rows = rows_of_rec[r], P = p_of_rec[r];
+    if (w.kind != 1 || rows < 2 || w.elems <= target) continue;
+    const int64_t want = (w.elems + target - 1) / target;
+    int32_t rr = (int32_t)((rows + want - 1) / want);
+    rr = std::max<int32_t>(rr, (64 + P - 1) / P);
+    const int32_t ranges = (rows + rr - 1) / rr;
+    if (ranges < 2) continue;
+    jobs.push_back(AwqSplitJob{w.tensor, w.bucket, P, rows, c0_of_rec[r], rr, ranges, 0, ck_words});
+    job_rec.push_back(r);
+    ck_words += (int64_t)(ranges - 1) * kAwqBlock;
+  }
+  auto make_records = [&](const std::vector<uint32_t> &failed) {
+    std::vector<AwqWork> out;
+    std::vector<int> split_of(base.size(), -1);
+    for (size_t j = 0; j < jobs.size(); ++j)
+      if (failed.empty() || failed[j] == 0u) split_of[job_rec[j]] = (int)j;
+    for (size_t r = 0; r < base.size(); ++r) {
+      if (split_of[r] < 0) {
+        out.push_back(base[r]);
+        continue;
+      }
+      const AwqSplitJob &J = jobs[(size_t)split_of[r]];
+      for (int32_t g = 0; g < J.ranges; ++g) {
+        const int32_t nrows = std::min(J.range_rows, J.rows - g * J.range_rows);
+        out.push_back(AwqWork{J.tensor, J.bucket, 1, 2, g, J.range_rows, J.ranges, 0, J.out,
+                              (int64_t)nrows * J.P * kAwqBlock});
+      }
+    }
+    // largest first, so the launch's last workgroups are its smallest
+    std::stable_sort(out.begin(), out.end(), [](const AwqWork &x, const AwqWork &y) { return x.elems > y.elems; });
+    return out;
+  };
+  std::vector<AwqWork> items = make_records({});
   auto plan = new (std::nothrow) mps_awq_plan();
   if (!plan) return fail(MPS_ERR_NO_MEMORY, "out of memory");
-  MPS_HIP_CHECK(hipGetDevice(&plan->device));
+  plan->device = dev;
   plan->count = count;
   plan->nwork = (int64_t)items.size();
   plan->first_out = count > 0 ? tensors[0].out : nullptr;
-  // status word (zero) | descriptors | work records: one allocation, one copy
+  // status word (zero) | descriptors | work records | split jobs | checkpoints | job failure flags
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
   const size_t o_tensors = 256;
-  const size_t o_work = o_tensors + ((sizeof(mps_awq_tensor) * (size_t)count + 255) & ~(size_t)255);
-  std::vector<char> host(o_work + sizeof(int4) * items.size(), 0);
+  const size_t o_work = o_tensors + up(sizeof(mps_awq_tensor) * (size_t)count);
+  const size_t o_jobs = o_work + up(sizeof(AwqWork) * items.size());
+  const size_t o_ckpt = o_jobs + up(sizeof(AwqSplitJob) * jobs.size());
+  const size_t o_failed = o_ckpt + up(sizeof(uint32_t) * (size_t)ck_words);
+  std::vector<char> host(o_failed + up(sizeof(uint32_t) * jobs.size()), 0);
   if (count > 0) std::memcpy(host.data() + o_tensors, tensors, sizeof(mps_awq_tensor) * (size_t)count);
-  for (size_t j = 0; j < items.size(); ++j)
-    std::memcpy(host.data() + o_work + j * sizeof(int4), &items[j].second, sizeof(int4));
+  if (!items.empty()) std::memcpy(host.data() + o_work, items.data(), sizeof(AwqWork) * items.size());
+  if (!jobs.empty()) std::memcpy(host.data() + o_jobs, jobs.data(), sizeof(AwqSplitJob) * jobs.size());
   hipError_t e = hipMalloc(&plan->d_block, host.size());
   if (e == hipSuccess) {
     char *blk = static_cast<char *>(plan->d_block);
     plan->d_status = reinterpret_cast<uint32_t *>(blk);
     plan->d_tensors = reinterpret_cast<mps_awq_tensor *>(blk + o_tensors);
-    plan->d_work = reinterpret_cast<int4 *>(blk + o_work);
+    plan->d_work = reinterpret_cast<AwqWork *>(blk + o_work);
+    plan->d_ckpt = reinterpret_cast<uint32_t *>(blk + o_ckpt);
     e = hipMemcpyAsync(blk, host.data(), host.size(), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && !jobs.empty()) {
+      hipLaunchKernelGGL(awq_checkpoints, dim3((unsigned)jobs.size()), dim3(kAwqBlock), 0, st, plan->d_tensors,
+                         reinterpret_cast<const AwqSplitJob *>(blk + o_jobs), plan->d_ckpt,
+                         reinterpret_cast<uint32_t *>(blk + o_failed));
+      e = hipGetLastError();
+      std::vector<uint32_t> failed(jobs.size(), 0u);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(failed.data(), blk + o_failed, sizeof(uint32_t) * jobs.size(), hipMemcpyDeviceToHost, st);
+      if (e == hipSuccess) e = hipStreamSynchronize(st);
+      if (e == hipSuccess && std::any_of(failed.begin(), failed.end(), [](uint32_t f) { return f != 0u; })) {
+        // keep the buckets whose walk failed whole (fewer records than before)
+        items = make_records(failed);
+        plan->nwork = (int64_t)items.size();
+        e = hipMemcpyAsync(blk + o_work, items.data(), sizeof(AwqWork) * items.size(), hipMemcpyHostToDevice, st);
+      }
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
   }
   if (e != hipSuccess) {
     mps_awq_plan_destroy(plan);
     return hip_fail(e, "mps_awq_plan_create");
   }
+  plan->splits = (int64_t)jobs.size();
   *plan_out = plan;
   return MPS_OK;
 }
@@ -1080,7 +1260,8 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
 static int awq_plan_launch(mps_awq_plan *plan, int64_t out_delta, uint32_t *status, void *stream) {
   if (plan->nwork == 0) return MPS_OK;
   hipLaunchKernelGGL(awq_decode_plan, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, status, out_delta);
+                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_ckpt, status,
+                     out_delta);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }

@@ -312,7 +312,9 @@ def test_plan_slab_path_matches_input_and_the_lane_path(by_scale, n, m, cap, see
     over P >= 4 blocks of 1024 columns (P % 4 == 0, or a step straddling two rows).
     Bit-exact to the input, equal to the per-lane path's output, status clean. The
     cases hold ESC keys, partial last slabs (by-scale group counts not a multiple
-    of 8) and partial last steps (per-lane counts not a multiple of 4)."""
+    of 8) and partial last steps (per-lane counts not a multiple of 4); the row
+    buckets of a lone tensor are split into row ranges started from lane
+    checkpoints."""
     print(f"[awq] slab path {'by-scale' if by_scale else 'rows'} {n}x{m} cap {cap}", flush=True)
     w = make_awq_weight(n, m, 128 if by_scale else None, seed=seed, device=DEV)
     sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, 1024, cap, by_scale, with_stats=True)
@@ -330,6 +332,9 @@ def test_plan_slab_path_matches_input_and_the_lane_path(by_scale, n, m, cap, see
         monkeypatch.setenv("MPSERVE_AWQ_SLAB", slab)
         out = torch.empty((n, m), dtype=torch.bfloat16, device=DEV)
         plan = awq.AwqDecodePlan([(w.int4_u8, sc, out)])
+        if slab == "1" and not by_scale:
+            # a lone tensor's row buckets exceed total / (2 CUs): split into row ranges
+            assert plan.info()["work_items"] > sc["bucket_table_i32"].shape[0]
         plan.read_status()
         for _ in range(2):
             out.zero_()
