@@ -676,6 +676,8 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
 // and end bits; (2) the tables' slices and the lane's first bitstream words.
 // Thread tid expands entries 32c .. 32c+31 of the table of int4 value tid / 64
 // (c = tid % 64).
+// kRanged: a row range (kind 2); whole buckets compile without the range logic.
+template <bool kRanged>
 __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const AwqWork &wk,
                                                 const uint32_t *__restrict__ ckpt, uint32_t *__restrict__ lut,
                                                 uint32_t *__restrict__ region, uint32_t *status) {
@@ -697,7 +699,7 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   }
   const uint32_t P = by_scale ? 0u : (uint32_t)cl / (uint32_t)kAwqBlock;
   // a row range (kind 2): its first row and row count; its lanes start and end at checkpoints
-  const bool ranged = wk.kind == 2 && !by_scale;
+  const bool ranged = kRanged && !by_scale;
   const int32_t first_row = ranged ? wk.range * wk.range_rows : 0;
   const int32_t nr = ranged ? (groups - first_row < wk.range_rows ? groups - first_row : wk.range_rows) : groups;
   if (nr <= 0) {
@@ -721,13 +723,15 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const __amdgpu_buffer_rsrc_t r_sb = awq_rsrc(T.bucket_thread_startbit + b * (kAwqBlock + 1), (kAwqBlock + 1) * 4u);
   const __amdgpu_buffer_rsrc_t r_ck =
       awq_rsrc(ranged ? ckpt + wk.ckpt : nullptr, ranged ? (uint32_t)(wk.ranges - 1) * (uint32_t)kAwqBlock * 4u : 0u);
+  // one unconditional load each from the chosen array (a load under a branch is
+  // waited for where the branch joins, which would serialise the set-up's loads)
   const bool from_ck = ranged && wk.range > 0, to_ck = ranged && wk.range + 1 < wk.ranges;
-  const uint32_t pos = from_ck ? __builtin_amdgcn_raw_buffer_load_b32(
-                                     r_ck, ((uint32_t)(wk.range - 1) * (uint32_t)kAwqBlock + t) * 4u, 0, 0)
-                               : __builtin_amdgcn_raw_buffer_load_b32(r_sb, t * 4u, 0, 0);
-  const uint32_t pos_end = to_ck ? __builtin_amdgcn_raw_buffer_load_b32(
-                                       r_ck, ((uint32_t)wk.range * (uint32_t)kAwqBlock + t) * 4u, 0, 0)
-                                 : __builtin_amdgcn_raw_buffer_load_b32(r_sb, (t + 1u) * 4u, 0, 0);
+  const __amdgpu_buffer_rsrc_t r_pos = from_ck ? r_ck : r_sb;
+  const __amdgpu_buffer_rsrc_t r_end = to_ck ? r_ck : r_sb;
+  const uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(
+      r_pos, from_ck ? ((uint32_t)(wk.range - 1) * (uint32_t)kAwqBlock + t) * 4u : t * 4u, 0, 0);
+  const uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(
+      r_end, to_ck ? ((uint32_t)wk.range * (uint32_t)kAwqBlock + t) * 4u : (t + 1u) * 4u, 0, 0);
   const uint64_t bucket_bit = (uint64_t)T.bucket_bit_base[b];
   // level 2
   const bool tab_ok = gq >= 0 && gq < T.num_tables;
@@ -915,6 +919,10 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
 // workgroup per CU).
 // out_delta: elements every tensor's output moves by (a plan decoding into a
 // buffer laid out like, but other than, the one it was created with).
+// kRanges: the plan has row ranges (kind 2 records). Plans without them launch
+// the instantiation that leaves the range path out: its code in the same kernel
+// measured 4.6% slower on a by-scale layer.
+template <bool kRanges>
 __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
                                                              const AwqWork *__restrict__ work,
                                                              const uint32_t *__restrict__ ckpt, uint32_t *status,
@@ -925,9 +933,15 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tenso
   const int4 w = make_int4(wk.tensor, wk.bucket, wk.nsub, wk.kind);
   mps_awq_tensor T = tensors[w.x];
   T.out += out_delta;
-  if (wk.kind != 0) {
-    awq_slab_bucket(T, wk, ckpt, lut, s_base, status);
+  if (wk.kind == 1) {
+    awq_slab_bucket<false>(T, wk, ckpt, lut, s_base, status);
     return;
+  }
+  if constexpr (kRanges) {
+    if (wk.kind == 2) {
+      awq_slab_bucket<true>(T, wk, ckpt, lut, s_base, status);
+      return;
+    }
   }
   const int nsub = w.z;
   const int per = kAwqBlock / nsub;
@@ -1042,6 +1056,7 @@ struct mps_awq_plan {
   AwqWork *d_work = nullptr;
   uint32_t *d_ckpt = nullptr;  // lane checkpoints of the row buckets split into ranges
   int64_t splits = 0;          // row buckets split into ranges
+  bool has_ranges = false;     // some work record is a row range (kind 2)
 };
 
 extern "C" {
@@ -1253,15 +1268,21 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     return hip_fail(e, "mps_awq_plan_create");
   }
   plan->splits = (int64_t)jobs.size();
+  plan->has_ranges = std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.kind == 2; });
   *plan_out = plan;
   return MPS_OK;
 }
 
 static int awq_plan_launch(mps_awq_plan *plan, int64_t out_delta, uint32_t *status, void *stream) {
   if (plan->nwork == 0) return MPS_OK;
-  hipLaunchKernelGGL(awq_decode_plan, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_ckpt, status,
-                     out_delta);
+  if (plan->has_ranges)
+    hipLaunchKernelGGL(awq_decode_plan<true>, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
+                       reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_ckpt, status,
+                       out_delta);
+  else
+    hipLaunchKernelGGL(awq_decode_plan<false>, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
+                       reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_ckpt, status,
+                       out_delta);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
