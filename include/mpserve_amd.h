@@ -109,7 +109,7 @@ int mps_fp8_plan_read_status(mps_fp8_plan *plan, void *stream, uint32_t *status_
 int mps_fp8_plan_destroy(mps_fp8_plan *plan);
 
 /* Allocation-free batched decode: decodes `count` tensors (at most 1024, with
- * at most 63,104 buckets in all) in one persistent launch, as a plan would,
+ * at most 63,100 buckets in all) in one persistent launch, as a plan would,
  * but without creating one. It calls no hipMalloc, hipFree or other
  * allocating routine and does not synchronise: the descriptors (read from the
  * host array before the call returns) and one work record per bucket go into

@@ -1077,8 +1077,13 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
   return w;
 }
 
+// kQueue: the work item also takes the ticket of the workgroup's next one
+// from the launch's work counter (queue[0]), at the start of its set-up, so
+// that the atomic's round trip overlaps the set-up's loads; every thread
+// gets it in `ticket` (zero without kQueue).
+template <bool kQueue>
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t *out, const WorkItem &w,
-                                              uint32_t *lds, uint32_t *status) {
+                                              uint32_t *lds, uint32_t *status, uint32_t *queue, uint32_t &ticket) {
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
@@ -1115,6 +1120,14 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   constexpr int kSlices = 256 * (kTable / 8) / kBlock;  // 4
   const bool rows_fast = k1024 || fast;
   const int wl = lane & 63;
+  // The ticket: a buffer atomic that only thread 0 addresses in range (the
+  // others' are dropped), so no branch holds the set-up's loads behind it.
+  uint32_t tk = 0;
+  if (kQueue) {
+    const __amdgpu_buffer_rsrc_t r_q = make_rsrc(queue, 4u);
+    tk = (uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, r_q, tid == 0 ? 0u : kBsPast, 0, 0);
+    tk = tid == 0 ? tk : 0u;
+  }
   const __amdgpu_buffer_rsrc_t r_ids = make_rsrc(w.table_ids, 256u * 4u);
   const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(w.row_idx, rows_fast ? (uint32_t)rows * 4u : 0u);
   const __amdgpu_buffer_rsrc_t r_sb = make_rsrc(sb, rows_fast ? (uint32_t)k_eff * 4u : 0u);
@@ -1225,16 +1238,19 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     *reinterpret_cast<uint4 *>(tab + (((uint32_t)part * 8u + 4u) ^ lut_spread(qt))) = make_uint4(e[4], e[5], e[6], e[7]);
   }
   // Block-wide ORs of "a row index is out of range" (bit 0) and "a table has an
-  // ESC entry" (bit 1): one word per wave, written by its first lane.
+  // ESC entry" (bit 1): one word per wave, written by its first lane. Wave 0's
+  // word also carries the ticket (bits 2..31).
   {
     const uint32_t wf = (__builtin_amdgcn_ballot_w64(bad_row) ? 1u : 0u) |
                         (__builtin_amdgcn_ballot_w64(esc_seen != 0) ? 2u : 0u);
-    if ((tid & 63) == 0) s_wflag[tid >> 6] = wf;
+    if ((tid & 63) == 0) s_wflag[tid >> 6] = wf | (tk << 2);
   }
   __syncthreads();
   uint32_t bflags = 0;
 #pragma unroll
   for (int w = 0; w < kBlock / 64; ++w) bflags |= s_wflag[w];
+  bflags = uni(bflags);
+  ticket = bflags >> 2;
   const bool has_esc = (bflags & 2u) != 0;
   const bool any_bad_row = (bflags & 1u) != 0;
   __syncthreads();  // the flag words belong to the queue from here on
@@ -1299,33 +1315,56 @@ __device__ __forceinline__ void end_bucket() {
 
 // Both kernels are persistent: one workgroup per CU (the LDS holds one
 // bucket's tables) walks its share of the buckets, so a bucket's set-up does
-// not also pay a workgroup launch. Every workgroup runs the same uniform loop
-// to its end.
+// not also pay a workgroup launch. fp8_decode_one deals the buckets
+// round-robin; every workgroup runs the same uniform loop to its end.
 __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
+  uint32_t ticket;
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
-    decode_bucket(T, T.out, bucket_item(T, b), lds, status);
+    decode_bucket<false>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket);
     end_bucket();
   }
 }
 
+// fp8_decode_plan takes its work items from a queue: workgroup g starts with
+// item g; each item's set-up takes a ticket t from queue[0], and the
+// workgroup's next item is gridDim.x + t. The items are sorted largest first,
+// so the CUs that drew small items or ran fast take more of them, and all
+// finish close together (a fixed deal would leave the CUs with the larger
+// shares running alone at the end). The last workgroup to leave (queue[1]
+// counts them) puts both words back to zero for the next launch: launches of
+// one queue must not overlap.
+//
 // out_delta: elements every tensor's output moves by (a plan decoding into a
 // buffer laid out like, but other than, the one it was created with).
+//
+// Tickets travel in 30 bits of the set-up's flag words: a launch holds fewer
+// than kMaxQueueItems work items.
+constexpr int64_t kMaxQueueItems = (int64_t(1) << 30) - 65536;
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
                                                           const WorkItem *__restrict__ work, int64_t nwork,
-                                                          uint32_t *status, int64_t out_delta) {
+                                                          uint32_t *status, int64_t out_delta, uint32_t *queue) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
-  if ((int64_t)blockIdx.x >= nwork) return;
-  // The next bucket's record (scalar registers) is loaded with this bucket's
-  // set-up, so the next set-up starts one round trip shorter.
-  WorkItem w = work[blockIdx.x];
-  for (int64_t i = blockIdx.x; i < nwork; i += gridDim.x) {
-    const int64_t inext = i + gridDim.x;
-    const WorkItem wn = work[inext < nwork ? inext : i];
-    const mps_fp8_tensor &T = tensors[w.tensor];
-    decode_bucket(T, T.out + out_delta, w, lds, status);
-    end_bucket();
-    w = wn;
+  if ((int64_t)blockIdx.x < nwork) {
+    WorkItem w = work[blockIdx.x];
+    for (;;) {
+      uint32_t ticket;
+      const mps_fp8_tensor &T = tensors[w.tensor];
+      decode_bucket<true>(T, T.out + out_delta, w, lds, status, queue, ticket);
+      const int64_t next = (int64_t)gridDim.x + ticket;
+      // The next record (scalar registers) is loaded before the drain of this
+      // item's stores, which covers its round trip.
+      const WorkItem wn = work[next < nwork ? next : 0];
+      end_bucket();
+      if (next >= nwork) break;
+      w = wn;
+    }
+  }
+  if (threadIdx.x == 0) {
+    if (atomicAdd(queue + 1, 1u) == gridDim.x - 1) {
+      atomicExch(queue, 0u);
+      atomicExch(queue + 1, 0u);
+    }
   }
 }
 
@@ -1430,12 +1469,15 @@ __global__ __launch_bounds__(kBlock) void fp8_checkpoints(const mps_fp8_tensor *
 // (that needs lane checkpoints, which a plan computes once).
 //
 // Layout of `scratch`: the descriptors (at most kMaxBatchTensors), then one
-// 64-byte work record per bucket (at most kMaxBatchWork).
+// 64-byte work record per bucket (at most kMaxBatchWork), then the decode
+// launch's queue words in the last 256 bytes (zero from module load; each
+// launch leaves them zero).
 // ---------------------------------------------------------------------------
 constexpr size_t kScratchBytes = size_t(4) << 20;
 constexpr int64_t kMaxBatchTensors = 1024;
 constexpr size_t kBatchWorkOff = ((sizeof(mps_fp8_tensor) * kMaxBatchTensors + 255) / 256) * 256;
-constexpr int64_t kMaxBatchWork = (int64_t)((kScratchBytes - kBatchWorkOff) / sizeof(WorkItem));
+constexpr size_t kBatchQueueOff = kScratchBytes - 256;
+constexpr int64_t kMaxBatchWork = (int64_t)((kBatchQueueOff - kBatchWorkOff) / sizeof(WorkItem));
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -1584,6 +1626,11 @@ using namespace mps;
 
 namespace {
 constexpr size_t kAlign = 256;
+constexpr size_t kQueueOff = 64;
+// A work item's set-up (tables into the LDS, the lanes' first loads, the
+// pipeline's fill and drain) costs about as long as decoding this many
+// elements; plans weigh items by their elements plus this.
+constexpr int64_t kItemSetup = 65536;
 size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 }  // namespace
 
@@ -1593,6 +1640,7 @@ size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 struct mps_fp8_plan {
   void *d_block = nullptr;
   uint32_t *d_status = nullptr;
+  uint32_t *d_queue = nullptr;  // the decode launch's work counter and exit count (zero between launches)
   mps_fp8_tensor *d_tensors = nullptr;
   WorkItem *d_work = nullptr;
   uint16_t *first_out = nullptr;  // the first tensor's output at creation (decode_into moves all by one offset)
@@ -1692,20 +1740,80 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   // split into row ranges of at most that size (and at least 64 elements per
   // substream, 16 groups, so that a range's set-up stays small beside its
   // decode). Each range starts from lane checkpoints (fp8_checkpoints).
+  //
+  // Then the tail. The launch's queue hands the items out largest first
+  // (fp8_decode_plan), and an item handed out when R elements of work remain
+  // (it and the items after it) can end up to about its size minus R / CUs
+  // after the others. Every item past the first CUs that exceeds
+  // kTailRatio * R / CUs has its bucket split twice as fine, until none does
+  // or none can be. Coarse items keep the set-ups few (each costs about as
+  // much as decoding kItemSetup elements); the fine ones at the end fill the
+  // CUs' last gaps.
+#ifndef MPS_SPLIT_DIV
+#define MPS_SPLIT_DIV 2
+#endif
+#ifndef MPS_TAIL_RATIO
+#define MPS_TAIL_RATIO 3
+#endif
+  constexpr int64_t kTailRatio = MPS_TAIL_RATIO;
   int64_t total = 0;
   for (int64_t x : elems) total += x;
-  const int64_t cap = std::max<int64_t>(total / (2 * (int64_t)std::max(cus, 1)), 65536);
+  const int64_t ncu = std::max(cus, 1);
+  const int64_t cap = std::max<int64_t>(total / (MPS_SPLIT_DIV * ncu), 65536);
+  std::vector<int64_t> nr(bucket.size(), 1), maxr(bucket.size(), 1);
+  for (size_t i = 0; i < bucket.size(); ++i) {
+    const WorkItem &w = bucket[i];
+    if ((w.path != kPathK1024 && w.path != kPathFast) || w.rows < 2) continue;
+    const int32_t P = w.cl / w.k_eff;
+    const int32_t min_rows = std::max<int32_t>(1, (64 + P - 1) / P);
+    maxr[i] = std::max<int64_t>(1, w.rows / min_rows);
+    if (elems[i] > cap) nr[i] = std::min<int64_t>((elems[i] + cap - 1) / cap, maxr[i]);
+  }
+  {
+    struct Piece {
+      int64_t cost;
+      size_t b;
+    };
+    std::vector<Piece> pieces;
+    std::vector<char> bump(bucket.size());
+    for (int iter = 0; iter < 64; ++iter) {
+      pieces.clear();
+      for (size_t i = 0; i < bucket.size(); ++i) {
+        const int64_t rows = bucket[i].rows;
+        const int64_t rr = nr[i] > 1 ? (rows + nr[i] - 1) / nr[i] : rows;
+        if (nr[i] <= 1 || rr <= 0) {
+          pieces.push_back({elems[i] + kItemSetup, i});
+          continue;
+        }
+        for (int64_t r0 = 0; r0 < rows; r0 += rr)
+          pieces.push_back({std::min(rr, rows - r0) * bucket[i].cl + kItemSetup, i});
+      }
+      std::stable_sort(pieces.begin(), pieces.end(), [](const Piece &a, const Piece &c) { return a.cost > c.cost; });
+      std::fill(bump.begin(), bump.end(), 0);
+      bool changed = false;
+      int64_t rest = 0;
+      for (size_t q = pieces.size(); q-- > 0;) {
+        rest += pieces[q].cost;
+        const size_t b = pieces[q].b;
+        if ((int64_t)q < ncu || bump[b] || nr[b] >= maxr[b]) continue;
+        if ((double)pieces[q].cost * (double)ncu > (double)kTailRatio * (double)rest) {
+          bump[b] = 1;
+          nr[b] = std::min(maxr[b], nr[b] * 2);
+          changed = true;
+        }
+      }
+      if (!changed) break;
+    }
+  }
   std::vector<SplitJob> jobs;
   std::vector<size_t> job_of(bucket.size(), SIZE_MAX);
   int64_t ck_words = 0, max_items = 0;
   for (size_t i = 0; i < bucket.size(); ++i) {
     const WorkItem &w = bucket[i];
     ++max_items;
-    if ((w.path != kPathK1024 && w.path != kPathFast) || elems[i] <= cap || w.rows < 2) continue;
+    if (nr[i] < 2) continue;
     const int32_t P = w.cl / w.k_eff;
-    const int32_t min_rows = std::max<int32_t>(1, (64 + P - 1) / P);
-    int64_t ranges = std::min<int64_t>((elems[i] + cap - 1) / cap, w.rows / min_rows);
-    if (ranges < 2) continue;
+    int64_t ranges = nr[i];
     const int32_t range_rows = (int32_t)((w.rows + ranges - 1) / ranges);
     ranges = (w.rows + range_rows - 1) / range_rows;
     if (ranges < 2) continue;
@@ -1728,7 +1836,10 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
     max_items += ranges - 1;
   }
 
-  // The plan's device block.
+  // The plan's device block: the status word at 0 and the queue at kQueueOff
+  // in the first kAlign bytes, then the descriptors, checkpoints, split jobs,
+  // their flags and the work records.
+  if (max_items >= kMaxQueueItems) return fail(MPS_ERR_INVALID_ARGUMENT, "too many work items for one plan");
   const size_t o_tensors = kAlign;
   const size_t o_ckpt = o_tensors + align_up(sizeof(mps_fp8_tensor) * (size_t)count);
   const size_t o_jobs = o_ckpt + align_up(sizeof(uint32_t) * (size_t)ck_words);
@@ -1753,10 +1864,11 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   };
   char *blk = static_cast<char *>(p->d_block);
   p->d_status = reinterpret_cast<uint32_t *>(blk);
+  p->d_queue = reinterpret_cast<uint32_t *>(blk + kQueueOff);
   p->d_tensors = reinterpret_cast<mps_fp8_tensor *>(blk + o_tensors);
   p->d_work = reinterpret_cast<WorkItem *>(blk + o_work);
   uint32_t *d_ckpt = reinterpret_cast<uint32_t *>(blk + o_ckpt);
-  // Status word (zero), descriptors, jobs and their flags (zero): one copy, on the caller's stream.
+  // Status word and queue (zero), descriptors, jobs and their flags (zero): one copy, on the caller's stream.
   std::vector<char> head(o_work, 0);
   if (count > 0) std::memcpy(head.data() + o_tensors, tensors, sizeof(mps_fp8_tensor) * (size_t)count);
   if (!jobs.empty()) std::memcpy(head.data() + o_jobs, jobs.data(), sizeof(SplitJob) * jobs.size());
@@ -1773,16 +1885,16 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   if (e != hipSuccess) return cleanup(e);
 
-  // Work items (buckets and ranges), largest first: the persistent launch
-  // deals them round-robin to the CUs, which then finish at about the same
-  // time. An item's cost is its element count plus a fixed set-up share.
+  // Work items (buckets and ranges), largest first, the order in which the
+  // launch's queue hands them out. An item's cost is its element count plus
+  // kItemSetup.
   std::vector<WorkItem> work;
   std::vector<int64_t> cost;
   for (size_t i = 0; i < bucket.size(); ++i) {
     const WorkItem &w = bucket[i];
     if (job_of[i] == SIZE_MAX || failed[job_of[i]]) {
       work.push_back(w);
-      cost.push_back(elems[i] + 65536);
+      cost.push_back(elems[i] + kItemSetup);
       continue;
     }
     const SplitJob &j = jobs[job_of[i]];
@@ -1794,7 +1906,7 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
       x.startbits = r == 0 ? w.startbits : ck + (int64_t)(r - 1) * j.K;
       x.endbits = r + 1 == j.ranges ? w.endbits : ck + (int64_t)r * j.K;
       work.push_back(x);
-      cost.push_back((int64_t)x.rows * w.cl + 65536);
+      cost.push_back((int64_t)x.rows * w.cl + kItemSetup);
     }
   }
   {
@@ -1822,7 +1934,7 @@ int plan_launch(mps_fp8_plan *plan, int64_t out_delta, uint32_t *status, void *s
   const int rc = persistent_grid(plan->work_items, &grid);
   if (rc != MPS_OK) return rc;
   hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                     plan->d_tensors, plan->d_work, plan->work_items, status, out_delta);
+                     plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, plan->d_queue);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
@@ -1918,7 +2030,7 @@ int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, i
   rc = persistent_grid(total, &grid);
   if (rc != MPS_OK) return rc;
   hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, st, d_tensors, d_work, total, status,
-                     (int64_t)0);
+                     (int64_t)0, reinterpret_cast<uint32_t *>(base + kBatchQueueOff));
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }

@@ -60,6 +60,9 @@ class DecodePlan:
     ``stream`` (default: the current stream), which may still be writing the
     sidecars, and reads their bucket metadata; it allocates the plan's device
     memory. Decodes allocate nothing and flag into the plan's own status word.
+    A decode hands the work items out through a queue in the plan's memory, so
+    two decodes of one plan must not overlap: launch them on one stream (or
+    order their streams), and give each concurrent stream a plan of its own.
     """
 
     def __init__(self, items: Iterable[Tuple[torch.Tensor, Mapping[str, torch.Tensor], torch.Tensor]],

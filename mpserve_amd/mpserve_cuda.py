@@ -176,7 +176,9 @@ class _SidecarPlans:
     launches the plan from then on.
 
     Invalidation rule. An entry is keyed by the device addresses of the FP8
-    tensor and the ten sidecar arrays, with n and m. For each of the eleven
+    tensor and the ten sidecar arrays, with n and m and the stream: a plan's
+    launches share its work queue and must not overlap, so each stream that
+    decodes a sidecar gets a plan of its own. For each of the eleven
     tensors it keeps a weak reference to the tensor's storage and the tensor's
     version counter (dtype views such as int64 -> uint64 share both with the
     tensor they view). It is used only while every storage is alive and no
@@ -210,7 +212,7 @@ class _SidecarPlans:
         ``extra``: further key parts (an AWQ group size)."""
         if self.capacity <= 0 or os.environ.get("MPSERVE_DECODE_PLANS", "1") == "0":
             return None
-        key = (device.index, n, m) + tuple(extra) + tuple(t.data_ptr() for t in tensors)
+        key = (device.index, int(stream), n, m) + tuple(extra) + tuple(t.data_ptr() for t in tensors)
         dropped = []
         try:
             with self._lock:

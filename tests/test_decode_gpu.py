@@ -218,6 +218,46 @@ def test_plan_decodes_many_tensors():
     assert plan.read_status() == 0
 
 
+def test_plan_queue_hands_out_every_item_on_every_launch():
+    """A plan with more work items than twice the CUs: each launch takes the items
+    from a queue in the plan's memory, which the launch's last workgroup resets.
+    Every launch, and every replay of a graph that captured one, decodes all items."""
+    from mpserve_amd.decode import DecodePlan
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    shapes = [(512, 4096, 1024)] * 6 + [(64, 1024, 256)] * 8 + [(300, 700, 512)]
+    items, refs = [], []
+    for i, (n, m, k) in enumerate(shapes):
+        bf, q, sc_u16 = synth(n, m, seed=90 + i)
+        items.append((torch.from_numpy(q).to(DEV), to_torch(oracle.encode(bf, q, sc_u16, 7, k), DEV)))
+        refs.append(bf)
+    outs = [torch.empty((q.shape[0], q.shape[1]), dtype=torch.bfloat16, device=DEV) for q, _ in items]
+    plan = DecodePlan([(q, sc, o) for (q, sc), o in zip(items, outs)])
+    assert plan.info()["work_items"] > 2 * cus
+
+    def check(tag):
+        torch.cuda.synchronize()
+        for j, (o, r) in enumerate(zip(outs, refs)):
+            got = o.view(torch.uint16).cpu().numpy()
+            assert np.array_equal(got, r), f"{tag}: tensor {j}, {(got != r).sum()} mismatches"
+
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        plan.decode()
+        check(f"launch {rep}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.decode()
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        check(f"replay {rep}")
+    assert plan.read_status() == 0
+
+
 def test_integrity_flags_on_corrupt_sidecar():
     """Corrupt lane starts / row indices / table ids are flagged (writes are checked
     against the output's bounds in test_corrupt_sidecar_writes_stay_inside_out)."""
