@@ -360,6 +360,7 @@ constexpr uint32_t kSlabOutPast = 0xFFFFFFF0u;  // BF16 byte offset beyond every
 constexpr uint32_t kSlabInPast = 0x80000000u;   // int4 byte offset beyond every input (n*m < 2^31)
 constexpr int kSlabCacheNT = 2;               // buffer cache-policy bits: non-temporal
 constexpr int kSlabMinGroups = 8, kSlabMaxGroups = 1024;
+constexpr uint32_t kRunTables = 1u << 8;        // run_flags: a run's tables are in the LDS
 static_assert(kSlabQSlots * kAwqBlock <= kRowSlots, "the slab queue lives in the row-offset region");
 
 // Buffer resource over [base, base + bytes): raw buffer loads past the end
@@ -677,13 +678,17 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
 // Thread tid expands entries 32c .. 32c+31 of the table of int4 value tid / 64
 // (c = tid % 64).
 // kRanged: a row range (kind 2); whole buckets compile without the range logic.
+// A by-scale record may hold a run of buckets b with identical table ids: the
+// first that gets past its checks (`tables`) loads and expands the tables and
+// records in run_flags that it did (kRunTables) and whether they have an ESC
+// entry (bit 1); the others reuse both.
 template <bool kRanged>
-__device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const AwqWork &wk,
-                                                const uint32_t *__restrict__ ckpt, uint32_t *__restrict__ lut,
-                                                uint32_t *__restrict__ region, uint32_t *status) {
+__device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const AwqWork &wk, int64_t b, bool tables,
+                                                uint32_t &run_flags, const uint32_t *__restrict__ ckpt,
+                                                uint32_t *__restrict__ lut, uint32_t *__restrict__ region,
+                                                uint32_t *status) {
   int tid;
   __asm__ volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
-  const int64_t b = wk.bucket;
   const bool by_scale = T.group_col_start != nullptr;
   const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
   const int32_t groups = rb - ra;  // groups (by-scale) or rows
@@ -735,6 +740,7 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const uint64_t bucket_bit = (uint64_t)T.bucket_bit_base[b];
   // level 2
   const bool tab_ok = gq >= 0 && gq < T.num_tables;
+  const bool tab_load = tables && tab_ok;
   const uint32_t G = (uint32_t)(T.num_tables > 0 ? T.num_tables : 0);
   const __amdgpu_buffer_rsrc_t r_syms = awq_rsrc(T.decode_syms, G * (uint32_t)(kAwqTable * 2));
   const __amdgpu_buffer_rsrc_t r_lens = awq_rsrc(T.decode_lens, G * (uint32_t)kAwqPacked);
@@ -742,12 +748,12 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const auto x = __builtin_amdgcn_raw_buffer_load_b128(
-        r_syms, tab_ok ? (uint32_t)gq * (uint32_t)(kAwqTable * 2) + (uint32_t)c * 64u + 16u * (uint32_t)i : kSlabBsPast,
+        r_syms, tab_load ? (uint32_t)gq * (uint32_t)(kAwqTable * 2) + (uint32_t)c * 64u + 16u * (uint32_t)i : kSlabBsPast,
         0, 0);
     sv[i] = make_uint4(x[0], x[1], x[2], x[3]);
   }
   const auto ln = __builtin_amdgcn_raw_buffer_load_b128(
-      r_lens, tab_ok ? (uint32_t)gq * (uint32_t)kAwqPacked + (uint32_t)c * 16u : kSlabBsPast, 0, 0);
+      r_lens, tab_load ? (uint32_t)gq * (uint32_t)kAwqPacked + (uint32_t)c * 16u : kSlabBsPast, 0, 0);
   uint2 first[4];
   {
     const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
@@ -763,7 +769,7 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
       first[2 * i + 1] = make_uint2(x[2], x[3]);
     }
   }
-  if (tid == 0) {
+  if (tables && tid == 0) {
     bool bad = false;
 #pragma unroll
     for (int qq = 0; qq < 16; ++qq) {
@@ -775,7 +781,7 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   // expansion: entry p of value q = sym << 16 | (nibble 15 ? 27 : nibble); a
   // missing table is all ESC entries, as the reference decodes it
   uint32_t esc_seen = tab_ok ? 0u : 1u;
-  {
+  if (tables) {
     const uint32_t nib32[4] = {ln[0], ln[1], ln[2], ln[3]};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -815,6 +821,9 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
 #pragma unroll
   for (int i = 0; i < kAwqBlock / 64; ++i) bflags |= s_wflag[i];
   __syncthreads();  // the flag words belong to the queue from here on
+  bflags = awq_uni(bflags);
+  if (tables) run_flags = (bflags & 2u) | kRunTables;
+  else bflags = (bflags & ~2u) | (run_flags & 2u);
   if (bflags & 1u) {
     if (tid == 0) flag(status, MPS_STATUS_BAD_ROW);
     return;
@@ -838,6 +847,77 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
     else MPS_AWQ_SLAB(false, kLayRowsWrap);
   }
 #undef MPS_AWQ_SLAB
+}
+
+// A later bucket of a by-scale run, once the run's tables are in the LDS:
+// each wave sets up and decodes its own part without meeting the others. A
+// lane's queue slots and a wave's group bases are its own, so nothing here
+// needs the workgroup: a wave that ends one bucket starts the next one's
+// loads while the others still decode, and their latency hides behind them.
+// A row or column out of range in a wave's groups flags and skips that
+// wave's part (its groups only).
+__device__ __forceinline__ void awq_slab_bucket_wave(const mps_awq_tensor &T, int64_t b, uint32_t run_flags,
+                                                     const uint32_t *__restrict__ lut,
+                                                     uint32_t *__restrict__ region, uint32_t *status) {
+  int tid;
+  __asm__ volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+  const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
+  const int32_t groups = rb - ra;
+  if (!(groups >= kSlabMinGroups && groups <= kSlabMaxGroups && T.group_size == 128) || ra < 0 ||
+      (int64_t)rb > T.num_row_indices || T.k != kAwqBlock) {
+    if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
+    return;
+  }
+  const uint32_t w = (uint32_t)tid >> 6, wl = (uint32_t)tid & 63u;
+  const uint32_t t = (w << 6) | (((uint32_t)tid & 15u) << 2) | (((uint32_t)tid >> 4) & 3u);  // substream
+  // level 1: this wave's groups 8 wl + w/2 and 8 (wl + 64) + w/2, the lane's start and end bits
+  const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra, (uint32_t)groups * 4u);
+  const __amdgpu_buffer_rsrc_t r_gcol = awq_rsrc(T.group_col_start + ra, (uint32_t)groups * 4u);
+  const uint32_t gi0 = 8u * wl + (w >> 1), gi1 = 8u * (wl + 64u) + (w >> 1);
+  const int32_t row0 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi0 * 4u, 0, 0);
+  const int32_t col0 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi0 * 4u, 0, 0);
+  const int32_t row1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi1 * 4u, 0, 0);
+  const int32_t col1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi1 * 4u, 0, 0);
+  const __amdgpu_buffer_rsrc_t r_sb = awq_rsrc(T.bucket_thread_startbit + b * (kAwqBlock + 1), (kAwqBlock + 1) * 4u);
+  const uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(r_sb, t * 4u, 0, 0);
+  const uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_sb, (t + 1u) * 4u, 0, 0);
+  const uint64_t bucket_bit = (uint64_t)T.bucket_bit_base[b];
+  // level 2: the lane's first bitstream words
+  uint2 first[4];
+  {
+    const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
+    const uint64_t base_byte = bucket_bit >> 3;
+    const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+    const __amdgpu_buffer_rsrc_t r_bs = awq_rsrc(
+        reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+    const uint32_t off0 = ((pos >> 5) & ~1u) * 4u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off0 + 16u * (uint32_t)i, 0, 0);
+      first[2 * i] = make_uint2(x[0], x[1]);
+      first[2 * i + 1] = make_uint2(x[2], x[3]);
+    }
+  }
+  const uint32_t m = (uint32_t)T.m;
+  auto gbase = [&](uint32_t gi, int32_t row, int32_t col, bool &bad) -> uint32_t {
+    if (gi >= (uint32_t)groups) return 0u;
+    bad |= row < 0 || (int64_t)row >= T.n || col < 0 || (int64_t)col + 128 > T.m;
+    return (uint32_t)row * m + (uint32_t)col + ((w & 1u) << 6);
+  };
+  bool bad_row = false;
+  const uint32_t base_lo = gbase(gi0, row0, col0, bad_row);
+  const uint32_t base_hi = gbase(gi1, row1, col1, bad_row);
+  if (__builtin_amdgcn_ballot_w64(bad_row)) {
+    if (wl == 0) flag(status, MPS_STATUS_BAD_ROW);
+    return;
+  }
+  const uint32_t count = (uint32_t)groups / 8u + ((w >> 1) < ((uint32_t)groups & 7u) ? 1u : 0u);
+  if (run_flags & 2u)
+    awq_slab_decode<true, kLayGroups>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)groups, 0u,
+                                      bucket_bit, first, pos, pos_end, status);
+  else
+    awq_slab_decode<false, kLayGroups>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)groups, 0u,
+                                       bucket_bit, first, pos, pos_end, status);
 }
 
 // Lane checkpoints of a slab-path row bucket split into row ranges: where each
@@ -933,13 +1013,26 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tenso
   const int4 w = make_int4(wk.tensor, wk.bucket, wk.nsub, wk.kind);
   mps_awq_tensor T = tensors[w.x];
   T.out += out_delta;
+  uint32_t run_flags = 0;
   if (wk.kind == 1) {
-    awq_slab_bucket<false>(T, wk, ckpt, lut, s_base, status);
+    // a run of nsub buckets with identical table ids: the first bucket that
+    // passes its checks loads the tables (the whole workgroup); the buckets
+    // after it run wave by wave. Until the tables are in, every bucket takes
+    // the workgroup path, whose checks are uniform, so all waves meet at its
+    // barriers.
+    for (int r = 0; r < wk.nsub; ++r) {
+      const int64_t b = (int64_t)wk.bucket + r;
+      if ((run_flags & kRunTables) == 0u) {
+        awq_slab_bucket<false>(T, wk, b, true, run_flags, ckpt, lut, s_base, status);
+      } else {
+        awq_slab_bucket_wave(T, b, run_flags, lut, s_base, status);
+      }
+    }
     return;
   }
   if constexpr (kRanges) {
     if (wk.kind == 2) {
-      awq_slab_bucket<true>(T, wk, ckpt, lut, s_base, status);
+      awq_slab_bucket<true>(T, wk, wk.bucket, true, run_flags, ckpt, lut, s_base, status);
       return;
     }
   }
@@ -1097,12 +1190,26 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   int dev = 0, cus = 0;
   MPS_HIP_CHECK(hipGetDevice(&dev));
   MPS_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  // Work records (AwqWork). Slab-eligible buckets get one record each (kind 1);
-  // the others run in runs of up to 1024 / k consecutive buckets of one tensor
-  // with identical table ids (one scale) and at most kRowSlots / 4 rows each, so
-  // they can share a workgroup's tables (kind 0).
+  // Work records (AwqWork). Slab-eligible buckets get one record each (kind 1),
+  // except that by-scale ones take in the following buckets with identical
+  // table ids (nsub in all); the others run in runs of up to 1024 / k
+  // consecutive buckets of one tensor with identical table ids (one scale) and
+  // at most kRowSlots / 4 rows each, so they can share a workgroup's tables
+  // (kind 0).
   std::vector<AwqWork> base;
   std::vector<int32_t> roff, clen, cst, btab, gcol;
+  // Elements a by-scale slab record's run of buckets may hold: a CU's share
+  // of the plan (records go out largest first, so the large ones run early
+  // and small ones fill the end; half a share measured 0.9% slower on an 8B
+  // layer, a quarter 4.8%).
+  int64_t all_elems = 0;
+  for (int64_t i = 0; i < count; ++i)
+    if (tensors[i].n > 0 && tensors[i].m > 0 && tensors[i].n < ((int64_t)1 << 31) && tensors[i].m < ((int64_t)1 << 31))
+      all_elems += tensors[i].n * tensors[i].m;
+#ifndef MPS_AWQ_RUN_DIV
+#define MPS_AWQ_RUN_DIV 1
+#endif
+  const int64_t run_cap = std::max<int64_t>(1, all_elems / (MPS_AWQ_RUN_DIV * (int64_t)std::max(cus, 1)));
   std::vector<int32_t> rows_of_rec, p_of_rec, c0_of_rec;  // row-layout slab records: rows, P, column start
   const char *slab_env = std::getenv("MPSERVE_AWQ_SLAB");
   const bool slab_on = !(slab_env && slab_env[0] == '0');
@@ -1143,29 +1250,44 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     };
     const int64_t maxsub = T.k <= kAwqBlock / 4 ? 4 : T.k <= kAwqBlock / 2 ? 2 : 1;
     const int64_t row_cap = kRowSlots / 4;
+    // (cst holds the column starts only for a slab-eligible row-layout tensor)
+    auto slab_ok = [&](int64_t bb) {
+      const bool shape =
+          slab_tensor &&
+          (T.group_col_start
+               ? rows_of(bb) >= kSlabMinGroups && rows_of(bb) <= kSlabMaxGroups
+               : rows_of(bb) >= 1 && rows_of(bb) <= 128 && clen[(size_t)bb] >= 4 * kAwqBlock &&
+                     clen[(size_t)bb] % kAwqBlock == 0 && cst[(size_t)bb] >= 0 && (cst[(size_t)bb] & 3) == 0 &&
+                     (int64_t)cst[(size_t)bb] + clen[(size_t)bb] <= T.m);
+      return shape && roff[(size_t)bb] >= 0 && roff[(size_t)bb + 1] <= T.num_row_indices;
+    };
+    auto same_tables = [&](int64_t x, int64_t y) {
+      return std::equal(btab.begin() + x * 16, btab.begin() + x * 16 + 16, btab.begin() + y * 16);
+    };
     int64_t b = 0;
     while (b < B) {
       total += elems_of(b);
-      // (cst holds the column starts only for a slab-eligible row-layout tensor)
-      const bool slab_shape =
-          slab_tensor &&
-          (T.group_col_start
-               ? rows_of(b) >= kSlabMinGroups && rows_of(b) <= kSlabMaxGroups
-               : rows_of(b) >= 1 && rows_of(b) <= 128 && clen[(size_t)b] >= 4 * kAwqBlock &&
-                     clen[(size_t)b] % kAwqBlock == 0 && cst[(size_t)b] >= 0 && (cst[(size_t)b] & 3) == 0 &&
-                     (int64_t)cst[(size_t)b] + clen[(size_t)b] <= T.m);
-      if (slab_shape && roff[(size_t)b] >= 0 && roff[(size_t)b + 1] <= T.num_row_indices) {
-        base.push_back(AwqWork{(int32_t)i, (int32_t)b, 1, 1, 0, 0, 1, 0, 0, elems_of(b)});
+      if (slab_ok(b)) {
+        // by-scale: a run of following buckets with identical table ids (one
+        // scale's group-cap chunks) joins the record, up to run_cap elements
+        int64_t run = 1, elems = elems_of(b);
+        if (T.group_col_start) {
+          while (b + run < B && elems + elems_of(b + run) <= run_cap && slab_ok(b + run) && same_tables(b, b + run)) {
+            elems += elems_of(b + run);
+            total += elems_of(b + run);
+            ++run;
+          }
+        }
+        base.push_back(AwqWork{(int32_t)i, (int32_t)b, (int32_t)run, 1, 0, 0, 1, 0, 0, elems});
         rows_of_rec.push_back(T.group_col_start ? 0 : (int32_t)rows_of(b));
         p_of_rec.push_back(T.group_col_start ? 0 : clen[(size_t)b] / kAwqBlock);
         c0_of_rec.push_back(T.group_col_start ? 0 : cst[(size_t)b]);
-        ++b;
+        b += run;
         continue;
       }
       int64_t nsub = 1, elems = elems_of(b);
       if (rows_of(b) <= row_cap) {
-        while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap &&
-               std::equal(btab.begin() + b * 16, btab.begin() + b * 16 + 16, btab.begin() + (b + nsub) * 16)) {
+        while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap && same_tables(b, b + nsub)) {
           elems += elems_of(b + nsub);
           total += elems_of(b + nsub);
           ++nsub;

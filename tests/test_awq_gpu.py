@@ -335,6 +335,10 @@ def test_plan_slab_path_matches_input_and_the_lane_path(by_scale, n, m, cap, see
         if slab == "1" and not by_scale:
             # a lone tensor's row buckets exceed total / (2 CUs): split into row ranges
             assert plan.info()["work_items"] > sc["bucket_table_i32"].shape[0]
+        if slab == "1" and by_scale and cap == 12:
+            # 12-group buckets of one scale are far below total / (2 CUs): runs of
+            # them with identical table ids share a record and its tables
+            assert plan.info()["work_items"] < sc["bucket_table_i32"].shape[0]
         plan.read_status()
         for _ in range(2):
             out.zero_()
