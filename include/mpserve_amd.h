@@ -82,9 +82,12 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
  * checkpoints, also owned by the plan). A sidecar whose bucket metadata, row
  * indices, start bits, tables, FP8 bytes or bitstream is rewritten needs a
  * new plan in that case. The pointed-to sidecars must stay alive while the
- * plan is used. Launches (like mps_fp8_decode's) are persistent: one
- * workgroup per CU walks its share of the work. Decodes are asynchronous on
- * their stream and OR their MPS_STATUS_* flags into the plan's status word
+ * plan is used. Launches are persistent: one workgroup per CU takes work
+ * items from a queue in the plan's memory, which each launch leaves as it
+ * found it, so launches of one plan (mps_fp8_plan_decode and
+ * mps_fp8_plan_decode_into alike) must not overlap: issue them on one stream,
+ * or order their streams. Decodes are asynchronous on their stream and OR
+ * their MPS_STATUS_* flags into the plan's status word
  * (mps_fp8_plan_read_status).
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:739); it serves its apply() and model loading paths
