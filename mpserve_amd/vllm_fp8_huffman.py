@@ -215,6 +215,7 @@ class _LayerDecode:
     weight: Optional[torch.Tensor] = None            # BF16 [N, K] the plan decodes into
     cached: bool = False                             # weight decoded once, kept
     pending: Optional[Tuple[torch.cuda.Event, torch.Tensor]] = None  # a prefetch's (event, weight)
+    last: Optional[Tuple[torch.cuda.Event, int]] = None  # after the plan's last launch: (event, stream handle)
     extra: Dict[str, object] = field(default_factory=dict)
 
 
@@ -363,12 +364,26 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
             raise RuntimeError("fp8_huffman: the layer's sidecar is not on a GPU")
         if st.cached:
             return st.weight
+        s = stream if stream is not None else torch.cuda.current_stream(st.weight.device)
+        # A plan's launches share its work queue and must not overlap: a launch
+        # on another stream than the last one (a prefetch on a side stream after
+        # a decode on the current one, or back) first waits for that one. Under
+        # graph capture the captured order stands.
+        capturing = torch.cuda.is_current_stream_capturing()
+        if st.last is not None and st.last[1] != s.cuda_stream and not capturing:
+            s.wait_event(st.last[0])
         if slot == 0:
-            st.plan.decode(stream)
-            return st.weight
-        buf = SCRATCH.get(st.weight.device, st.weight.numel(), slot)
-        st.plan.decode_into(buf, stream)
-        return buf.view(st.weight.shape)
+            st.plan.decode(s)
+            out = st.weight
+        else:
+            buf = SCRATCH.get(st.weight.device, st.weight.numel(), slot)
+            st.plan.decode_into(buf, s)
+            out = buf.view(st.weight.shape)
+        if not capturing:
+            ev = st.last[0] if st.last is not None else torch.cuda.Event()
+            ev.record(s)
+            st.last = (ev, s.cuda_stream)
+        return out
 
     def prefetch(self, layer: torch.nn.Module, m_in: Optional[int] = None, stream: Optional[torch.cuda.Stream] = None,
                  slot: int = 1) -> None:

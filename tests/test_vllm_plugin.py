@@ -228,6 +228,34 @@ def test_plans_built_at_load_and_reused_by_apply(monkeypatch):
 
 
 @pytest.mark.gpu
+def test_launches_on_two_streams_are_ordered():
+    """A layer decoded on the current stream and, right after, on a side stream
+    (a prefetch into slot 1) launches its plan on two streams; the plan's work
+    queue is shared, so the second launch waits for the first. Both results are
+    exact every round, with no synchronisation between the two launches."""
+    k = 4096
+    bf, q, sc = synth(2048, k, seed=230)
+    layer, method = make_layer("model.layers.2.self_attn.o_proj", [2048], k)
+    load(layer, _to(stored_sidecar(bf, q, sc), DEV))
+    method.process_weights_after_loading(layer)
+    w = torch.from_numpy(bf).view(torch.bfloat16).to(DEV)
+    side = torch.cuda.Stream()
+    w1 = method.decoded_weight(layer, slot=1, stream=side)
+    torch.cuda.synchronize()
+    for rnd in range(4):
+        layer._fp8_huff.weight.zero_()
+        w1.zero_()
+        torch.cuda.synchronize()
+        w0 = method.decoded_weight(layer)                      # current stream
+        assert method.decoded_weight(layer, slot=1, stream=side).data_ptr() == w1.data_ptr()  # side stream
+        method.decoded_weight(layer)                           # and back
+        torch.cuda.synchronize()
+        assert torch.equal(w0.view(torch.uint16), w.view(torch.uint16)), rnd
+        assert torch.equal(w1.view(torch.uint16), w.view(torch.uint16)), rnd
+    assert layer._fp8_huff.plan.read_status() == 0
+
+
+@pytest.mark.gpu
 def test_cache_mode_decodes_once_at_load(monkeypatch):
     monkeypatch.setenv("MPSERVE_FP8_HUFFMAN_CACHE", "1")
     k = 512
