@@ -363,6 +363,45 @@ def _op_call(sc, w, n, m, group, out=None):
         sc["bucket_thread_startbit_u32"], sc["bucket_bit_base_i64"], n, m, 11, out=out)
 
 
+def test_plan_run_with_a_bad_group_row():
+    """A by-scale plan takes a run of buckets with identical table ids into one
+    record, and the run's later buckets set up wave by wave. A group row out of
+    range in such a bucket flags MPS_STATUS_BAD_ROW, no write leaves the output
+    (guards on both sides), and every element outside that bucket decodes exactly."""
+    from mpserve_amd._native import MPS_STATUS_BAD_ROW
+
+    n, m = 2048, 4096
+    w = make_awq_weight(n, m, 128, seed=702, device=DEV)
+    sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, 1024, 12, True)
+    tab = sc["bucket_table_i32"].cpu().numpy()
+    goff = sc["bucket_group_offsets_i32"].cpu().numpy().astype(np.int64)
+    ng = np.diff(goff)
+    same = np.concatenate([[False], (tab[1:] == tab[:-1]).all(1)])
+    # the second bucket of a run: same tables as the one before it, which starts the run
+    second = [b for b in range(2, len(tab)) if same[b] and not same[b - 1] and ng[b] >= 8 and ng[b - 1] >= 8]
+    assert second, "no same-table runs"
+    b = second[len(second) // 2]
+    bad = dict(sc)
+    rows = sc["group_rows_i32"].clone()
+    rows[int(goff[b]) + 3] = n + 1000
+    bad["group_rows_i32"] = rows
+    guard = 4096
+    buf = torch.zeros(n * m + 2 * guard, dtype=torch.bfloat16, device=DEV)
+    out = buf[guard:guard + n * m].view(n, m)
+    plan = awq.AwqDecodePlan([(w.int4_u8, bad, out)])
+    assert plan.info()["work_items"] < len(tab)  # runs share records
+    plan.read_status()
+    plan.decode()
+    torch.cuda.synchronize()
+    assert plan.read_status() & MPS_STATUS_BAD_ROW
+    assert bool((buf[:guard] == 0).all()) and bool((buf[guard + n * m:] == 0).all())
+    keep = torch.ones((n, m), dtype=torch.bool, device=DEV)
+    for r, c in zip(sc["group_rows_i32"][goff[b]:goff[b + 1]].tolist(),
+                    sc["group_col_start_i32"][goff[b]:goff[b + 1]].tolist()):
+        keep[r, c:c + 128] = False
+    assert torch.equal(out.view(torch.int16)[keep], w.bf16.view(torch.int16)[keep])
+
+
 def test_op_plan_cache_alternating_sidecars():
     """The AWQ decode ops keep one plan per sidecar with k = 1024 (by-scale with
     128-column groups, or row buckets) from their second call on, so its buckets take
