@@ -21,7 +21,9 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <mutex>
+#include <queue>
 #include <type_traits>
 #include <vector>
 
@@ -1804,6 +1806,40 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
       }
       if (!changed) break;
     }
+  }
+  // Splitting pays only where it shortens the launch: a tensor whose buckets
+  // about match the CUs (a 70B gate_proj: 224 buckets of 1 M elements for 256
+  // CUs) already ends after one bucket per CU, and its ranges would only add
+  // set-ups. So the plan predicts both launches (items largest first, each to
+  // the CU that frees first, an item costing its elements plus kItemSetup) and
+  // keeps the buckets whole unless the split one ends sooner.
+  {
+    auto makespan = [&](const std::vector<int64_t> &ranges) {
+      std::vector<int64_t> items;
+      for (size_t i = 0; i < bucket.size(); ++i) {
+        const int64_t rows = bucket[i].rows;
+        if (ranges[i] <= 1 || rows <= 0) {
+          items.push_back(elems[i] + kItemSetup);
+          continue;
+        }
+        const int64_t rr = (rows + ranges[i] - 1) / ranges[i];
+        for (int64_t r0 = 0; r0 < rows; r0 += rr) items.push_back(std::min(rr, rows - r0) * bucket[i].cl + kItemSetup);
+      }
+      std::sort(items.begin(), items.end(), std::greater<int64_t>());
+      std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> cu;
+      for (int64_t c = 0; c < ncu; ++c) cu.push(0);
+      int64_t end = 0;
+      for (int64_t x : items) {
+        const int64_t t = cu.top() + x;
+        cu.pop();
+        cu.push(t);
+        end = std::max(end, t);
+      }
+      return end;
+    };
+    const std::vector<int64_t> whole(bucket.size(), 1);
+    if (std::any_of(nr.begin(), nr.end(), [](int64_t x) { return x > 1; }) && makespan(whole) <= makespan(nr))
+      nr = whole;
   }
   std::vector<SplitJob> jobs;
   std::vector<size_t> job_of(bucket.size(), SIZE_MAX);
