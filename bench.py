@@ -77,6 +77,9 @@ def parse_args(argv=None):
                         "awq8b: AWQ int4 decode of one 8B layer, both layouts")
     p.add_argument("--awq-k", type=int, default=1024,
                    help="substreams per bucket of the AWQ sidecars (the reference builders default to 256)")
+    p.add_argument("--fp8-k", type=int, default=1024,
+                   help="--compare-libs on an FP8 workload: substreams per bucket of its sidecars (the headline uses "
+                        "1024; the reference's compress script defaults to 1024, its builder to 256)")
     p.add_argument("--cpu-seconds", type=float, default=8.0, help="time budget of each multi-threaded CPU sample")
     p.add_argument("--cpu-threads", type=int, default=0,
                    help="CPU baseline threads (0: the CPUs this process may run on, capped by OMP_NUM_THREADS)")
@@ -332,8 +335,8 @@ def cache_flush(dev, mib: int = 1024):
     return flush
 
 
-def build_fp8_entries(weights, dev):
-    """(name, fp8, sidecar, bf16 source) of each weight, built on the GPU."""
+def build_fp8_entries(weights, dev, k=1024):
+    """(name, fp8, sidecar, bf16 source) of each weight, built on the GPU with k substreams per bucket."""
     import torch
 
     from mpserve_amd.encode import build_fp8_sidecar
@@ -343,7 +346,7 @@ def build_fp8_entries(weights, dev):
     entries = []
     for i, (name, n, m, seed, sigma, outlier_p) in enumerate(weights):
         w = make_weight(n, m, sigma=sigma, seed=seed, outlier_p=outlier_p, device=dev)
-        sc = build_fp8_sidecar(w.bf16, w.fp8_u8, w.scale_u16, max_len=7, threads_per_block=1024)
+        sc = build_fp8_sidecar(w.bf16, w.fp8_u8, w.scale_u16, max_len=7, threads_per_block=k)
         entries.append((name, w.fp8_u8, sc, w.bf16))
         if i % 7 == 6 or i == len(weights) - 1:
             log(f"built {i + 1}/{len(weights)} ({time.perf_counter() - t0:.1f} s)")
@@ -823,7 +826,7 @@ def compare_libs(args, dev) -> int:
 
         workload = "model8b" if args.workload in ("all", "gemm8b") else args.workload
         kind, tensor_t = "fp8", _native.MpsFp8Tensor
-        entries, _ = build_fp8_entries(config_weights(workload), dev)
+        entries, _ = build_fp8_entries(config_weights(workload), dev, args.fp8_k)
         outs = [torch.empty(src.shape, dtype=torch.bfloat16, device=dev) for _, _, _, src in entries]
         descs = [_descriptor(*sidecar_decode_args(f, sc)[:13], o) for (_, f, sc, _), o in zip(entries, outs)]
     arr = (tensor_t * len(descs))(*descs)

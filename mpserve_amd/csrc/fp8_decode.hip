@@ -71,6 +71,9 @@ __device__ uint32_t g_zero_chunks[2];
 
 // Decode path of a bucket.
 enum : int32_t { kPathBad = 0, kPathGeneric = 1, kPathFast = 2, kPathK1024 = 3 };
+// A plan's fast-path item whose 1024 / k_eff row ranges of one bucket run side
+// by side, one per k_eff work-items (WorkItem::path bit 4; bits 8..15: rows a range).
+constexpr int32_t kMultiRange = 0x10;
 
 struct BucketShape {
   int32_t rows;   // 0 for a bad bucket
@@ -112,7 +115,8 @@ __host__ __device__ inline BucketShape bucket_shape(int32_t ra, int32_t rb, int3
 struct WorkItem {
   int32_t tensor;       // index into the plan's descriptors
   int32_t c0, cl;       // col_start[b], col_len[b]
-  int32_t rows, k_eff, path;
+  int32_t rows, k_eff;
+  int32_t path;                // decode path (bits 0..3); kMultiRange (bit 4): ranges side by side, bits 8..15 their rows
   int64_t bit_base;            // bucket_bit_base[b]
   const int32_t *table_ids;    // bucket_table + 256 b
   const uint32_t *startbits;   // per substream: start bit, relative to bit_base
@@ -337,8 +341,8 @@ __device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin
 
 __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, uint16_t *out,
                                                  const uint32_t *__restrict__ lut,
-                                                 uint32_t *__restrict__ queue, uint32_t lane, uint32_t k_eff,
-                                                 uint32_t rows, uint32_t P, uint32_t rowoff_lo,
+                                                 uint32_t *__restrict__ queue, uint32_t qlane, uint32_t lane,
+                                                 uint32_t k_eff, uint32_t rows, uint32_t P, uint32_t rowoff_lo,
                                                  uint32_t rowoff_hi, uint64_t bucket_bit,
                                                  uint2 first[3], uint32_t pos, uint32_t pos_end,
                                                  uint32_t *status) {
@@ -362,7 +366,7 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, uint16
   auto chunk_mem = [&](uint32_t c) -> uint32_t {
     return __builtin_amdgcn_raw_buffer_load_b32(r_bs, (c ^ 1u) << 2, 0, 0);
   };
-  auto qidx = [&](uint32_t c) -> uint32_t { return ((c & (kQSlots - 1)) * kBlock) + lane; };
+  auto qidx = [&](uint32_t c) -> uint32_t { return ((c & (kQSlots - 1)) * kBlock) + qlane; };
 
   // Initial queue: the three pairs loaded during set-up.
   const uint32_t rq0 = (pos >> 5) & ~1u;
@@ -1096,18 +1100,28 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   int tid;
   __asm__ volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
 
-  const int32_t c0 = w.c0, cl = w.cl, rows = w.rows, k_eff = w.k_eff;
-  const bool bucket_ok = w.path != kPathBad;
+  const int32_t path = w.path & 0xF;
+  const int32_t c0 = w.c0, cl = w.cl, k_eff = w.k_eff;
+  const bool bucket_ok = path != kPathBad;
+  const bool k1024 = path == kPathK1024;
+  const bool fast = path == kPathFast;
+  // A multi-range item (fast path, k_eff 256 or 512): work-items
+  // [sub * k_eff, (sub + 1) * k_eff) decode its sub-th range, whose rows,
+  // start bits and end bits follow the previous range's (uniform per wave).
+  const bool multi = (w.path & kMultiRange) != 0;
+  const int32_t mrr = (w.path >> 8) & 0xFF;
+  const int32_t sub = multi ? (int32_t)uni((uint32_t)(tid >> (k_eff == 256 ? 8 : 9))) : 0;
+  const int32_t rows = multi ? max(0, min(mrr, w.rows - sub * mrr)) : w.rows;
   const int64_t total = (int64_t)rows * cl;
   const uint64_t nm = (uint64_t)T.n * (uint64_t)T.m;
-  const bool k1024 = w.path == kPathK1024;
-  const bool fast = w.path == kPathFast;
-  const int lane = tid;
+  const int lane = multi ? (tid & (k_eff - 1)) : tid;  // the lane's substream (work-item within its range)
   // Substream of this work-item: the k = 1024 paths give wave w's 16-lane row
   // R, position v the column 64w + 4v + R (see decode_slab4); the others, the lane.
-  const int col = k1024 ? ((tid & ~63) | ((tid & 15) << 2) | ((tid >> 4) & 3)) : tid;
+  const int col = k1024 ? ((tid & ~63) | ((tid & 15) << 2) | ((tid >> 4) & 3)) : lane;
   const bool active = bucket_ok && rows > 0 && lane < k_eff;
-  const uint32_t *sb = w.startbits;
+  const uint32_t *sb = w.startbits + (int64_t)sub * k_eff;
+  const uint32_t *eb = w.endbits + (int64_t)sub * k_eff;
+  const int32_t *row_idx = w.row_idx + (int64_t)sub * mrr;
   const uint64_t base = (uint64_t)w.bit_base;
 
   // Set-up: two levels of loads, each issued in full before any of its
@@ -1131,9 +1145,9 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     tk = tid == 0 ? tk : 0u;
   }
   const __amdgpu_buffer_rsrc_t r_ids = make_rsrc(w.table_ids, 256u * 4u);
-  const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(w.row_idx, rows_fast ? (uint32_t)rows * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t r_rows = make_rsrc(row_idx, rows_fast ? (uint32_t)rows * 4u : 0u);
   const __amdgpu_buffer_rsrc_t r_sb = make_rsrc(sb, rows_fast ? (uint32_t)k_eff * 4u : 0u);
-  const __amdgpu_buffer_rsrc_t r_eb = make_rsrc(w.endbits, rows_fast ? (uint32_t)k_eff * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t r_eb = make_rsrc(eb, rows_fast ? (uint32_t)k_eff * 4u : 0u);
   int32_t gids[kSlices];
 #pragma unroll
   for (int i = 0; i < kSlices; ++i)
@@ -1294,8 +1308,8 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     else MPS_K1024(1);
 #undef MPS_K1024
   } else if (fast) {
-    decode_rows_fast(T, out, lut, qregion, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows, (uint32_t)(cl / k_eff),
-                     rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
+    decode_rows_fast(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows,
+                     (uint32_t)(cl / k_eff), rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
   } else {
     const uint64_t pos0 = base + sb[lane];
     const uint64_t pend = base + w.endbits[lane];
@@ -1392,9 +1406,9 @@ struct SplitJob {
   int32_t c0;          // first column
   int32_t range_rows;  // rows per range (the last range may have fewer)
   int32_t ranges;
-  int32_t pad;
+  int32_t full;        // also rows 0 (the lanes' start bits) and `ranges` (their end bits)
   int64_t bit_base;
-  int64_t out;         // first u32 of the job's checkpoints: [ranges - 1][K]
+  int64_t out;         // first u32 of the job's checkpoints: [ranges - 1][K], or [ranges + 1][K] when full
   const int32_t *table_ids;
   const uint32_t *startbits;
   const int32_t *row_idx;
@@ -1428,6 +1442,11 @@ __global__ __launch_bounds__(kBlock) void fp8_checkpoints(const mps_fp8_tensor *
   const uint64_t nchunks = empty ? 2u : (uint64_t)T.bitstream_words * 2u;
   const uint8_t *lens = reinterpret_cast<const uint8_t *>(s_lens);
   uint64_t pos = (uint64_t)J.bit_base + J.startbits[tid];
+  const int64_t row0 = J.out + (J.full ? 0 : -(int64_t)J.K);  // where checkpoint row 0 would go
+  if (J.full) {
+    ckpt[row0 + tid] = J.startbits[tid];
+    ckpt[row0 + (int64_t)J.ranges * J.K + tid] = J.startbits[tid + 1];
+  }
   uint64_t cidx = ~0ull;
   uint32_t ca = 0, cb = 0;
   const int64_t per_range = (int64_t)J.range_rows * J.P;
@@ -1457,7 +1476,7 @@ __global__ __launch_bounds__(kBlock) void fp8_checkpoints(const mps_fp8_tensor *
       const uint32_t nib = (lens[q * kPacked + (peek >> 1)] >> ((peek & 1u) * 4u)) & 0xFu;
       pos += (nib & 7u) + ((nib & 8u) ? 16u : 0u);
     }
-    ckpt[J.out + (int64_t)(j - 1) * J.K + tid] = (uint32_t)(pos - (uint64_t)J.bit_base);
+    ckpt[row0 + (int64_t)j * J.K + tid] = (uint32_t)(pos - (uint64_t)J.bit_base);
   }
 }
 
@@ -1743,6 +1762,16 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   // substream, 16 groups, so that a range's set-up stays small beside its
   // decode). Each range starts from lane checkpoints (fp8_checkpoints).
   //
+  // A fast-path bucket with k_eff 256 or 512 fills only k_eff of a
+  // workgroup's 1024 work-items, and its tables allow one workgroup per CU. So
+  // it is cut into a multiple of S = 1024 / k_eff row ranges, and each work
+  // item runs S of them side by side over the same tables (kMultiRange): the
+  // unit of splitting is then an item of S ranges.
+  //
+  // An item's cost is the time its work-items take: the elements each one
+  // decodes times 1024 (the elements of a k = 1024 item; S ranges side by
+  // side cost one range's), plus kItemSetup for its set-up.
+  //
   // Then the tail. The launch's queue hands the items out largest first
   // (fp8_decode_plan), and an item handed out when R elements of work remain
   // (it and the items after it) can end up to about its size minus R / CUs
@@ -1758,18 +1787,50 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
 #define MPS_TAIL_RATIO 3
 #endif
   constexpr int64_t kTailRatio = MPS_TAIL_RATIO;
-  int64_t total = 0;
-  for (int64_t x : elems) total += x;
   const int64_t ncu = std::max(cus, 1);
-  const int64_t cap = std::max<int64_t>(total / (MPS_SPLIT_DIV * ncu), 65536);
-  std::vector<int64_t> nr(bucket.size(), 1), maxr(bucket.size(), 1);
+  // Per bucket: ranges per item (1, or S for a multi-range bucket), the most
+  // items it may be cut into, and its cost as one item (elements + set-up).
+  std::vector<int64_t> per_item(bucket.size(), 1), maxi(bucket.size(), 1), whole_cost(bucket.size());
+  // cost of `rows` rows of split-capable bucket i decoded by one group of work-items
+  auto rows_cost = [&](size_t i, int64_t rows) {
+    return rows * (int64_t)(bucket[i].cl / bucket[i].k_eff) * 1024 + kItemSetup;
+  };
   for (size_t i = 0; i < bucket.size(); ++i) {
     const WorkItem &w = bucket[i];
+    const int64_t ke = std::max<int64_t>(w.k_eff, 1);
+    whole_cost[i] = (elems[i] + ke - 1) / ke * 1024 + kItemSetup;
     if ((w.path != kPathK1024 && w.path != kPathFast) || w.rows < 2) continue;
     const int32_t P = w.cl / w.k_eff;
     const int32_t min_rows = std::max<int32_t>(1, (64 + P - 1) / P);
-    maxr[i] = std::max<int64_t>(1, w.rows / min_rows);
-    if (elems[i] > cap) nr[i] = std::min<int64_t>((elems[i] + cap - 1) / cap, maxr[i]);
+    const int64_t maxr = std::max<int64_t>(1, w.rows / min_rows);
+    const int64_t S = w.path == kPathFast && (w.k_eff == 256 || w.k_eff == 512) ? 1024 / w.k_eff : 1;
+    // range rows ride in 8 bits of the work record (fast buckets hold <= 128 rows)
+    if (S > 1 && maxr >= S && w.rows <= 255) {
+      per_item[i] = S;
+      maxi[i] = maxr / S;
+      whole_cost[i] = rows_cost(i, (w.rows + S - 1) / S);
+    } else {
+      maxi[i] = maxr;
+    }
+  }
+  // Items of bucket i cut into ni items: their costs, largest first.
+  auto for_items = [&](size_t i, int64_t ni, auto &&emit) {
+    const int64_t rows = bucket[i].rows;
+    if (ni <= 1 && per_item[i] == 1) {
+      emit(whole_cost[i]);
+      return;
+    }
+    const int64_t rr = (rows + ni * per_item[i] - 1) / (ni * per_item[i]);  // rows per range
+    const int64_t step = rr * per_item[i];                                    // rows per item
+    for (int64_t r0 = 0; r0 < rows; r0 += step) emit(rows_cost(i, std::min(rr, rows - r0)));
+  };
+  int64_t total = 0;
+  for (size_t i = 0; i < bucket.size(); ++i) total += whole_cost[i] - kItemSetup;
+  const int64_t cap = std::max<int64_t>(total / (MPS_SPLIT_DIV * ncu), 65536);
+  std::vector<int64_t> ni(bucket.size(), 1);  // items of each bucket
+  for (size_t i = 0; i < bucket.size(); ++i) {
+    const int64_t c = whole_cost[i] - kItemSetup;
+    if (c > cap) ni[i] = std::min<int64_t>((c + cap - 1) / cap, maxi[i]);
   }
   {
     struct Piece {
@@ -1780,16 +1841,7 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
     std::vector<char> bump(bucket.size());
     for (int iter = 0; iter < 64; ++iter) {
       pieces.clear();
-      for (size_t i = 0; i < bucket.size(); ++i) {
-        const int64_t rows = bucket[i].rows;
-        const int64_t rr = nr[i] > 1 ? (rows + nr[i] - 1) / nr[i] : rows;
-        if (nr[i] <= 1 || rr <= 0) {
-          pieces.push_back({elems[i] + kItemSetup, i});
-          continue;
-        }
-        for (int64_t r0 = 0; r0 < rows; r0 += rr)
-          pieces.push_back({std::min(rr, rows - r0) * bucket[i].cl + kItemSetup, i});
-      }
+      for (size_t i = 0; i < bucket.size(); ++i) for_items(i, ni[i], [&](int64_t c) { pieces.push_back({c, i}); });
       std::stable_sort(pieces.begin(), pieces.end(), [](const Piece &a, const Piece &c) { return a.cost > c.cost; });
       std::fill(bump.begin(), bump.end(), 0);
       bool changed = false;
@@ -1797,10 +1849,10 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
       for (size_t q = pieces.size(); q-- > 0;) {
         rest += pieces[q].cost;
         const size_t b = pieces[q].b;
-        if ((int64_t)q < ncu || bump[b] || nr[b] >= maxr[b]) continue;
+        if ((int64_t)q < ncu || bump[b] || ni[b] >= maxi[b]) continue;
         if ((double)pieces[q].cost * (double)ncu > (double)kTailRatio * (double)rest) {
           bump[b] = 1;
-          nr[b] = std::min(maxr[b], nr[b] * 2);
+          ni[b] = std::min(maxi[b], ni[b] * 2);
           changed = true;
         }
       }
@@ -1811,20 +1863,12 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   // about match the CUs (a 70B gate_proj: 224 buckets of 1 M elements for 256
   // CUs) already ends after one bucket per CU, and its ranges would only add
   // set-ups. So the plan predicts both launches (items largest first, each to
-  // the CU that frees first, an item costing its elements plus kItemSetup) and
-  // keeps the buckets whole unless the split one ends sooner.
+  // the CU that frees first) and keeps the buckets whole (multi-range buckets:
+  // one item) unless the split one ends sooner.
   {
-    auto makespan = [&](const std::vector<int64_t> &ranges) {
+    auto makespan = [&](const std::vector<int64_t> &items_of) {
       std::vector<int64_t> items;
-      for (size_t i = 0; i < bucket.size(); ++i) {
-        const int64_t rows = bucket[i].rows;
-        if (ranges[i] <= 1 || rows <= 0) {
-          items.push_back(elems[i] + kItemSetup);
-          continue;
-        }
-        const int64_t rr = (rows + ranges[i] - 1) / ranges[i];
-        for (int64_t r0 = 0; r0 < rows; r0 += rr) items.push_back(std::min(rr, rows - r0) * bucket[i].cl + kItemSetup);
-      }
+      for (size_t i = 0; i < bucket.size(); ++i) for_items(i, items_of[i], [&](int64_t c) { items.push_back(c); });
       std::sort(items.begin(), items.end(), std::greater<int64_t>());
       std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> cu;
       for (int64_t c = 0; c < ncu; ++c) cu.push(0);
@@ -1838,9 +1882,12 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
       return end;
     };
     const std::vector<int64_t> whole(bucket.size(), 1);
-    if (std::any_of(nr.begin(), nr.end(), [](int64_t x) { return x > 1; }) && makespan(whole) <= makespan(nr))
-      nr = whole;
+    if (std::any_of(ni.begin(), ni.end(), [](int64_t x) { return x > 1; }) && makespan(whole) <= makespan(ni))
+      ni = whole;
   }
+  // Ranges of each bucket.
+  std::vector<int64_t> nr(bucket.size());
+  for (size_t i = 0; i < bucket.size(); ++i) nr[i] = ni[i] * per_item[i];
   std::vector<SplitJob> jobs;
   std::vector<size_t> job_of(bucket.size(), SIZE_MAX);
   int64_t ck_words = 0, max_items = 0;
@@ -1866,9 +1913,10 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
     j.table_ids = w.table_ids;
     j.startbits = w.startbits;
     j.row_idx = w.row_idx;
+    j.full = per_item[i] > 1 ? 1 : 0;
     job_of[i] = jobs.size();
     jobs.push_back(j);
-    ck_words += (ranges - 1) * w.k_eff;
+    ck_words += (per_item[i] > 1 ? ranges + 1 : ranges - 1) * w.k_eff;
     max_items += ranges - 1;
   }
 
@@ -1922,19 +1970,33 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   if (e != hipSuccess) return cleanup(e);
 
   // Work items (buckets and ranges), largest first, the order in which the
-  // launch's queue hands them out. An item's cost is its element count plus
-  // kItemSetup.
+  // launch's queue hands them out, by the cost above.
   std::vector<WorkItem> work;
   std::vector<int64_t> cost;
   for (size_t i = 0; i < bucket.size(); ++i) {
     const WorkItem &w = bucket[i];
     if (job_of[i] == SIZE_MAX || failed[job_of[i]]) {
       work.push_back(w);
-      cost.push_back(elems[i] + kItemSetup);
+      cost.push_back(per_item[i] > 1 ? rows_cost(i, w.rows) : whole_cost[i]);  // a failed walk: one range
       continue;
     }
     const SplitJob &j = jobs[job_of[i]];
     const uint32_t *ck = d_ckpt + j.out;
+    if (j.full) {
+      // S ranges an item; range r's start bits are checkpoint row r, its end bits row r + 1
+      const int32_t S = 1024 / j.K;
+      for (int32_t r = 0; r < j.ranges; r += S) {
+        WorkItem x = w;
+        x.path = kPathFast | kMultiRange | (j.range_rows << 8);
+        x.rows = w.rows - r * j.range_rows;
+        x.row_idx = w.row_idx + (int64_t)r * j.range_rows;
+        x.startbits = ck + (int64_t)r * j.K;
+        x.endbits = ck + (int64_t)(r + 1) * j.K;
+        work.push_back(x);
+        cost.push_back(rows_cost(i, std::min(j.range_rows, x.rows)));
+      }
+      continue;
+    }
     for (int32_t r = 0; r < j.ranges; ++r) {
       WorkItem x = w;
       x.rows = std::min(j.range_rows, w.rows - r * j.range_rows);
@@ -1942,7 +2004,7 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
       x.startbits = r == 0 ? w.startbits : ck + (int64_t)(r - 1) * j.K;
       x.endbits = r + 1 == j.ranges ? w.endbits : ck + (int64_t)r * j.K;
       work.push_back(x);
-      cost.push_back((int64_t)x.rows * w.cl + kItemSetup);
+      cost.push_back(rows_cost(i, x.rows));
     }
   }
   {

@@ -300,10 +300,14 @@ def _plan_decode(items):
     return [o.view(torch.uint16).cpu().numpy() for _, _, o in dev_items], plan.info(), plan.read_status()
 
 
-@pytest.mark.parametrize("case", ["slab_p8", "slab_wrap_p14", "esc_k1024", "fast_k256", "mixed"])
+@pytest.mark.parametrize("case", ["slab_p8", "slab_wrap_p14", "esc_k1024", "fast_k256", "fast_k512", "fast_k256_ragged",
+                                  "mixed", "mixed_multi"])
 def test_plan_splits_buckets_into_row_ranges(case):
     """A plan with few large buckets splits them into row ranges started from lane
-    checkpoints; every range decodes bit-exact and ends where the next begins."""
+    checkpoints; every range decodes bit-exact and ends where the next begins. A
+    fast-path bucket with k = 256 or 512 runs 1024 / k of its ranges side by side
+    in one work item (its other work-items would idle): fewer items than ranges,
+    and with ragged rows the last item has fewer ranges than work-item groups."""
     if case == "slab_p8":       # 2 buckets of 128 rows x 8192 columns (one scale key)
         bf, q, sc = synth(256, 8192, seed=81)
         items = [(bf, q, oracle.encode(bf, q, sc[:1].copy(), 7, 1024))]
@@ -318,6 +322,17 @@ def test_plan_splits_buckets_into_row_ranges(case):
     elif case == "fast_k256":   # k = 256 substreams, P = 8
         bf, q, sc = synth(300, 2048, seed=84)
         items = [(bf, q, oracle.encode(bf, q, sc[:1].copy(), 7, 256))]
+    elif case == "fast_k512":   # k = 512, P = 8: two ranges an item
+        bf, q, sc = synth(256, 4096, seed=89)
+        items = [(bf, q, oracle.encode(bf, q, sc[:1].copy(), 7, 512))]
+    elif case == "fast_k256_ragged":  # 10 rows, P = 128: five ranges of 2 rows, the second item holds one
+        bf, q, sc = synth(10, 32768, seed=90)
+        items = [(bf, q, oracle.encode(bf, q, sc[:1].copy(), 7, 256))]
+    elif case == "mixed_multi":  # a multi-range bucket beside k = 1024 slab buckets
+        a = synth(256, 8192, seed=91)
+        b = synth(200, 2048, seed=92)
+        items = [(a[0], a[1], oracle.encode(a[0], a[1], a[2][:1].copy(), 7, 1024)),
+                 (b[0], b[1], oracle.encode(b[0], b[1], b[2][:1].copy(), 7, 256))]
     else:                       # a split tensor next to whole buckets and a generic-path tensor
         a = synth(256, 8192, seed=85)
         b = synth(64, 4096, seed=86)
@@ -327,7 +342,10 @@ def test_plan_splits_buckets_into_row_ranges(case):
                  (c[0], c[1], oracle.encode(c[0], c[1], c[2], 7, 1024))]
     buckets = sum(sc["bucket_table_i32"].shape[0] for _, _, sc in items)
     outs, info, status = _plan_decode(items)
-    assert info["work_items"] > buckets
+    if case.startswith("fast_k"):
+        assert info["work_items"] >= buckets  # ranges run side by side: items, not ranges
+    else:
+        assert info["work_items"] > buckets
     for (bf, _, _), got in zip(items, outs):
         assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
     assert status == 0
