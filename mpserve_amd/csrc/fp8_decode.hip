@@ -763,9 +763,10 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, uint16_t *
 // symbol from the 16 raw bits. ESC codes are rare (the symbols a key's
 // 127 most frequent leave out), so the wave almost never takes that branch.
 // ---------------------------------------------------------------------------
-template <bool kWrap, bool kEsc>
+template <bool kWrap, bool kEsc, int kShift>
 __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *out, const uint32_t *__restrict__ lut,
-                                             uint32_t *__restrict__ queue, uint32_t lane, uint32_t rows, uint32_t P,
+                                             uint32_t *__restrict__ queue, uint32_t qlane, uint32_t lane,
+                                             uint32_t kshift, uint32_t rows, uint32_t P,
                                              uint32_t rowoff_lo, uint32_t rowoff_hi, uint64_t bucket_bit,
                                              const uint2 (&first)[4], uint32_t pos, uint32_t pos_end,
                                              uint32_t *status) {
@@ -776,6 +777,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   static_assert(DF >= 4 && DF % 4 == 0, "the bitstream is served once per four groups");
   rows = uni(rows);
   P = uni(P);
+  kshift = kShift ? (uint32_t)kShift : uni(kshift);
   bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
   const uint32_t count = rows * P;  // elements per lane
   const uint32_t nfull = count >> 2;
@@ -790,7 +792,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   const __amdgpu_buffer_rsrc_t r_bs =
       make_rsrc(reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
 
-  const uint32_t lane4 = lane << 2;
+  const uint32_t lane4 = qlane << 2;  // the work-item's queue column
   const uint32_t R = (lane >> 4) & 3u;
   const uint32_t colw = (lane & ~63u) | ((lane & 15u) << 2);  // 64w + 4v
   const char *qbytes = reinterpret_cast<const char *>(queue);
@@ -805,7 +807,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   };
   // Chunks h (even) and h + 1: slots (~h) & 7 and the one below it.
   auto put_pair = [&](uint32_t h, uint32_t hi, uint32_t lo) {
-    uint32_t *slot = queue + (((~h << 10) & 0x1800u) | lane);
+    uint32_t *slot = queue + (((~h << 10) & 0x1800u) | qlane);
     slot[0] = lo;     // chunk h + 1
     slot[1024] = hi;  // chunk h: the high half of a bitstream word is its first chunk
   };
@@ -915,20 +917,20 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   uint32_t w_g = 0, w_row = 0, w_blk = 0;
   uint32_t w_off = row_offset(0);
   uint32_t w_next = row_offset(rows > 1u ? 1u : 0u);  // offset of row w_row + 1 (kWrap)
-  const uint32_t vf_al = R * 1024u + colw;           // lane's FP8 byte offset within an aligned group
+  const uint32_t vf_al = (R << kshift) + colw;       // lane's FP8 byte offset within an aligned group
   // FP8 load of the walker's group; returns the group's BF16 store offset
   // (aligned: the uniform element offset of slab 4g; kWrap: the lane's byte offset).
   auto load_group = [&](uint32_t &F) -> uint32_t {
     uint32_t ret;
     if constexpr (!kWrap) {
-      const uint32_t so = uni(w_off + (w_blk << 10));
+      const uint32_t so = uni(w_off + (w_blk << kshift));
       F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, vf_al, so, MPS_SLAB_FP8_CPOL);
       ret = so;
     } else {
       const uint32_t b = w_blk + R;
       const bool wrap = b >= P;
       const bool ok = !wrap || w_row + 1u < rows;
-      const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << 10) + colw;
+      const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << kshift) + colw;
       F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, ok ? off : 0u, 0, MPS_SLAB_FP8_CPOL);
       ret = ok ? off << 1 : kSlabPast;
     }
@@ -1026,7 +1028,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
 #define MPS_PRIO_LEAD 8
 #endif
   const uint32_t quarter = uni(nfull / 4u > 0u ? nfull / 4u : 1u);
-  const uint32_t lead = (3u - (uni(lane) >> 8)) * (quarter * MPS_PRIO_LEAD / 16u);  // head start (groups)
+  const uint32_t lead = (3u - (uni(qlane) >> 8)) * (quarter * MPS_PRIO_LEAD / 16u);  // head start (groups)
   uint32_t prio = 3u - (lead / quarter < 3u ? lead / quarter : 3u);
   uint32_t prio_at = (lead / quarter + 1u) * quarter - lead;  // groups done when the priority next drops
   if (prio == 3u) __builtin_amdgcn_s_setprio(3);
@@ -1087,7 +1089,11 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
 // from the launch's work counter (queue[0]), at the start of its set-up, so
 // that the atomic's round trip overlaps the set-up's loads; every thread
 // gets it in `ticket` (zero without kQueue).
-template <bool kQueue>
+// kSlabK: fast-path buckets with k_eff 256 or 512 and P % 4 == 0 take the slab
+// path (else the scalar element walk). Only launches whose tensors have such
+// k compile it in: the extra slab instances cost the k = 1024 launches 1.5%
+// (registers), though their own code is unchanged.
+template <bool kQueue, bool kSlabK>
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t *out, const WorkItem &w,
                                               uint32_t *lds, uint32_t *status, uint32_t *queue, uint32_t &ticket) {
   uint32_t *qregion = lds;
@@ -1117,7 +1123,10 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   const int lane = multi ? (tid & (k_eff - 1)) : tid;  // the lane's substream (work-item within its range)
   // Substream of this work-item: the k = 1024 paths give wave w's 16-lane row
   // R, position v the column 64w + 4v + R (see decode_slab4); the others, the lane.
-  const int col = k1024 ? ((tid & ~63) | ((tid & 15) << 2) | ((tid >> 4) & 3)) : lane;
+  // A fast-path bucket with k_eff 256 or 512 and P % 4 == 0 takes the slab path too (kSlabK).
+  const bool slab = kSlabK && fast && (k_eff == 256 || k_eff == 512) && cl % (4 * k_eff) == 0;
+  const int col = k1024 ? ((tid & ~63) | ((tid & 15) << 2) | ((tid >> 4) & 3))
+                  : slab ? ((lane & ~63) | ((lane & 15) << 2) | ((lane >> 4) & 3)) : lane;
   const bool active = bucket_ok && rows > 0 && lane < k_eff;
   const uint32_t *sb = w.startbits + (int64_t)sub * k_eff;
   const uint32_t *eb = w.endbits + (int64_t)sub * k_eff;
@@ -1279,9 +1288,9 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   if (k1024) {
     const uint32_t P = (uint32_t)cl / 1024u;
     if (P >= 4) {
-#define MPS_SLAB(WRAP, ESC)                                                                                \
-  decode_slab4<WRAP, ESC>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)rows, P, rowoff_lo, rowoff_hi, base, \
-                          first, pos, pos_end, status)
+#define MPS_SLAB(WRAP, ESC)                                                                               \
+  decode_slab4<WRAP, ESC, 10>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)lane, 10u, (uint32_t)rows, P, \
+                              rowoff_lo, rowoff_hi, base, first, pos, pos_end, status)
       if (P % 4 == 0) {
         if (has_esc) MPS_SLAB(false, true);
         else MPS_SLAB(false, false);
@@ -1307,6 +1316,16 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     else if (P % 2 == 0) MPS_K1024(2);
     else MPS_K1024(1);
 #undef MPS_K1024
+  } else if (kSlabK && slab) {
+    // k_eff 256 / 512 with P % 4 == 0: work-item tid decodes substream `col` of its range
+    const uint32_t ks = k_eff == 512 ? 9u : 8u;
+    const uint32_t P = (uint32_t)cl >> ks;
+    if (has_esc)
+      decode_slab4<false, true, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
+                                   rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
+    else
+      decode_slab4<false, false, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
+                                    rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
   } else if (fast) {
     decode_rows_fast(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows,
                      (uint32_t)(cl / k_eff), rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
@@ -1333,11 +1352,12 @@ __device__ __forceinline__ void end_bucket() {
 // bucket's tables) walks its share of the buckets, so a bucket's set-up does
 // not also pay a workgroup launch. fp8_decode_one deals the buckets
 // round-robin; every workgroup runs the same uniform loop to its end.
+template <bool kSlabK>
 __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   uint32_t ticket;
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
-    decode_bucket<false>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket);
+    decode_bucket<false, kSlabK>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket);
     end_bucket();
   }
 }
@@ -1357,6 +1377,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
 // Tickets travel in 30 bits of the set-up's flag words: a launch holds fewer
 // than kMaxQueueItems work items.
 constexpr int64_t kMaxQueueItems = (int64_t(1) << 30) - 65536;
+template <bool kSlabK>
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
                                                           const WorkItem *__restrict__ work, int64_t nwork,
                                                           uint32_t *status, int64_t out_delta, uint32_t *queue) {
@@ -1366,7 +1387,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
     for (;;) {
       uint32_t ticket;
       const mps_fp8_tensor &T = tensors[w.tensor];
-      decode_bucket<true>(T, T.out + out_delta, w, lds, status, queue, ticket);
+      decode_bucket<true, kSlabK>(T, T.out + out_delta, w, lds, status, queue, ticket);
       const int64_t next = (int64_t)gridDim.x + ticket;
       // The next record (scalar registers) is loaded before the drain of this
       // item's stores, which covers its round trip.
@@ -1658,6 +1679,9 @@ size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 // A plan owns one device allocation: its status word, the tensor descriptors,
 // the lane checkpoints of the buckets it split, the work records and (during
 // creation) the checkpoint jobs and their failure flags.
+// Tensors with k 256 or 512 substreams may have buckets for the slab path at that k.
+inline bool slab_k(int64_t k) { return k == 256 || k == 512; }
+
 struct mps_fp8_plan {
   void *d_block = nullptr;
   uint32_t *d_status = nullptr;
@@ -1668,6 +1692,7 @@ struct mps_fp8_plan {
   int64_t count = 0;
   int64_t work_items = 0;
   int device = 0;
+  bool slab_k = false;  // some tensor has k 256 or 512: launch fp8_decode_plan<true>
 };
 
 extern "C" {
@@ -1696,8 +1721,12 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream) 
   unsigned grid = 0;
   rc = persistent_grid(tensor->num_buckets, &grid);
   if (rc != MPS_OK) return rc;
-  hipLaunchKernelGGL(fp8_decode_one, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream), *tensor,
-                     status);
+  if (slab_k(tensor->k))
+    hipLaunchKernelGGL(fp8_decode_one<true>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
+                       *tensor, status);
+  else
+    hipLaunchKernelGGL(fp8_decode_one<false>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
+                       *tensor, status);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
@@ -1933,6 +1962,7 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   auto *p = new (std::nothrow) mps_fp8_plan();
   if (!p) return fail(MPS_ERR_NO_MEMORY, "out of memory");
   p->count = count;
+  p->slab_k = std::any_of(tensors, tensors + count, [](const mps_fp8_tensor &t) { return slab_k(t.k); });
   p->device = device;
   p->first_out = count > 0 ? tensors[0].out : nullptr;
   hipError_t e = hipMalloc(&p->d_block, bytes);
@@ -2031,8 +2061,12 @@ int plan_launch(mps_fp8_plan *plan, int64_t out_delta, uint32_t *status, void *s
   unsigned grid = 0;
   const int rc = persistent_grid(plan->work_items, &grid);
   if (rc != MPS_OK) return rc;
-  hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                     plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, plan->d_queue);
+  if (plan->slab_k)
+    hipLaunchKernelGGL(fp8_decode_plan<true>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
+                       plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, plan->d_queue);
+  else
+    hipLaunchKernelGGL(fp8_decode_plan<false>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
+                       plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, plan->d_queue);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
@@ -2127,8 +2161,13 @@ int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, i
   unsigned grid = 0;
   rc = persistent_grid(total, &grid);
   if (rc != MPS_OK) return rc;
-  hipLaunchKernelGGL(fp8_decode_plan, dim3(grid), dim3(kBlock), 0, st, d_tensors, d_work, total, status,
-                     (int64_t)0, reinterpret_cast<uint32_t *>(base + kBatchQueueOff));
+  const bool sk = std::any_of(tensors, tensors + count, [](const mps_fp8_tensor &t) { return slab_k(t.k); });
+  if (sk)
+    hipLaunchKernelGGL(fp8_decode_plan<true>, dim3(grid), dim3(kBlock), 0, st, d_tensors, d_work, total, status,
+                       (int64_t)0, reinterpret_cast<uint32_t *>(base + kBatchQueueOff));
+  else
+    hipLaunchKernelGGL(fp8_decode_plan<false>, dim3(grid), dim3(kBlock), 0, st, d_tensors, d_work, total, status,
+                       (int64_t)0, reinterpret_cast<uint32_t *>(base + kBatchQueueOff));
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }

@@ -87,6 +87,34 @@ def test_decode_k1024_esc(n, m, seed):
     assert _status() == 0
 
 
+@pytest.mark.parametrize("n,m,k,seed,esc", [
+    (200, 4096, 256, 120, False),   # P = 16, per-row scales
+    (100, 1536, 256, 121, False),   # P = 6: groups straddle rows
+    (64, 3584, 512, 122, False),    # P = 7
+    (130, 2048, 512, 123, False),   # P = 4
+    (40, 2048, 256, 124, True),     # ESC entries, P = 8
+    (30, 1792, 256, 125, True),     # ESC entries, P = 7
+])
+def test_decode_slab_k256_k512(n, m, k, seed, esc):
+    """Buckets with k = 256 or 512 substreams and P = col_len / k >= 4 take the slab
+    path (groups of four elements across 4 x 4 lane transposes), as the single
+    op and inside a plan (whole buckets and row ranges side by side)."""
+    if esc:
+        bf, q, scales = _esc_inputs(n, m, seed)
+        sc, stats = oracle.encode(bf, q, scales, 7, k, with_stats=True)
+        assert stats["esc_keys"] >= 1 and stats["esc_elements"] > 0
+    else:
+        bf, q, scales = synth(n, m, seed=seed)
+        sc = oracle.encode(bf, q, scales, 7, k)
+    _status()
+    got = _gpu_decode(sc, q)
+    assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
+    assert _status() == 0
+    outs, _, status = _plan_decode([(bf, q, sc)])
+    assert np.array_equal(outs[0], bf), f"plan mismatches: {(outs[0] != bf).sum()}"
+    assert status == 0
+
+
 def test_decode_scalar_scale_many_buckets():
     n, m = 1000, 640
     bf, q, sc_u16 = synth(n, m, seed=11)
