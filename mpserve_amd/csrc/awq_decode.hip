@@ -343,7 +343,10 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
 //  kind 1: one slab-path bucket;
 //  kind 2: rows [range * range_rows, +range_rows) of a slab-path row bucket split into
 //          `ranges` ranges, starting from the lane checkpoints at ckpt + (range - 1) * 1024
-//          and ending at ckpt + range * 1024 (the bucket's own start and end bits at its ends).
+//          and ending at ckpt + range * 1024 (the bucket's own start and end bits at its ends);
+//  kind 3: ranges range .. range + 1024 / k - 1 of a row bucket with k 256 or 512 split into
+//          `ranges` ranges, side by side on the slab path: range r starts at checkpoint row
+//          r and ends at row r + 1 of ckpt ([ranges + 1][k]).
 struct AwqWork {
   int32_t tensor, bucket, nsub, kind;
   int32_t range, range_rows, ranges, pad;
@@ -378,9 +381,14 @@ enum : int { kLayGroups = 0, kLayRows = 1, kLayRowsWrap = 2 };
 // base_lo / base_hi: lane l holds slab l's and l + 64's base (groups), or row
 // l's and l + 64's offset (rows, column start included); rows and P describe a
 // row bucket (rows x P elements per lane).
-template <bool kEsc, int kLay>
+// kShift: log2 of the substream count k (the row layouts' block stride), 10,
+// or 0 for the run-time `kshift` (kLayRows with k 256 or 512, several row
+// ranges side by side: `lane` is the work-item's substream within its range's
+// group of k, `qlane` the work-item, whose LDS queue column it owns).
+template <bool kEsc, int kLay, int kShift = 10>
 __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const uint32_t *__restrict__ lut,
-                                                uint32_t *__restrict__ queue, uint32_t lane, uint32_t count,
+                                                uint32_t *__restrict__ queue, uint32_t qlane, uint32_t lane,
+                                                uint32_t kshift, uint32_t count,
                                                 uint32_t base_lo, uint32_t base_hi, uint32_t rows, uint32_t P,
                                                 uint64_t bucket_bit, const uint2 (&first)[4], uint32_t pos,
                                                 uint32_t pos_end, uint32_t *status) {
@@ -394,7 +402,9 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   constexpr int FE = MPS_AWQ_FEED_EVERY;     // steps per bitstream feed (16 bytes: 2 x 44 bits fit)
   static_assert(DF % FE == 0 && (FE == 1 || FE == 2), "a feed every one or two steps");
   constexpr int RB = 4;  // 16-byte blocks per bitstream request
+  static_assert(kShift == 10 || (kShift == 0 && kLay == kLayRows), "k < 1024: row buckets with P % 4 == 0");
   count = awq_uni(count);
+  kshift = kShift ? (uint32_t)kShift : awq_uni(kshift);
   bucket_bit = ((uint64_t)awq_uni((uint32_t)(bucket_bit >> 32)) << 32) | awq_uni((uint32_t)bucket_bit);
   const uint32_t nfull = count >> 2;
   const uint32_t tail = count & 3u;  // elements of the last, partial step
@@ -408,7 +418,7 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   const __amdgpu_buffer_rsrc_t r_bs =
       awq_rsrc(reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
 
-  const uint32_t lane4 = lane << 2;
+  const uint32_t lane4 = qlane << 2;
   const uint32_t R = (lane >> 4) & 3u;
   const uint32_t v4 = (lane & 15u) << 2;
   const char *qbytes = reinterpret_cast<const char *>(queue);
@@ -422,7 +432,7 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     return __builtin_amdgcn_raw_buffer_load_b32(r_bs, ((h - 2u) ^ 1u) << 2, 0, 0);
   };
   auto put_pair = [&](uint32_t h, uint32_t hi, uint32_t lo) {  // chunks h (even) and h + 1
-    uint32_t *slot = queue + (((~h << 10) & 0x1800u) | lane);
+    uint32_t *slot = queue + (((~h << 10) & 0x1800u) | qlane);
     slot[0] = lo;
     slot[1024] = hi;
   };
@@ -515,8 +525,8 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     w_off = row_offset(0);
     w_next = row_offset(rows > 1u ? 1u : 0u);  // offset of row w_row + 1 (kLayRowsWrap)
   }
-  const uint32_t colw = (lane & ~63u) | v4;  // 64w + 4v: the lane's columns within a 1024-block
-  const uint32_t vf_al = R * 1024u + colw;   // ... and its block within an aligned step
+  const uint32_t colw = (lane & ~63u) | v4;    // 64w + 4v: the lane's columns within a k-block
+  const uint32_t vf_al = (R << kshift) + colw;  // ... and its block within an aligned step
   auto load_step = [&](uint32_t &F) -> uint32_t {
     uint32_t ret;
     if constexpr (kLay == kLayGroups) {
@@ -529,14 +539,14 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
       F = __builtin_amdgcn_raw_buffer_load_b32(r_q, ok ? off : kSlabInPast, 0, 0);
       ret = ok ? off << 1 : kSlabOutPast;
     } else if constexpr (kLay == kLayRows) {
-      const uint32_t so = awq_uni(w_off + (w_blk << 10));
+      const uint32_t so = awq_uni(w_off + (w_blk << kshift));
       F = __builtin_amdgcn_raw_buffer_load_b32(r_q, vf_al, so, 0);
       ret = so;
     } else {
       const uint32_t b = w_blk + R;
       const bool wrap = b >= P;
       const bool ok = !wrap || w_row + 1u < rows;
-      const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << 10) + colw;
+      const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << kshift) + colw;
       F = __builtin_amdgcn_raw_buffer_load_b32(r_q, ok ? off : kSlabInPast, 0, 0);
       ret = ok ? off << 1 : kSlabOutPast;
     }
@@ -630,7 +640,7 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
 #define MPS_AWQ_PRIO_LEAD 16
 #endif
   const uint32_t quarter = awq_uni(nfull / 4u > 0u ? nfull / 4u : 1u);
-  const uint32_t lead = (3u - (awq_uni(lane) >> 8)) * (quarter * MPS_AWQ_PRIO_LEAD / 16u);  // head start (steps)
+  const uint32_t lead = (3u - (awq_uni(qlane) >> 8)) * (quarter * MPS_AWQ_PRIO_LEAD / 16u);  // head start (steps)
   uint32_t prio = 3u - (lead / quarter < 3u ? lead / quarter : 3u);
   uint32_t prio_at = (lead / quarter + 1u) * quarter - lead;  // steps done when the priority next drops
   if (MPS_AWQ_PRIO) {
@@ -677,12 +687,15 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
 // and end bits; (2) the tables' slices and the lane's first bitstream words.
 // Thread tid expands entries 32c .. 32c+31 of the table of int4 value tid / 64
 // (c = tid % 64).
-// kRanged: a row range (kind 2); whole buckets compile without the range logic.
+// kRanged: 0 a whole bucket, 1 a row range (kind 2), 2 row ranges side by side
+// (kind 3: k 256 or 512, the work-items [s k, (s + 1) k) decode range
+// wk.range + s, from checkpoint rows range + s and range + s + 1 of a full
+// [ranges + 1][k] set); whole buckets compile without the range logic.
 // A by-scale record may hold a run of buckets b with identical table ids: the
 // first that gets past its checks (`tables`) loads and expands the tables and
 // records in run_flags that it did (kRunTables) and whether they have an ESC
 // entry (bit 1); the others reuse both.
-template <bool kRanged>
+template <int kRanged>
 __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const AwqWork &wk, int64_t b, bool tables,
                                                 uint32_t &run_flags, const uint32_t *__restrict__ ckpt,
                                                 uint32_t *__restrict__ lut, uint32_t *__restrict__ region,
@@ -694,30 +707,41 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const int32_t groups = rb - ra;  // groups (by-scale) or rows
   const int32_t c0 = by_scale ? 0 : T.bucket_col_start[b];
   const int32_t cl = by_scale ? 128 : T.bucket_col_len[b];
+  constexpr bool kMulti = kRanged == 2;
+  const int32_t K = kMulti ? (int32_t)T.k : kAwqBlock;  // substreams (the block stride)
+  const uint32_t ks = K == 256 ? 8u : K == 512 ? 9u : 10u;
   const bool shape_ok =
-      by_scale ? (groups >= kSlabMinGroups && groups <= kSlabMaxGroups && T.group_size == 128)
-               : (groups >= 1 && groups <= 128 && cl >= 4 * kAwqBlock && cl % kAwqBlock == 0 && c0 >= 0 &&
+      by_scale ? (!kMulti && groups >= kSlabMinGroups && groups <= kSlabMaxGroups && T.group_size == 128)
+               : (groups >= 1 && groups <= 128 && cl >= 4 * K && cl % (kMulti ? 4 * K : K) == 0 && c0 >= 0 &&
                   (int64_t)c0 + cl <= T.m);
-  if (!shape_ok || ra < 0 || (int64_t)rb > T.num_row_indices || T.k != kAwqBlock) {
+  const bool k_ok = kMulti ? (K == 256 || K == 512) : T.k == kAwqBlock;
+  if (!shape_ok || !k_ok || ra < 0 || (int64_t)rb > T.num_row_indices) {
     if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
     return;
   }
-  const uint32_t P = by_scale ? 0u : (uint32_t)cl / (uint32_t)kAwqBlock;
-  // a row range (kind 2): its first row and row count; its lanes start and end at checkpoints
-  const bool ranged = kRanged && !by_scale;
-  const int32_t first_row = ranged ? wk.range * wk.range_rows : 0;
-  const int32_t nr = ranged ? (groups - first_row < wk.range_rows ? groups - first_row : wk.range_rows) : groups;
-  if (nr <= 0) {
+  const uint32_t P = by_scale ? 0u : (uint32_t)cl >> ks;
+  // a row range (kinds 2, 3): its first row and row count; its lanes start and
+  // end at checkpoints. Kind 3: this work-item's group of K (uniform per wave)
+  // and its range; a last record's spare groups have no rows and only take
+  // part in the barriers.
+  const bool ranged = kRanged != 0 && !by_scale;
+  const int32_t sub = kMulti ? (int32_t)awq_uni((uint32_t)tid >> ks) : 0;
+  const int32_t range = wk.range + sub;
+  const int32_t first_row = ranged ? range * wk.range_rows : 0;
+  const int32_t nr_all = ranged ? (groups - first_row < wk.range_rows ? groups - first_row : wk.range_rows) : groups;
+  const int32_t nr = kMulti ? (range < wk.ranges && nr_all > 0 ? nr_all : 0) : nr_all;
+  if (!kMulti && nr <= 0) {
     if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
     return;
   }
-  const uint32_t w = (uint32_t)tid >> 6, wl = (uint32_t)tid & 63u;
+  const uint32_t lane = kMulti ? (uint32_t)tid & (uint32_t)(K - 1) : (uint32_t)tid;  // within the group of K
+  const uint32_t w = lane >> 6, wl = (uint32_t)tid & 63u;  // wave within the group of K, lane within the wave
   const uint32_t t = (w << 6) | (((uint32_t)tid & 15u) << 2) | (((uint32_t)tid >> 4) & 3u);  // substream
   const int q = tid >> 6, c = tid & 63;
   // level 1
   const __amdgpu_buffer_rsrc_t r_tab = awq_rsrc(T.bucket_table + b * 16, 64u);
   const int32_t gq = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_tab, (uint32_t)q * 4u, 0, 0);
-  const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra + first_row, (uint32_t)nr * 4u);
+  const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra + first_row, (uint32_t)(nr > 0 ? nr : 0) * 4u);
   const __amdgpu_buffer_rsrc_t r_gcol = awq_rsrc(by_scale ? T.group_col_start + ra : nullptr, by_scale ? (uint32_t)groups * 4u : 0u);
   // by-scale: groups 8 wl + w/2 and 8 (wl + 64) + w/2 (slabs wl and wl + 64); rows: rows wl and wl + 64
   const uint32_t gi0 = by_scale ? 8u * wl + (w >> 1) : wl, gi1 = by_scale ? 8u * (wl + 64u) + (w >> 1) : wl + 64u;
@@ -726,17 +750,20 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const int32_t row1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi1 * 4u, 0, 0);
   const int32_t col1 = by_scale ? (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi1 * 4u, 0, 0) : c0;
   const __amdgpu_buffer_rsrc_t r_sb = awq_rsrc(T.bucket_thread_startbit + b * (kAwqBlock + 1), (kAwqBlock + 1) * 4u);
-  const __amdgpu_buffer_rsrc_t r_ck =
-      awq_rsrc(ranged ? ckpt + wk.ckpt : nullptr, ranged ? (uint32_t)(wk.ranges - 1) * (uint32_t)kAwqBlock * 4u : 0u);
+  // kind 2: ranges - 1 checkpoint rows (between ranges); kind 3: ranges + 1 (the ends too)
+  const uint32_t ck_rows = !ranged ? 0u : kMulti ? (uint32_t)wk.ranges + 1u : (uint32_t)wk.ranges - 1u;
+  const __amdgpu_buffer_rsrc_t r_ck = awq_rsrc(ranged ? ckpt + wk.ckpt : nullptr, ck_rows * (uint32_t)K * 4u);
   // one unconditional load each from the chosen array (a load under a branch is
   // waited for where the branch joins, which would serialise the set-up's loads)
-  const bool from_ck = ranged && wk.range > 0, to_ck = ranged && wk.range + 1 < wk.ranges;
+  const bool from_ck = ranged && (kMulti || wk.range > 0), to_ck = ranged && (kMulti || wk.range + 1 < wk.ranges);
   const __amdgpu_buffer_rsrc_t r_pos = from_ck ? r_ck : r_sb;
   const __amdgpu_buffer_rsrc_t r_end = to_ck ? r_ck : r_sb;
+  const uint32_t ck0 = kMulti ? (uint32_t)range : (uint32_t)(wk.range - 1);  // checkpoint row of the range's start
+  const uint32_t live = kMulti && nr <= 0 ? kSlabBsPast : 0u;               // spare groups load nothing
   const uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(
-      r_pos, from_ck ? ((uint32_t)(wk.range - 1) * (uint32_t)kAwqBlock + t) * 4u : t * 4u, 0, 0);
+      r_pos, live | (from_ck ? ((ck0 << ks) + t) * 4u : t * 4u), 0, 0);
   const uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(
-      r_end, to_ck ? ((uint32_t)wk.range * (uint32_t)kAwqBlock + t) * 4u : (t + 1u) * 4u, 0, 0);
+      r_end, live | (to_ck ? (((ck0 + 1u) << ks) + t) * 4u : (t + 1u) * 4u), 0, 0);
   const uint64_t bucket_bit = (uint64_t)T.bucket_bit_base[b];
   // level 2
   const bool tab_ok = gq >= 0 && gq < T.num_tables;
@@ -814,7 +841,7 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   {
     const uint32_t wf = (__builtin_amdgcn_ballot_w64(bad_row) ? 1u : 0u) |
                         (__builtin_amdgcn_ballot_w64(esc_seen != 0u) ? 2u : 0u);
-    if (wl == 0) s_wflag[w] = wf;
+    if (wl == 0) s_wflag[tid >> 6] = wf;  // one word per wave of the workgroup
   }
   __syncthreads();
   uint32_t bflags = 0;
@@ -833,9 +860,19 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const uint32_t count = by_scale ? (uint32_t)groups / 8u + ((w >> 1) < ((uint32_t)groups & 7u) ? 1u : 0u)
                                   : (uint32_t)nr * P;
   const bool esc = (bflags & 2u) != 0u;
-#define MPS_AWQ_SLAB(ESC, LAY)                                                                                   \
-  awq_slab_decode<ESC, LAY>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)nr, P, bucket_bit, \
-                            first, pos, pos_end, status)
+  if constexpr (kMulti) {
+    if (nr <= 0) return;  // a spare group
+    if (esc)
+      awq_slab_decode<true, kLayRows, 0>(T, lut, region, (uint32_t)tid, lane, ks, count, base_lo, base_hi,
+                                         (uint32_t)nr, P, bucket_bit, first, pos, pos_end, status);
+    else
+      awq_slab_decode<false, kLayRows, 0>(T, lut, region, (uint32_t)tid, lane, ks, count, base_lo, base_hi,
+                                          (uint32_t)nr, P, bucket_bit, first, pos, pos_end, status);
+    return;
+  }
+#define MPS_AWQ_SLAB(ESC, LAY)                                                                               \
+  awq_slab_decode<ESC, LAY>(T, lut, region, (uint32_t)tid, (uint32_t)tid, 10u, count, base_lo, base_hi,       \
+                            (uint32_t)nr, P, bucket_bit, first, pos, pos_end, status)
   if (by_scale) {
     if (esc) MPS_AWQ_SLAB(true, kLayGroups);
     else MPS_AWQ_SLAB(false, kLayGroups);
@@ -913,25 +950,27 @@ __device__ __forceinline__ void awq_slab_bucket_wave(const mps_awq_tensor &T, in
   }
   const uint32_t count = (uint32_t)groups / 8u + ((w >> 1) < ((uint32_t)groups & 7u) ? 1u : 0u);
   if (run_flags & 2u)
-    awq_slab_decode<true, kLayGroups>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)groups, 0u,
-                                      bucket_bit, first, pos, pos_end, status);
+    awq_slab_decode<true, kLayGroups>(T, lut, region, (uint32_t)tid, (uint32_t)tid, 10u, count, base_lo, base_hi,
+                                      (uint32_t)groups, 0u, bucket_bit, first, pos, pos_end, status);
   else
-    awq_slab_decode<false, kLayGroups>(T, lut, region, (uint32_t)tid, count, base_lo, base_hi, (uint32_t)groups, 0u,
-                                       bucket_bit, first, pos, pos_end, status);
+    awq_slab_decode<false, kLayGroups>(T, lut, region, (uint32_t)tid, (uint32_t)tid, 10u, count, base_lo, base_hi,
+                                       (uint32_t)groups, 0u, bucket_bit, first, pos, pos_end, status);
 }
 
 // Lane checkpoints of a slab-path row bucket split into row ranges: where each
 // substream stands at the first row of every range after the first, found by
 // walking it through the code lengths once (the int4 value picks the table, the
 // next 11 bits the length nibble; a nibble of 15 is an 11-bit ESC code and 16
-// raw bits). One workgroup per bucket to split; lane t walks substream t, whose
-// element (row r, block p) is column c0 + t + 1024 p of the bucket's row r. A row
-// index or table id out of range stops the walk and marks the job failed (the
-// plan then keeps the bucket whole, and its decode reports them).
+// raw bits). One workgroup per bucket to split; lane t < k walks substream t,
+// whose element (row r, block p) is column c0 + t + k p of the bucket's row r. A
+// row index or table id out of range stops the walk and marks the job failed
+// (the plan then keeps the bucket whole, and its decode reports them). A `full`
+// job (ranges side by side, k 256 or 512) also writes rows 0 (the substreams'
+// start bits) and `ranges` (their end bits).
 struct AwqSplitJob {
   int32_t tensor, bucket, P, rows;
-  int32_t c0, range_rows, ranges, pad;
-  int64_t out;  // first u32 of the job's checkpoints: [ranges - 1][1024]
+  int32_t c0, range_rows, ranges, full;
+  int64_t out;  // first u32 of the job's checkpoints: [ranges - 1][k], or [ranges + 1][k] when full
 };
 
 __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tensor *__restrict__ tensors,
@@ -960,9 +999,17 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
   const bool empty = T.bitstream_words <= 0;
   const uint32_t *__restrict__ bs32 = empty ? g_awq_zero_chunks : reinterpret_cast<const uint32_t *>(T.bitstream);
   const uint64_t nchunks = empty ? 2u : (uint64_t)T.bitstream_words * 2u;
+  const int32_t K = (int32_t)T.k;
+  if (tid >= K) return;
   const uint64_t bit_base = (uint64_t)T.bucket_bit_base[J.bucket];
   const int32_t ra = T.bucket_row_offsets[J.bucket];
-  uint64_t pos = bit_base + T.bucket_thread_startbit[(int64_t)J.bucket * (kAwqBlock + 1) + tid];
+  const uint32_t *sb = T.bucket_thread_startbit + (int64_t)J.bucket * (K + 1);
+  const int64_t row0 = J.out - (J.full ? 0 : K);  // where checkpoint row 0 would go
+  if (J.full) {
+    ckpt[row0 + tid] = sb[tid];
+    ckpt[row0 + (int64_t)J.ranges * K + tid] = sb[tid + 1];
+  }
+  uint64_t pos = bit_base + sb[tid];
   uint64_t cidx = ~0ull;
   uint32_t ca = 0, cb = 0;
   for (int j = 1; j < J.ranges; ++j) {
@@ -974,7 +1021,7 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
       }
       const uint8_t *qrow = T.int4 + (int64_t)row * T.m + J.c0 + tid;
       for (int32_t p = 0; p < J.P; ++p) {
-        const uint32_t q = qrow[(int64_t)p * kAwqBlock] & 15u;
+        const uint32_t q = qrow[(int64_t)p * K] & 15u;
         const uint64_t c = pos >> 5;
         if (c != cidx) {
           cidx = c;
@@ -986,7 +1033,7 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
         pos += nib == 15u ? (uint64_t)kAwqEscLow : (uint64_t)nib;
       }
     }
-    ckpt[J.out + (int64_t)(j - 1) * kAwqBlock + tid] = (uint32_t)(pos - bit_base);
+    ckpt[row0 + (int64_t)j * K + tid] = (uint32_t)(pos - bit_base);
   }
 }
 
@@ -999,10 +1046,11 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
 // workgroup per CU).
 // out_delta: elements every tensor's output moves by (a plan decoding into a
 // buffer laid out like, but other than, the one it was created with).
-// kRanges: the plan has row ranges (kind 2 records). Plans without them launch
-// the instantiation that leaves the range path out: its code in the same kernel
-// measured 4.6% slower on a by-scale layer.
-template <bool kRanges>
+// kRanges: bit 0, the plan has row ranges (kind 2 records); bit 1, row ranges
+// side by side (kind 3). Plans without them launch the instantiation that
+// leaves that path out: the range path's code in the same kernel measured 4.6%
+// slower on a by-scale layer.
+template <int kRanges>
 __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
                                                              const AwqWork *__restrict__ work,
                                                              const uint32_t *__restrict__ ckpt, uint32_t *status,
@@ -1023,16 +1071,22 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tenso
     for (int r = 0; r < wk.nsub; ++r) {
       const int64_t b = (int64_t)wk.bucket + r;
       if ((run_flags & kRunTables) == 0u) {
-        awq_slab_bucket<false>(T, wk, b, true, run_flags, ckpt, lut, s_base, status);
+        awq_slab_bucket<0>(T, wk, b, true, run_flags, ckpt, lut, s_base, status);
       } else {
         awq_slab_bucket_wave(T, b, run_flags, lut, s_base, status);
       }
     }
     return;
   }
-  if constexpr (kRanges) {
+  if constexpr ((kRanges & 1) != 0) {
     if (wk.kind == 2) {
-      awq_slab_bucket<true>(T, wk, wk.bucket, true, run_flags, ckpt, lut, s_base, status);
+      awq_slab_bucket<1>(T, wk, wk.bucket, true, run_flags, ckpt, lut, s_base, status);
+      return;
+    }
+  }
+  if constexpr ((kRanges & 2) != 0) {
+    if (wk.kind == 3) {
+      awq_slab_bucket<2>(T, wk, wk.bucket, true, run_flags, ckpt, lut, s_base, status);
       return;
     }
   }
@@ -1149,7 +1203,7 @@ struct mps_awq_plan {
   AwqWork *d_work = nullptr;
   uint32_t *d_ckpt = nullptr;  // lane checkpoints of the row buckets split into ranges
   int64_t splits = 0;          // row buckets split into ranges
-  bool has_ranges = false;     // some work record is a row range (kind 2)
+  int ranges_mode = 0;         // bit 0: some work record is a row range (kind 2); bit 1: ranges side by side (kind 3)
 };
 
 extern "C" {
@@ -1210,7 +1264,9 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
 #define MPS_AWQ_RUN_DIV 1
 #endif
   const int64_t run_cap = std::max<int64_t>(1, all_elems / (MPS_AWQ_RUN_DIV * (int64_t)std::max(cus, 1)));
-  std::vector<int32_t> rows_of_rec, p_of_rec, c0_of_rec;  // row-layout slab records: rows, P, column start
+  // row-layout slab records: rows, P, column start; k for the records of
+  // buckets whose ranges may run side by side (0: others)
+  std::vector<int32_t> rows_of_rec, p_of_rec, c0_of_rec, k_of_rec;
   const char *slab_env = std::getenv("MPSERVE_AWQ_SLAB");
   const bool slab_on = !(slab_env && slab_env[0] == '0');
   int64_t total = 0;
@@ -1239,7 +1295,13 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
       MPS_HIP_CHECK(hipMemcpy(gcol.data(), T.group_col_start, sizeof(int32_t) * T.num_row_indices, hipMemcpyDefault));
       slab_tensor = std::all_of(gcol.begin(), gcol.end(), [](int32_t c) { return (c & 3) == 0; });
     }
-    if (slab_tensor && !T.group_col_start) {
+    // Row buckets with k 256 or 512 and P = col_len / k a multiple of 4: the
+    // slab path at stride k, with 1024 / k row ranges side by side a record
+    // (kind 3), else a bucket fills only k of the 1024 work-items.
+    const bool multi_tensor = slab_on && (T.k == 256 || T.k == 512) && !T.group_col_start && T.m % 4 == 0 &&
+                              (reinterpret_cast<uintptr_t>(T.int4) & 3u) == 0 &&
+                              (reinterpret_cast<uintptr_t>(T.out) & 7u) == 0;
+    if ((slab_tensor || multi_tensor) && !T.group_col_start) {
       cst.resize((size_t)B);
       MPS_HIP_CHECK(hipMemcpy(cst.data(), T.bucket_col_start, sizeof(int32_t) * B, hipMemcpyDefault));
     }
@@ -1260,6 +1322,13 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
                      clen[(size_t)bb] % kAwqBlock == 0 && cst[(size_t)bb] >= 0 && (cst[(size_t)bb] & 3) == 0 &&
                      (int64_t)cst[(size_t)bb] + clen[(size_t)bb] <= T.m);
       return shape && roff[(size_t)bb] >= 0 && roff[(size_t)bb + 1] <= T.num_row_indices;
+    };
+    auto multi_ok = [&](int64_t bb) {
+      const int64_t kk = T.k;
+      return multi_tensor && rows_of(bb) >= 1 && rows_of(bb) <= 128 && clen[(size_t)bb] >= 4 * kk &&
+             clen[(size_t)bb] % (4 * kk) == 0 && cst[(size_t)bb] >= 0 && (cst[(size_t)bb] & 3) == 0 &&
+             (int64_t)cst[(size_t)bb] + clen[(size_t)bb] <= T.m && roff[(size_t)bb] >= 0 &&
+             roff[(size_t)bb + 1] <= T.num_row_indices;
     };
     auto same_tables = [&](int64_t x, int64_t y) {
       return std::equal(btab.begin() + x * 16, btab.begin() + x * 16 + 16, btab.begin() + y * 16);
@@ -1282,12 +1351,25 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
         rows_of_rec.push_back(T.group_col_start ? 0 : (int32_t)rows_of(b));
         p_of_rec.push_back(T.group_col_start ? 0 : clen[(size_t)b] / kAwqBlock);
         c0_of_rec.push_back(T.group_col_start ? 0 : cst[(size_t)b]);
+        k_of_rec.push_back(0);
         b += run;
+        continue;
+      }
+      if (multi_ok(b)) {
+        // a per-lane record (kind 0), replaced by side-by-side ranges once its
+        // checkpoint walk succeeds
+        base.push_back(AwqWork{(int32_t)i, (int32_t)b, 1, 0, 0, 0, 1, 0, 0, elems_of(b)});
+        rows_of_rec.push_back((int32_t)rows_of(b));
+        p_of_rec.push_back((int32_t)(clen[(size_t)b] / T.k));
+        c0_of_rec.push_back(cst[(size_t)b]);
+        k_of_rec.push_back((int32_t)T.k);
+        ++b;
         continue;
       }
       int64_t nsub = 1, elems = elems_of(b);
       if (rows_of(b) <= row_cap) {
-        while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap && same_tables(b, b + nsub)) {
+        while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap && !multi_ok(b + nsub) &&
+               same_tables(b, b + nsub)) {
           elems += elems_of(b + nsub);
           total += elems_of(b + nsub);
           ++nsub;
@@ -1297,12 +1379,16 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
       rows_of_rec.push_back(0);
       p_of_rec.push_back(0);
       c0_of_rec.push_back(0);
+      k_of_rec.push_back(0);
       b += nsub;
     }
   }
   // Row ranges: a slab-path row bucket with more than total / (2 * CUs) elements
   // is split into row ranges of at least 64 elements a lane, each started from
   // lane checkpoints that one walk over the bucket's substreams finds.
+  // A bucket with k 256 or 512 (k_of_rec) is always cut, into up to 1024 / k
+  // ranges a record (one record per total / (2 * CUs) elements), which share
+  // the record's set-up.
   const int64_t target = std::max<int64_t>(1, total / (2 * (int64_t)std::max(cus, 1)));
   std::vector<AwqSplitJob> jobs;
   std::vector<size_t> job_rec;  // the base record each job splits
@@ -1310,6 +1396,17 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   for (size_t r = 0; r < base.size(); ++r) {
     const AwqWork &w = base[r];
     const int32_t rows = rows_of_rec[r], P = p_of_rec[r];
+    if (k_of_rec[r] > 0) {
+      const int64_t S = kAwqBlock / k_of_rec[r];
+      const int64_t recs = std::max<int64_t>(1, (w.elems + target - 1) / target);
+      int64_t ranges = std::min<int64_t>(rows, S * recs);
+      const int32_t rr = (int32_t)((rows + ranges - 1) / ranges);
+      ranges = (rows + rr - 1) / rr;
+      jobs.push_back(AwqSplitJob{w.tensor, w.bucket, P, rows, c0_of_rec[r], rr, (int32_t)ranges, 1, ck_words});
+      job_rec.push_back(r);
+      ck_words += (ranges + 1) * k_of_rec[r];
+      continue;
+    }
     if (w.kind != 1 || rows < 2 || w.elems <= target) continue;
     const int64_t want = (w.elems + target - 1) / target;
     int32_t rr = (int32_t)((rows + want - 1) / want);
@@ -1331,6 +1428,16 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
         continue;
       }
       const AwqSplitJob &J = jobs[(size_t)split_of[r]];
+      if (J.full) {
+        // 1024 / k ranges a record; the cost: one range's elements a work-item, x 1024
+        const int32_t S = kAwqBlock / k_of_rec[r];
+        for (int32_t g = 0; g < J.ranges; g += S) {
+          const int32_t nrows = std::min(J.range_rows, J.rows - g * J.range_rows);
+          out.push_back(AwqWork{J.tensor, J.bucket, 1, 3, g, J.range_rows, J.ranges, 0, J.out,
+                                (int64_t)nrows * J.P * kAwqBlock});
+        }
+        continue;
+      }
       for (int32_t g = 0; g < J.ranges; ++g) {
         const int32_t nrows = std::min(J.range_rows, J.rows - g * J.range_rows);
         out.push_back(AwqWork{J.tensor, J.bucket, 1, 2, g, J.range_rows, J.ranges, 0, J.out,
@@ -1390,21 +1497,24 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     return hip_fail(e, "mps_awq_plan_create");
   }
   plan->splits = (int64_t)jobs.size();
-  plan->has_ranges = std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.kind == 2; });
+  plan->ranges_mode = (std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.kind == 2; }) ? 1 : 0) |
+                      (std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.kind == 3; }) ? 2 : 0);
   *plan_out = plan;
   return MPS_OK;
 }
 
 static int awq_plan_launch(mps_awq_plan *plan, int64_t out_delta, uint32_t *status, void *stream) {
   if (plan->nwork == 0) return MPS_OK;
-  if (plan->has_ranges)
-    hipLaunchKernelGGL(awq_decode_plan<true>, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
-                       reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_ckpt, status,
-                       out_delta);
-  else
-    hipLaunchKernelGGL(awq_decode_plan<false>, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0,
-                       reinterpret_cast<hipStream_t>(stream), plan->d_tensors, plan->d_work, plan->d_ckpt, status,
-                       out_delta);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0, reinterpret_cast<hipStream_t>(stream),
+                       plan->d_tensors, plan->d_work, plan->d_ckpt, status, out_delta);
+  };
+  switch (plan->ranges_mode) {
+    case 0: launch(awq_decode_plan<0>); break;
+    case 1: launch(awq_decode_plan<1>); break;
+    case 2: launch(awq_decode_plan<2>); break;
+    default: launch(awq_decode_plan<3>); break;
+  }
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }

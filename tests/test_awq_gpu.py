@@ -351,6 +351,66 @@ def test_plan_slab_path_matches_input_and_the_lane_path(by_scale, n, m, cap, see
     assert torch.equal(outs["1"].view(torch.uint16), outs["0"].view(torch.uint16))
 
 
+@pytest.mark.parametrize(
+    "k,n,m,seed",
+    [(256, 2048, 4096, 730), (512, 512, 14336, 731), (256, 512, 14336, 732), (256, 300, 1024, 733),
+     (512, 96, 2048, 734)],
+    ids=["k256_p16", "k512_p28", "k256_p56", "k256_p4", "k512_p4"])
+def test_plan_rows_k256_k512_ranges_side_by_side(k, n, m, seed, monkeypatch):
+    """Row buckets with k = 256 or 512 and P = col_len / k a multiple of 4 decode on
+    the slab path at stride k, 1024 / k row ranges side by side in a record (from
+    a full set of lane checkpoints; a last record may hold fewer ranges than
+    groups). Bit-exact to the input and equal to the per-lane path's output."""
+    print(f"[awq] rows side by side k {k} {n}x{m}", flush=True)
+    w = make_awq_weight(n, m, None, seed=seed, device=DEV)
+    sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, k, 1024, False, with_stats=True)
+    assert st["esc_collisions"] == 0
+    outs = {}
+    for slab in ("1", "0"):
+        monkeypatch.setenv("MPSERVE_AWQ_SLAB", slab)
+        out = torch.empty((n, m), dtype=torch.bfloat16, device=DEV)
+        plan = awq.AwqDecodePlan([(w.int4_u8, sc, out)])
+        plan.read_status()
+        for _ in range(2):
+            out.zero_()
+            plan.decode()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)), slab
+        assert plan.read_status() == 0
+        plan.close()
+        outs[slab] = out
+    assert torch.equal(outs["1"].view(torch.uint16), outs["0"].view(torch.uint16))
+    # the op: whole buckets on the first call, the sidecar's cached plan from the second
+    monkeypatch.setenv("MPSERVE_AWQ_SLAB", "1")
+    read_status(torch.device(DEV))
+    for _ in range(3):
+        got = _op_call(sc, w, n, m, None)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.uint16), w.bf16.view(torch.uint16))
+    assert read_status(torch.device(DEV)) == 0
+
+
+def test_plan_mixes_both_range_kinds(monkeypatch):
+    """One plan over a k = 1024 row tensor (its buckets split into row ranges) and
+    a k = 256 row tensor (ranges side by side) launches the kernel with both
+    range paths; both decode bit-exact."""
+    monkeypatch.setenv("MPSERVE_AWQ_SLAB", "1")
+    a = make_awq_weight(1024, 4096, None, seed=740, device=DEV)
+    b = make_awq_weight(512, 4096, None, seed=741, device=DEV)
+    sa = awq.build_awq_sidecar(a.bf16, a.int4_u8, a.scale_u16, 11, 1024, 1024, False)
+    sb = awq.build_awq_sidecar(b.bf16, b.int4_u8, b.scale_u16, 11, 256, 1024, False)
+    oa = torch.empty((1024, 4096), dtype=torch.bfloat16, device=DEV)
+    ob = torch.empty((512, 4096), dtype=torch.bfloat16, device=DEV)
+    plan = awq.AwqDecodePlan([(a.int4_u8, sa, oa), (b.int4_u8, sb, ob)])
+    plan.read_status()
+    plan.decode()
+    torch.cuda.synchronize()
+    assert torch.equal(oa.view(torch.uint16), a.bf16.view(torch.uint16))
+    assert torch.equal(ob.view(torch.uint16), b.bf16.view(torch.uint16))
+    assert plan.read_status() == 0
+    plan.close()
+
+
 def _op_call(sc, w, n, m, group, out=None):
     if "bucket_group_offsets_i32" in sc:
         return MPServe_cuda.huffman_decode_awq_int4_bucket_by_scale(
