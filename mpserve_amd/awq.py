@@ -202,17 +202,19 @@ def _launch(int4, bitstream, syms, lens, table, col_start, col_len, offsets, row
     if n * m >= (1 << 31):
         raise ValueError("tensor too large for the AWQ decode kernel (n*m >= 2^31)")
     # From its second call on a sidecar that the slab path can take (k = 1024: by-scale
-    # with 128-column groups, or row buckets; k = 256 or 512: row buckets, whose rows the
-    # plan splits into ranges decoded side by side, when m is a multiple of 4k) the op
-    # launches the sidecar's cached plan; other sidecars (whose plans would take the
-    # per-lane path, slower than this kernel's two workgroups per bucket when a tensor
-    # has fewer buckets than CUs) and the first call decode over whole buckets, as the
-    # reference does.
+    # with 128-column groups, or row buckets; k = 256 or 512: by-scale with 128-column
+    # groups, or row buckets when m is a multiple of 4k, whose buckets the plan splits
+    # into ranges decoded side by side) the op launches the sidecar's cached plan; other
+    # sidecars (whose plans would take the per-lane path, slower than this kernel's two
+    # workgroups per bucket when a tensor has fewer buckets than CUs) and the first call
+    # decode over whole buckets, as the reference does.
     key_tensors = tuple(t for t in (int4, bitstream, syms, lens, table, col_start, col_len, offsets, rows, group_col,
                                     startbit, bit_base) if t is not None)
     k = startbit.size(1) - 1
-    slab = (k == 1024 and (group_col is None or int(group_size) == 128)) or \
-        (group_col is None and k in (256, 512) and m % (4 * k) == 0)
+    if group_col is None:
+        slab = k == 1024 or (k in (256, 512) and m % (4 * k) == 0)
+    else:
+        slab = k in (256, 512, 1024) and int(group_size) == 128
     with torch.cuda.device(dev):
         stream = _stream_handle(dev)
         plan = None

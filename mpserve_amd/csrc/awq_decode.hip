@@ -402,7 +402,7 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   constexpr int FE = MPS_AWQ_FEED_EVERY;     // steps per bitstream feed (16 bytes: 2 x 44 bits fit)
   static_assert(DF % FE == 0 && (FE == 1 || FE == 2), "a feed every one or two steps");
   constexpr int RB = 4;  // 16-byte blocks per bitstream request
-  static_assert(kShift == 10 || (kShift == 0 && kLay == kLayRows), "k < 1024: row buckets with P % 4 == 0");
+  static_assert(kShift == 10 || (kShift == 0 && kLay != kLayRowsWrap), "k < 1024: no steps across rows");
   count = awq_uni(count);
   kshift = kShift ? (uint32_t)kShift : awq_uni(kshift);
   bucket_bit = ((uint64_t)awq_uni((uint32_t)(bucket_bit >> 32)) << 32) | awq_uni((uint32_t)bucket_bit);
@@ -711,7 +711,7 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const int32_t K = kMulti ? (int32_t)T.k : kAwqBlock;  // substreams (the block stride)
   const uint32_t ks = K == 256 ? 8u : K == 512 ? 9u : 10u;
   const bool shape_ok =
-      by_scale ? (!kMulti && groups >= kSlabMinGroups && groups <= kSlabMaxGroups && T.group_size == 128)
+      by_scale ? (groups >= (kMulti ? 1 : kSlabMinGroups) && groups <= kSlabMaxGroups && T.group_size == 128)
                : (groups >= 1 && groups <= 128 && cl >= 4 * K && cl % (kMulti ? 4 * K : K) == 0 && c0 >= 0 &&
                   (int64_t)c0 + cl <= T.m);
   const bool k_ok = kMulti ? (K == 256 || K == 512) : T.k == kAwqBlock;
@@ -723,13 +723,20 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   // a row range (kinds 2, 3): its first row and row count; its lanes start and
   // end at checkpoints. Kind 3: this work-item's group of K (uniform per wave)
   // and its range; a last record's spare groups have no rows and only take
-  // part in the barriers.
+  // part in the barriers. A by-scale kind 3 range is a range of slabs (K / 128
+  // groups each): [s0, s0 + ns) of the bucket's slabs.
   const bool ranged = kRanged != 0 && !by_scale;
+  const bool from_ckpt = ranged || kMulti;  // lanes start (and end) at checkpoints
   const int32_t sub = kMulti ? (int32_t)awq_uni((uint32_t)tid >> ks) : 0;
   const int32_t range = wk.range + sub;
   const int32_t first_row = ranged ? range * wk.range_rows : 0;
   const int32_t nr_all = ranged ? (groups - first_row < wk.range_rows ? groups - first_row : wk.range_rows) : groups;
-  const int32_t nr = kMulti ? (range < wk.ranges && nr_all > 0 ? nr_all : 0) : nr_all;
+  const int32_t gps = K >> 7;  // by-scale: groups per slab
+  const int32_t s0 = kMulti && by_scale ? range * wk.range_rows : 0;
+  const int32_t ns_all = (groups + gps - 1) / gps - s0;
+  const int32_t ns = kMulti && by_scale ? (ns_all < wk.range_rows ? ns_all : wk.range_rows) : 0;
+  // rows of the range (rows), or the bucket's groups (by-scale); 0 for a spare group
+  const int32_t nr = kMulti ? (range < wk.ranges && (by_scale ? ns > 0 : nr_all > 0) ? nr_all : 0) : nr_all;
   if (!kMulti && nr <= 0) {
     if (tid == 0) flag(status, MPS_STATUS_BAD_BUCKET);
     return;
@@ -743,19 +750,21 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const int32_t gq = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_tab, (uint32_t)q * 4u, 0, 0);
   const __amdgpu_buffer_rsrc_t r_grow = awq_rsrc(T.row_indices + ra + first_row, (uint32_t)(nr > 0 ? nr : 0) * 4u);
   const __amdgpu_buffer_rsrc_t r_gcol = awq_rsrc(by_scale ? T.group_col_start + ra : nullptr, by_scale ? (uint32_t)groups * 4u : 0u);
-  // by-scale: groups 8 wl + w/2 and 8 (wl + 64) + w/2 (slabs wl and wl + 64); rows: rows wl and wl + 64
-  const uint32_t gi0 = by_scale ? 8u * wl + (w >> 1) : wl, gi1 = by_scale ? 8u * (wl + 64u) + (w >> 1) : wl + 64u;
+  // by-scale: groups gps (s0 + wl) + w/2 and gps (s0 + wl + 64) + w/2 (slabs s0 + wl and s0 + wl + 64);
+  // rows: rows wl and wl + 64
+  const uint32_t gi0 = by_scale ? (uint32_t)gps * ((uint32_t)s0 + wl) + (w >> 1) : wl;
+  const uint32_t gi1 = by_scale ? (uint32_t)gps * ((uint32_t)s0 + wl + 64u) + (w >> 1) : wl + 64u;
   const int32_t row0 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi0 * 4u, 0, 0);
   const int32_t col0 = by_scale ? (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi0 * 4u, 0, 0) : c0;
   const int32_t row1 = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_grow, gi1 * 4u, 0, 0);
   const int32_t col1 = by_scale ? (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r_gcol, gi1 * 4u, 0, 0) : c0;
   const __amdgpu_buffer_rsrc_t r_sb = awq_rsrc(T.bucket_thread_startbit + b * (kAwqBlock + 1), (kAwqBlock + 1) * 4u);
   // kind 2: ranges - 1 checkpoint rows (between ranges); kind 3: ranges + 1 (the ends too)
-  const uint32_t ck_rows = !ranged ? 0u : kMulti ? (uint32_t)wk.ranges + 1u : (uint32_t)wk.ranges - 1u;
-  const __amdgpu_buffer_rsrc_t r_ck = awq_rsrc(ranged ? ckpt + wk.ckpt : nullptr, ck_rows * (uint32_t)K * 4u);
+  const uint32_t ck_rows = !from_ckpt ? 0u : kMulti ? (uint32_t)wk.ranges + 1u : (uint32_t)wk.ranges - 1u;
+  const __amdgpu_buffer_rsrc_t r_ck = awq_rsrc(from_ckpt ? ckpt + wk.ckpt : nullptr, ck_rows * (uint32_t)K * 4u);
   // one unconditional load each from the chosen array (a load under a branch is
   // waited for where the branch joins, which would serialise the set-up's loads)
-  const bool from_ck = ranged && (kMulti || wk.range > 0), to_ck = ranged && (kMulti || wk.range + 1 < wk.ranges);
+  const bool from_ck = from_ckpt && (kMulti || wk.range > 0), to_ck = from_ckpt && (kMulti || wk.range + 1 < wk.ranges);
   const __amdgpu_buffer_rsrc_t r_pos = from_ck ? r_ck : r_sb;
   const __amdgpu_buffer_rsrc_t r_end = to_ck ? r_ck : r_sb;
   const uint32_t ck0 = kMulti ? (uint32_t)range : (uint32_t)(wk.range - 1);  // checkpoint row of the range's start
@@ -862,6 +871,18 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const bool esc = (bflags & 2u) != 0u;
   if constexpr (kMulti) {
     if (nr <= 0) return;  // a spare group
+    if (by_scale) {
+      // this wave's slabs in the range: those whose group gps i + w/2 exists
+      const int32_t cw = groups > (int32_t)(w >> 1) ? (groups - (int32_t)(w >> 1) + gps - 1) / gps : 0;
+      const int32_t cnt = cw - s0 < 0 ? 0 : cw - s0 < ns ? cw - s0 : ns;
+      if (esc)
+        awq_slab_decode<true, kLayGroups, 0>(T, lut, region, (uint32_t)tid, lane, ks, (uint32_t)cnt, base_lo,
+                                             base_hi, (uint32_t)groups, 0u, bucket_bit, first, pos, pos_end, status);
+      else
+        awq_slab_decode<false, kLayGroups, 0>(T, lut, region, (uint32_t)tid, lane, ks, (uint32_t)cnt, base_lo,
+                                              base_hi, (uint32_t)groups, 0u, bucket_bit, first, pos, pos_end, status);
+      return;
+    }
     if (esc)
       awq_slab_decode<true, kLayRows, 0>(T, lut, region, (uint32_t)tid, lane, ks, count, base_lo, base_hi,
                                          (uint32_t)nr, P, bucket_bit, first, pos, pos_end, status);
@@ -966,7 +987,8 @@ __device__ __forceinline__ void awq_slab_bucket_wave(const mps_awq_tensor &T, in
 // row index or table id out of range stops the walk and marks the job failed
 // (the plan then keeps the bucket whole, and its decode reports them). A `full`
 // job (ranges side by side, k 256 or 512) also writes rows 0 (the substreams'
-// start bits) and `ranges` (their end bits).
+// start bits) and `ranges` (their end bits). A by-scale job's ranges are ranges
+// of slabs (`range_rows` slabs of k / 128 groups each; `rows`: the groups).
 struct AwqSplitJob {
   int32_t tensor, bucket, P, rows;
   int32_t c0, range_rows, ranges, full;
@@ -1012,6 +1034,36 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
   uint64_t pos = bit_base + sb[tid];
   uint64_t cidx = ~0ull;
   uint32_t ca = 0, cb = 0;
+  auto step = [&](uint32_t q) {  // past the code of one element with int4 value q
+    const uint64_t c = pos >> 5;
+    if (c != cidx) {
+      cidx = c;
+      ca = chunk_at(bs32, nchunks, c);
+      cb = chunk_at(bs32, nchunks, c + 1);
+    }
+    const uint32_t peek = (uint32_t)(((((uint64_t)ca << 32) | cb) << (pos & 31u)) >> (64 - kAwqL));
+    const uint32_t nib = (s_lens[q * kAwqPacked + (peek >> 1)] >> ((peek & 1u) * 4u)) & 0xFu;
+    pos += nib == 15u ? (uint64_t)kAwqEscLow : (uint64_t)nib;
+  };
+  if (T.group_col_start) {
+    // by-scale (J.rows groups of 128 columns): ranges of J.range_rows slabs of K / 128
+    // groups; substream t's element in slab i is column t % 128 of group (K / 128) i + t / 128
+    const int32_t gps = K >> 7, gsub = tid >> 7, col = tid & 127;
+    for (int j = 1; j < J.ranges; ++j) {
+      for (int32_t i = (j - 1) * J.range_rows; i < j * J.range_rows; ++i) {
+        const int32_t g = gps * i + gsub;
+        if (g >= J.rows) break;
+        const int32_t row = T.row_indices[ra + g], c0 = T.group_col_start[ra + g];
+        if (row < 0 || row >= T.n || c0 < 0 || (int64_t)c0 + 128 > T.m) {
+          failed[blockIdx.x] = 1u;
+          return;
+        }
+        step(T.int4[(int64_t)row * T.m + c0 + col] & 15u);
+      }
+      ckpt[row0 + (int64_t)j * K + tid] = (uint32_t)(pos - bit_base);
+    }
+    return;
+  }
   for (int j = 1; j < J.ranges; ++j) {
     for (int32_t r = (j - 1) * J.range_rows; r < j * J.range_rows; ++r) {
       const int32_t row = T.row_indices[ra + r];
@@ -1020,18 +1072,7 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
         return;
       }
       const uint8_t *qrow = T.int4 + (int64_t)row * T.m + J.c0 + tid;
-      for (int32_t p = 0; p < J.P; ++p) {
-        const uint32_t q = qrow[(int64_t)p * K] & 15u;
-        const uint64_t c = pos >> 5;
-        if (c != cidx) {
-          cidx = c;
-          ca = chunk_at(bs32, nchunks, c);
-          cb = chunk_at(bs32, nchunks, c + 1);
-        }
-        const uint32_t peek = (uint32_t)(((((uint64_t)ca << 32) | cb) << (pos & 31u)) >> (64 - kAwqL));
-        const uint32_t nib = (s_lens[q * kAwqPacked + (peek >> 1)] >> ((peek & 1u) * 4u)) & 0xFu;
-        pos += nib == 15u ? (uint64_t)kAwqEscLow : (uint64_t)nib;
-      }
+      for (int32_t p = 0; p < J.P; ++p) step(qrow[(int64_t)p * K] & 15u);
     }
     ckpt[row0 + (int64_t)j * K + tid] = (uint32_t)(pos - bit_base);
   }
@@ -1290,10 +1331,17 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     // 4-element boundary and the buffers must be aligned to match.
     bool slab_tensor = slab_on && T.k == kAwqBlock && (!T.group_col_start || T.group_size == 128) && T.m % 4 == 0 &&
                        (reinterpret_cast<uintptr_t>(T.int4) & 3u) == 0 && (reinterpret_cast<uintptr_t>(T.out) & 7u) == 0;
-    if (slab_tensor && T.group_col_start && T.num_row_indices > 0) {
+    // By-scale sidecars with k 256 or 512 and 128-column groups: buckets cut into
+    // ranges of slabs (k / 128 groups each), 1024 / k ranges side by side a record.
+    bool bmulti_tensor = slab_on && (T.k == 256 || T.k == 512) && T.group_col_start && T.group_size == 128 &&
+                         T.m % 4 == 0 && (reinterpret_cast<uintptr_t>(T.int4) & 3u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(T.out) & 7u) == 0;
+    if ((slab_tensor || bmulti_tensor) && T.group_col_start && T.num_row_indices > 0) {
       gcol.resize((size_t)T.num_row_indices);
       MPS_HIP_CHECK(hipMemcpy(gcol.data(), T.group_col_start, sizeof(int32_t) * T.num_row_indices, hipMemcpyDefault));
-      slab_tensor = std::all_of(gcol.begin(), gcol.end(), [](int32_t c) { return (c & 3) == 0; });
+      const bool aligned = std::all_of(gcol.begin(), gcol.end(), [](int32_t c) { return (c & 3) == 0; });
+      slab_tensor = slab_tensor && aligned;
+      bmulti_tensor = bmulti_tensor && aligned;
     }
     // Row buckets with k 256 or 512 and P = col_len / k a multiple of 4: the
     // slab path at stride k, with 1024 / k row ranges side by side a record
@@ -1325,10 +1373,13 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     };
     auto multi_ok = [&](int64_t bb) {
       const int64_t kk = T.k;
+      if (roff[(size_t)bb] < 0 || roff[(size_t)bb + 1] > T.num_row_indices) return false;
+      // by-scale: at least 32 slabs (below that the set-up outweighs the decode, and
+      // runs of same-scale buckets on the per-lane path share one set-up)
+      if (T.group_col_start) return bmulti_tensor && rows_of(bb) >= 32 * (kk / 128) && rows_of(bb) <= kSlabMaxGroups;
       return multi_tensor && rows_of(bb) >= 1 && rows_of(bb) <= 128 && clen[(size_t)bb] >= 4 * kk &&
              clen[(size_t)bb] % (4 * kk) == 0 && cst[(size_t)bb] >= 0 && (cst[(size_t)bb] & 3) == 0 &&
-             (int64_t)cst[(size_t)bb] + clen[(size_t)bb] <= T.m && roff[(size_t)bb] >= 0 &&
-             roff[(size_t)bb + 1] <= T.num_row_indices;
+             (int64_t)cst[(size_t)bb] + clen[(size_t)bb] <= T.m;
     };
     auto same_tables = [&](int64_t x, int64_t y) {
       return std::equal(btab.begin() + x * 16, btab.begin() + x * 16 + 16, btab.begin() + y * 16);
@@ -1359,9 +1410,9 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
         // a per-lane record (kind 0), replaced by side-by-side ranges once its
         // checkpoint walk succeeds
         base.push_back(AwqWork{(int32_t)i, (int32_t)b, 1, 0, 0, 0, 1, 0, 0, elems_of(b)});
-        rows_of_rec.push_back((int32_t)rows_of(b));
-        p_of_rec.push_back((int32_t)(clen[(size_t)b] / T.k));
-        c0_of_rec.push_back(cst[(size_t)b]);
+        rows_of_rec.push_back((int32_t)rows_of(b));  // rows, or groups (by-scale: P = 0)
+        p_of_rec.push_back(T.group_col_start ? 0 : (int32_t)(clen[(size_t)b] / T.k));
+        c0_of_rec.push_back(T.group_col_start ? 0 : cst[(size_t)b]);
         k_of_rec.push_back((int32_t)T.k);
         ++b;
         continue;
@@ -1397,11 +1448,19 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     const AwqWork &w = base[r];
     const int32_t rows = rows_of_rec[r], P = p_of_rec[r];
     if (k_of_rec[r] > 0) {
+      // units: rows, or slabs of k / 128 groups (by-scale, at most 128 a range: the
+      // slab path keeps a wave's 128 group bases in two registers)
+      // More than one record only while each range keeps >= 64 elements a lane.
       const int64_t S = kAwqBlock / k_of_rec[r];
-      const int64_t recs = std::max<int64_t>(1, (w.elems + target - 1) / target);
-      int64_t ranges = std::min<int64_t>(rows, S * recs);
-      const int32_t rr = (int32_t)((rows + ranges - 1) / ranges);
-      ranges = (rows + rr - 1) / rr;
+      const int64_t gps = k_of_rec[r] / 128;
+      const int64_t units = P > 0 ? rows : (rows + gps - 1) / gps;
+      const int64_t min_units = P > 0 ? (64 + P - 1) / P : 64;
+      const int64_t recs = std::min(std::max<int64_t>(1, (w.elems + target - 1) / target),
+                                    std::max<int64_t>(1, units / (S * min_units)));
+      int64_t ranges = std::min<int64_t>(units, S * recs);
+      if (P == 0) ranges = std::max<int64_t>(ranges, (units + 127) / 128);
+      const int32_t rr = (int32_t)((units + ranges - 1) / ranges);
+      ranges = (units + rr - 1) / rr;
       jobs.push_back(AwqSplitJob{w.tensor, w.bucket, P, rows, c0_of_rec[r], rr, (int32_t)ranges, 1, ck_words});
       job_rec.push_back(r);
       ck_words += (ranges + 1) * k_of_rec[r];
@@ -1431,10 +1490,12 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
       if (J.full) {
         // 1024 / k ranges a record; the cost: one range's elements a work-item, x 1024
         const int32_t S = kAwqBlock / k_of_rec[r];
+        const int32_t gps = k_of_rec[r] / 128;
+        const int32_t units = J.P > 0 ? J.rows : (J.rows + gps - 1) / gps;
         for (int32_t g = 0; g < J.ranges; g += S) {
-          const int32_t nrows = std::min(J.range_rows, J.rows - g * J.range_rows);
+          const int32_t n = std::min(J.range_rows, units - g * J.range_rows);
           out.push_back(AwqWork{J.tensor, J.bucket, 1, 3, g, J.range_rows, J.ranges, 0, J.out,
-                                (int64_t)nrows * J.P * kAwqBlock});
+                                (int64_t)n * std::max(J.P, 1) * kAwqBlock});
         }
         continue;
       }

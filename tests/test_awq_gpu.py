@@ -390,6 +390,46 @@ def test_plan_rows_k256_k512_ranges_side_by_side(k, n, m, seed, monkeypatch):
     assert read_status(torch.device(DEV)) == 0
 
 
+@pytest.mark.parametrize(
+    "k,n,m,cap,seed",
+    [(256, 4096, 4096, 1024, 750), (512, 1024, 4096, 1024, 751), (256, 2048, 4096, 201, 752),
+     (512, 4096, 14336, 1024, 753), (256, 512, 4096, 12, 754)],
+    ids=["k256_q", "k512_kv", "k256_cap201", "k512_down", "k256_cap12_runs"])
+def test_plan_by_scale_k256_k512_slab_ranges(k, n, m, cap, seed, monkeypatch):
+    """By-scale buckets with k = 256 or 512 (and at least 32 slabs) decode on the slab
+    path in ranges of at most 128 slabs (k / 128 groups each), 1024 / k ranges side
+    by side in a record, from a full set of lane checkpoints. Group counts that are
+    not a multiple of k / 128 leave partial last slabs (cap 201); small buckets (cap
+    12) stay on the per-lane path in same-scale runs. Bit-exact to the input, equal
+    to the per-lane path's output."""
+    print(f"[awq] by-scale slab ranges k {k} {n}x{m} cap {cap}", flush=True)
+    w = make_awq_weight(n, m, 128, seed=seed, device=DEV)
+    sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, k, cap, True)
+    outs = {}
+    for slab in ("1", "0"):
+        monkeypatch.setenv("MPSERVE_AWQ_SLAB", slab)
+        out = torch.empty((n, m), dtype=torch.bfloat16, device=DEV)
+        plan = awq.AwqDecodePlan([(w.int4_u8, sc, out)])
+        plan.read_status()
+        for _ in range(2):
+            out.zero_()
+            plan.decode()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)), slab
+        assert plan.read_status() == 0
+        plan.close()
+        outs[slab] = out
+    assert torch.equal(outs["1"].view(torch.uint16), outs["0"].view(torch.uint16))
+    # the op: whole buckets on the first call, the sidecar's cached plan from the second
+    monkeypatch.setenv("MPSERVE_AWQ_SLAB", "1")
+    read_status(torch.device(DEV))
+    for _ in range(3):
+        got = _op_call(sc, w, n, m, 128)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.uint16), w.bf16.view(torch.uint16))
+    assert read_status(torch.device(DEV)) == 0
+
+
 def test_plan_mixes_both_range_kinds(monkeypatch):
     """One plan over a k = 1024 row tensor (its buckets split into row ranges) and
     a k = 256 row tensor (ranges side by side) launches the kernel with both
