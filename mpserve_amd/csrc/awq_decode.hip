@@ -1092,13 +1092,10 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
 // leaves that path out: the range path's code in the same kernel measured 4.6%
 // slower on a by-scale layer.
 template <int kRanges>
-__global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
-                                                             const AwqWork *__restrict__ work,
-                                                             const uint32_t *__restrict__ ckpt, uint32_t *status,
-                                                             int64_t out_delta) {
-  __shared__ uint32_t lut[kLutEntries];
-  __shared__ uint32_t s_base[kRowSlots];
-  const AwqWork wk = work[blockIdx.x];
+__device__ __forceinline__ void awq_plan_record(const mps_awq_tensor *__restrict__ tensors, const AwqWork &wk,
+                                                const uint32_t *__restrict__ ckpt, uint32_t *status,
+                                                int64_t out_delta, uint32_t *__restrict__ lut,
+                                                uint32_t *__restrict__ s_base) {
   const int4 w = make_int4(wk.tensor, wk.bucket, wk.nsub, wk.kind);
   mps_awq_tensor T = tensors[w.x];
   T.out += out_delta;
@@ -1206,6 +1203,43 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tenso
   else awq_lane<false>(T, lut, my_base, b, ra, c0, cl, total, k, k_eff, lane, status);
 }
 
+// Record trace, in instrumented builds only (python -m mpserve_amd.build
+// --define MPS_TRACE_ITEMS=1 --out LIB; mpserve_amd.item_trace reads it):
+// record r < kAwqTraceRecs stores the real-time clock (100 MHz) at its start
+// and after a closing barrier, kind << 32 | nsub, and its ordering key.
+#ifndef MPS_TRACE_ITEMS
+#define MPS_TRACE_ITEMS 0
+#endif
+#if MPS_TRACE_ITEMS
+constexpr int kAwqTraceRecs = 8192;
+__device__ uint64_t g_awq_trace[kAwqTraceRecs * 4];
+#endif
+
+template <int kRanges>
+__global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
+                                                             const AwqWork *__restrict__ work,
+                                                             const uint32_t *__restrict__ ckpt, uint32_t *status,
+                                                             int64_t out_delta) {
+  __shared__ uint32_t lut[kLutEntries];
+  __shared__ uint32_t s_base[kRowSlots];
+#if MPS_TRACE_ITEMS
+  const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
+#endif
+  const AwqWork wk = work[blockIdx.x];
+  awq_plan_record<kRanges>(tensors, wk, ckpt, status, out_delta, lut, s_base);
+#if MPS_TRACE_ITEMS
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0 && blockIdx.x < kAwqTraceRecs) {
+    uint64_t *tp = g_awq_trace + (size_t)blockIdx.x * 4;
+    tp[0] = tr0;
+    tp[1] = __builtin_amdgcn_s_memrealtime();
+    tp[2] = ((uint64_t)(uint32_t)wk.kind << 32) | (uint32_t)wk.nsub;
+    tp[3] = (uint64_t)wk.elems;
+  }
+#endif
+}
+
 int check_awq(const mps_awq_tensor *t) {
   if (!t) return fail(MPS_ERR_INVALID_ARGUMENT, "tensor is NULL");
   if (t->n <= 0 || t->m <= 0) return fail(MPS_ERR_INVALID_ARGUMENT, "n,m must be > 0");
@@ -1248,6 +1282,20 @@ struct mps_awq_plan {
 };
 
 extern "C" {
+
+#if MPS_TRACE_ITEMS
+// The record trace's host side (instrumented builds only; not part of the product ABI).
+int mps_awq_trace_clear(void) {
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_awq_trace)) != hipSuccess) return MPS_ERR_HIP;
+  return hipMemset(p, 0, sizeof(g_awq_trace)) == hipSuccess ? MPS_OK : MPS_ERR_HIP;
+}
+int mps_awq_trace_read(uint64_t *dst, int64_t words) {
+  if (!dst || words < (int64_t)(sizeof(g_awq_trace) / 8)) return MPS_ERR_INVALID_ARGUMENT;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_awq_trace), sizeof(g_awq_trace)) == hipSuccess ? MPS_OK : MPS_ERR_HIP;
+}
+#endif
+
 
 int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream) {
   last_error().clear();

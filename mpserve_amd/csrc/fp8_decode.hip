@@ -1377,6 +1377,21 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
 // Tickets travel in 30 bits of the set-up's flag words: a launch holds fewer
 // than kMaxQueueItems work items.
 constexpr int64_t kMaxQueueItems = (int64_t(1) << 30) - 65536;
+
+// Item trace, in instrumented builds only (python -m mpserve_amd.build --define
+// MPS_TRACE_ITEMS=1 --out LIB; mpserve_amd.item_trace reads it): workgroup g <
+// kTraceWgs records its first kTraceItems items, 4 words each: the real-time
+// clock (100 MHz) at the item's start and after its end barrier, the item's
+// path << 40 | rows << 20 | k_eff, and its col_len. Thread 0 writes them with
+// ordinary stores after the barrier.
+#ifndef MPS_TRACE_ITEMS
+#define MPS_TRACE_ITEMS 0
+#endif
+#if MPS_TRACE_ITEMS
+constexpr int kTraceWgs = 256, kTraceItems = 128;
+__device__ uint64_t g_item_trace[kTraceWgs * kTraceItems * 4];
+#endif
+
 template <bool kSlabK>
 __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *__restrict__ tensors,
                                                           const WorkItem *__restrict__ work, int64_t nwork,
@@ -1384,8 +1399,14 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   if ((int64_t)blockIdx.x < nwork) {
     WorkItem w = work[blockIdx.x];
+#if MPS_TRACE_ITEMS
+    int tr_it = 0;
+#endif
     for (;;) {
       uint32_t ticket;
+#if MPS_TRACE_ITEMS
+      const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
+#endif
       const mps_fp8_tensor &T = tensors[w.tensor];
       decode_bucket<true, kSlabK>(T, T.out + out_delta, w, lds, status, queue, ticket);
       const int64_t next = (int64_t)gridDim.x + ticket;
@@ -1393,6 +1414,16 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
       // item's stores, which covers its round trip.
       const WorkItem wn = work[next < nwork ? next : 0];
       end_bucket();
+#if MPS_TRACE_ITEMS
+      if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && tr_it < kTraceItems) {
+        uint64_t *tp = g_item_trace + ((size_t)blockIdx.x * kTraceItems + tr_it) * 4;
+        tp[0] = tr0;
+        tp[1] = __builtin_amdgcn_s_memrealtime();
+        tp[2] = ((uint64_t)(uint32_t)w.path << 40) | ((uint64_t)(uint32_t)w.rows << 20) | (uint64_t)(uint32_t)w.k_eff;
+        tp[3] = (uint64_t)(uint32_t)w.cl;
+      }
+      ++tr_it;
+#endif
       if (next >= nwork) break;
       w = wn;
     }
@@ -1696,6 +1727,21 @@ struct mps_fp8_plan {
 };
 
 extern "C" {
+
+#if MPS_TRACE_ITEMS
+// The item trace's host side (instrumented builds only; not part of the product ABI).
+int mps_item_trace_clear(void) {
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_item_trace)) != hipSuccess) return MPS_ERR_HIP;
+  return hipMemset(p, 0, sizeof(g_item_trace)) == hipSuccess ? MPS_OK : MPS_ERR_HIP;
+}
+int mps_item_trace_read(uint64_t *dst, int64_t words) {
+  if (!dst || words < (int64_t)(sizeof(g_item_trace) / 8)) return MPS_ERR_INVALID_ARGUMENT;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_item_trace), sizeof(g_item_trace)) == hipSuccess ? MPS_OK
+                                                                                                  : MPS_ERR_HIP;
+}
+#endif
+
 
 const char *mps_last_error(void) { return last_error().c_str(); }
 

@@ -32,6 +32,16 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_product_library_has_no_item_trace():
+    """The item and record traces exist only in instrumented builds
+    (--define MPS_TRACE_ITEMS=1); the product library carries none of them."""
+    from mpserve_amd import _native
+
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    for name in ("mps_item_trace_clear", "mps_item_trace_read", "mps_awq_trace_clear", "mps_awq_trace_read"):
+        assert not hasattr(lib, name), name
+
+
 def test_last_error_is_empty_string_initially():
     from mpserve_amd import _native
 
