@@ -44,10 +44,10 @@ def _weight(n, m, seed, sigma, outlier_p):
     return make_weight(n, m, sigma=sigma, seed=seed, outlier_p=outlier_p, device=DEV)
 
 
-def _gpu_build(w):
+def _gpu_build(w, k=1024):
     from mpserve_amd.encode import build_fp8_sidecar
 
-    return build_fp8_sidecar(w.bf16, w.fp8_u8, w.scale_u16, max_len=7, threads_per_block=1024, with_stats=True)
+    return build_fp8_sidecar(w.bf16, w.fp8_u8, w.scale_u16, max_len=7, threads_per_block=k, with_stats=True)
 
 
 def _assert_same_as_oracle(side, w):
@@ -130,6 +130,41 @@ def test_cfg3_layer70b(name, n, m, seed, sigma, outlier_p):
         assert (ostats["esc_elements"] > 0) == (stats["esc_keys"] > 0)
     _assert_invariants(side, n, m)
     _decode_op_and_plan(side, w)
+
+
+@pytest.mark.parametrize("k", [256, 512])
+def test_cfg2_layer8b_k256_k512_one_plan_and_op(k):
+    """Config 2 with sidecars of k = 256 / 512 substreams (the reference builder's
+    default is 256): all seven 8B linears in one plan launch, where their buckets
+    run 1024 / k row ranges side by side on the slab path at stride k, and each
+    through the op (whole buckets, then the sidecar's cached plan). Bit-exact, status
+    clean. A 70B q_proj with outliers adds ESC tables at this k."""
+    import MPServe_cuda
+    from mpserve_amd.decode import DecodePlan
+
+    items = []
+    for name, n, m, seed, sigma, outlier_p in list(CFG2) + [c for c in CFG3 if c[0] == "layers.0.q_proj"]:
+        w = _weight(n, m, seed, sigma, outlier_p)
+        side, stats = _gpu_build(w, k)
+        assert stats["esc_collisions"] == 0
+        if outlier_p > 0:
+            assert stats["esc_keys"] > 0
+        items.append((w, side))
+    _status()
+    outs = [torch.zeros_like(w.bf16) for w, _ in items]
+    plan = DecodePlan([(w.fp8_u8, side, o) for (w, side), o in zip(items, outs)])
+    plan.decode()
+    torch.cuda.synchronize()
+    for (w, _), o in zip(items, outs):
+        assert torch.equal(o.view(torch.uint16), w.bf16.view(torch.uint16))
+    assert plan.read_status() == 0
+    plan.close()
+    for w, side in items:
+        for _ in range(2):
+            out = MPServe_cuda.huffman_decode_fp8(*decode_args(side, w.fp8_u8))
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16))
+    assert _status() == 0
 
 
 def test_cfg5_model8b_all_weights_one_plan():
