@@ -430,6 +430,39 @@ def test_plan_by_scale_k256_k512_slab_ranges(k, n, m, cap, seed, monkeypatch):
     assert read_status(torch.device(DEV)) == 0
 
 
+@pytest.mark.parametrize("by_scale", [False, True])
+def test_side_by_side_ranges_with_corrupt_sidecars(by_scale, monkeypatch):
+    """k = 256 plans whose buckets would run ranges side by side, over corrupt
+    sidecars: a row index out of range (the checkpoint walk stops and the bucket
+    keeps its per-lane record), a table id out of range, shifted start bits. The
+    flags are raised and nothing is written outside the output."""
+    monkeypatch.setenv("MPSERVE_AWQ_SLAB", "1")
+    n, m = (512, 4096) if by_scale else (256, 4096)
+    w = make_awq_weight(n, m, 128 if by_scale else None, seed=760 + by_scale, device=DEV)
+    sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, 256, 1024, by_scale)
+    rows_key = "group_rows_i32" if by_scale else "row_indices_i32"
+    guard = 4096
+    for what, flag_bit in (("row", 0x2), ("table", 0x4), ("start", 0x8)):
+        bad = {key: v.clone() for key, v in sc.items()}
+        if what == "row":
+            bad[rows_key][3] = n + 1000
+        elif what == "table":
+            bad["bucket_table_i32"][0, 5] = 10 ** 8
+        else:
+            bad["bucket_thread_startbit_u32"].view(torch.int32)[0, 7] += 3  # (no uint32 add on the GPU)
+        buf = torch.zeros(n * m + 2 * guard, dtype=torch.bfloat16, device=DEV)
+        out = buf[guard:guard + n * m].view(n, m)
+        plan = awq.AwqDecodePlan([(w.int4_u8, bad, out)])
+        plan.read_status()
+        plan.decode()
+        st = plan.read_status()
+        plan.close()
+        torch.cuda.synchronize()
+        assert st & flag_bit, (what, st)
+        g = buf.view(torch.uint16)
+        assert int((g[:guard] != 0).sum()) == 0 and int((g[guard + n * m:] != 0).sum()) == 0, what
+
+
 def test_plan_mixes_both_range_kinds(monkeypatch):
     """One plan over a k = 1024 row tensor (its buckets split into row ranges) and
     a k = 256 row tensor (ranges side by side) launches the kernel with both

@@ -444,15 +444,19 @@ def ctypes_work_items(plan) -> int:
     return int(wi.value)
 
 
-def test_corrupt_sidecar_writes_stay_inside_out():
+@pytest.mark.parametrize("k", [1024, 256])
+def test_corrupt_sidecar_writes_stay_inside_out(k):
     """Decoding corrupt sidecars into the middle of a larger buffer (op, then a
-    plan): the flags are raised and the words around the output stay zero."""
+    plan): the flags are raised and the words around the output stay zero. At
+    k = 256 (one scale: two 128-row buckets) the plan runs the buckets' row
+    ranges side by side on the slab path, from lane checkpoints walked over the
+    corrupt sidecar."""
     import MPServe_cuda
     from mpserve_amd.decode import DecodePlan
 
     n, m = 256, 1024
     bf, q, sc_u16 = synth(n, m, seed=72)
-    sc = oracle.encode(bf, q, sc_u16, 7, 1024)
+    sc = oracle.encode(bf, q, sc_u16 if k == 1024 else sc_u16[:1].copy(), 7, k)
     q_t = torch.from_numpy(q).to(DEV)
     guard = 4096
     corruptions = [
