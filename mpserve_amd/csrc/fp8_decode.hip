@@ -499,229 +499,9 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, uint16
 }
 
 // ---------------------------------------------------------------------------
-// k = 1024 path: every bucket of a checkpoint written with the compress CLI's
-// default of 1024 substreams, whose column range is a multiple of 1024 (every
-// Llama linear). Lane t's i-th element is row i / P, column c0 + t + (i % P) *
-// 1024 (P = col_len / 1024), so a row splits into P / G blocks of G elements
-// that share one scalar offset: element j of a block is at voffset lane + j *
-// 1024 (BF16: 2 * lane + j * 2048), the block offset goes in soffset and the
-// j-dependent part in the 12-bit immediate. The walk costs a few scalar
-// instructions per block and none per element.
-//
-// A step is S blocks (S * G <= 8 elements). Each step: the bitstream pair
-// requested R steps earlier joins the lane's LDS queue, a new pair is
-// requested if fewer than kAhead chunks are queued ahead, the FP8 bytes of the
-// step R - 1 ahead are loaded, and the step is decoded. Every step issues the
-// same memory instructions, so the in-order vmcnt waits stay static.
-//
-// Queue indices are biased by two chunks: queue chunk h holds stream chunk
-// h - 2 and bit position p is kept as p + 64, so a bitstream word (a pair of
-// chunks) starts at an even h and fills queue slots 2i and 2i + 1. The 32-bit
-// window at biased position p is alignbit(Q[(p-1)/32], Q[(p-1)/32 + 1], -p),
-// whose shift (-p) & 31 is exact for every p (for p % 32 == 0 it selects the
-// second chunk whole, and the first may be anything).
-//
-// Without ESC codes a window of 32 bits covers 4 codes of <= 7 bits: the
-// decode shifts the window by the table entry itself (its low bits are the
-// length) and sums the entries, whose low halves sum to the bits consumed. A
-// step first checks (one ballot) that every lane has the bits of the whole
-// step queued; otherwise that step reads windows through the checked path,
-// which falls back to memory. Buckets with ESC tables use the checked path
-// throughout and track the position per code.
-// ---------------------------------------------------------------------------
-template <int G, bool kEsc>
-__device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, uint16_t *out, const uint32_t *__restrict__ lut,
-                                             uint32_t *__restrict__ queue, uint32_t lane, uint32_t col,
-                                             uint32_t rows, uint32_t P, uint32_t rowoff_lo, uint32_t rowoff_hi,
-                                             uint64_t bucket_bit, const uint2 (&first)[4], uint32_t pos,
-                                             uint32_t pos_end, uint32_t *status) {
-  constexpr uint32_t K = 1024;
-  constexpr int S = G >= 8 ? 1 : 8 / G;  // blocks per step
-  constexpr int SG = S * G;              // elements per step
-  constexpr int R = 4;                   // steps in flight
-  constexpr int kLastW = G - 4 * ((G - 1) / 4);                // codes in a block's last window
-  constexpr uint32_t kNeed = 7u * (uint32_t)(SG - kLastW) + 32u;  // bits a step may need queued
-  rows = uni(rows);
-  P = uni(P);
-  bucket_bit = ((uint64_t)uni((uint32_t)(bucket_bit >> 32)) << 32) | uni((uint32_t)bucket_bit);
-  const uint32_t NB = P / (uint32_t)G;
-  const uint32_t nblocks = rows * NB;
-  const uint32_t nsteps = (nblocks + S - 1) / S;
-  const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
-  const uint64_t base_byte = bucket_bit >> 3;
-  const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
-  const __amdgpu_buffer_rsrc_t r_bs =
-      make_rsrc(reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
-  const uint32_t lane4 = lane << 2;
-  const char *qbytes = reinterpret_cast<const char *>(queue);
-  const __amdgpu_buffer_rsrc_t r_fp8 = make_rsrc(T.fp8, (uint32_t)(T.n * T.m));
-
-  // Window at biased position p from the queue (its chunks must be there).
-  auto window_q = [&](uint32_t p) -> uint32_t {
-    const uint32_t a0 = (((p << 7) - 128u) & 0x7000u) | lane4;
-    const uint32_t a1 = (((p << 7) + 3968u) & 0x7000u) | lane4;
-    const uint32_t c0 = *reinterpret_cast<const uint32_t *>(qbytes + a0);
-    const uint32_t c1 = *reinterpret_cast<const uint32_t *>(qbytes + a1);
-    return __builtin_amdgcn_alignbit(c0, c1, 0u - p);
-  };
-  // Biased chunk h straight from memory (h < 2 reads out of range: zeros).
-  auto chunk_mem = [&](uint32_t h) -> uint32_t {
-    return __builtin_amdgcn_raw_buffer_load_b32(r_bs, ((h - 2u) ^ 1u) << 2, 0, 0);
-  };
-  uint32_t wq;  // queue chunks below wq are (or were) written
-  auto window_chk = [&](uint32_t p) -> uint32_t {
-    uint32_t w = window_q(p);
-    const uint32_t h = (p - 1u) >> 5;
-    const bool dry = h + 1u >= wq;
-    if (__builtin_amdgcn_ballot_w64(dry)) {
-      if (dry) {
-        w = __builtin_amdgcn_alignbit(chunk_mem(h), chunk_mem(h + 1u), 0u - p);
-        __asm__ volatile("" ::"v"(w));  // wait for the loads here, not at a later join
-      }
-    }
-    return w;
-  };
-  // Write the pair whose first (biased, even) chunk is h: slots h & 7 and h & 7 | 1.
-  auto put_pair = [&](uint32_t h, uint32_t hi, uint32_t lo) {
-    uint32_t *slot = queue + (((h & (kQSlots - 1)) << 10) | lane);
-    slot[0] = hi;  // the high half of a bitstream word is its first chunk
-    slot[K] = lo;
-  };
-
-  // Initial queue: the three pairs loaded during set-up.
-  const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
-#pragma unroll
-  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
-  uint32_t rq = rq0 + 6;  // next pair to request (biased index of its first chunk)
-  wq = rq0 + 6;
-  uint32_t pb = pos + 64u;
-
-  // Uniform block walker: element offset of the next block, clamped to the last one.
-  auto row_offset = [&](uint32_t r) -> uint32_t {
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_lo, (int)(r & 63u));
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)rowoff_hi, (int)(r & 63u));
-    return r < 64u ? a : b;
-  };
-  // Branch-free (scalar selects): a taken branch costs the wave an instruction refetch.
-  uint32_t w_blk = 0, w_row = 0;
-  uint32_t w_rowoff = row_offset(0);
-  auto walk = [&]() -> uint32_t {
-    const uint32_t off = w_rowoff + w_blk * (uint32_t)(G * K);
-    const bool wrap = w_blk + 1u == NB;
-    const bool more = w_row + 1u < rows;
-    const uint32_t next_row = w_row + ((wrap && more) ? 1u : 0u);
-    const uint32_t next_off = row_offset(next_row);
-    // past the last block the walk stays on it (its loads are in bounds)
-    w_blk = wrap ? (more ? 0u : w_blk) : w_blk + 1u;
-    w_rowoff = next_row != w_row ? next_off : w_rowoff;
-    w_row = next_row;
-    return off;
-  };
-
-  uint32_t qr[R][SG];
-  uint32_t so[R][S];
-  uint2 infl[R];
-  bool valid[R];
-  auto load_step = [&](int s) {
-#pragma unroll
-    for (int b = 0; b < S; ++b) {
-      so[s][b] = walk();
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-        qr[s][b * G + j] = __builtin_amdgcn_raw_buffer_load_b8(r_fp8, col + (uint32_t)j * K, so[s][b], 0);
-    }
-  };
-#pragma unroll
-  for (int s = 0; s < R; ++s) {
-    valid[s] = false;
-    infl[s] = make_uint2(0u, 0u);
-  }
-#pragma unroll
-  for (int s = 0; s < R - 1; ++s) load_step(s);
-
-  // Decode block b of ring slot s. Entries are {sym << 16 | esc << 4 | len};
-  // the store writes the high half. Unchecked: the window position advances
-  // in pw by whole entries (only its low 16 bits are the position) and pb is
-  // brought up to date once per step.
-  auto decode_block = [&](auto chk, int s, int b, uint32_t &pw) {
-    constexpr bool kChk = decltype(chk)::value;
-    uint16_t *dst = out + so[s][b];
-#pragma unroll
-    for (int g = 0; g < G; g += 4) {
-      uint32_t win = kChk ? window_chk(pb) : window_q(pw);
-#pragma unroll
-      for (int j = g; j < (g + 4 < G ? g + 4 : G); ++j) {
-        const uint32_t q = qr[s][b * G + j];
-        __builtin_assume(q < 256u);  // buffer_load_ubyte zero-extends
-        uint32_t ent = lut[(q << kL) | ((win >> (32 - kL)) ^ lut_spread(q))];
-        if constexpr (!kEsc) {
-          win <<= ent;
-          if constexpr (kChk) pb += ent & 7u;
-          else pw += ent;
-        } else {
-          const uint32_t len = ent & 7u;
-          win <<= len;
-          pb += len;
-          if (__builtin_amdgcn_ballot_w64((ent & kEscBit) != 0u)) {
-            if (ent & kEscBit) {
-              // ESC: the symbol is the next 16 raw bits (the window's high half).
-              ent = window_chk(pb);
-              pb += 16;
-              win = window_chk(pb);
-            }
-          }
-        }
-        dst[col + (uint32_t)j * K] = (uint16_t)(ent >> 16);
-      }
-    }
-  };
-
-  auto step = [&](int slot, uint32_t si) {
-    // 1. the pair requested R steps ago joins the queue
-    if (valid[slot]) {
-      put_pair(wq, infl[slot].y, infl[slot].x);
-      wq += 2;
-    }
-    // 2. request the next pair if fewer than kAhead chunks are queued ahead
-    const bool need = (int32_t)(rq - (pb >> 5)) < (int32_t)kAhead;
-    {
-      const uint32_t off = need ? (rq - 2u) * 4u : kBsPast;
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r_bs, off, 0, 0);
-      infl[slot] = make_uint2(v[0], v[1]);
-    }
-    valid[slot] = need;
-    rq += need ? 2u : 0u;
-    // 3. FP8 bytes R - 1 steps ahead
-    load_step((slot + R - 1) % R);
-    // 4. decode this step
-    if (si < nsteps) {
-      bool chk = kEsc;
-      if constexpr (!kEsc) chk = __builtin_amdgcn_ballot_w64((wq << 5) < pb + kNeed) != 0;
-      if (chk) {
-        uint32_t pw = 0;
-#pragma unroll
-        for (int b = 0; b < S; ++b)
-          if (S == 1 || si * S + (uint32_t)b < nblocks) decode_block(std::true_type{}, slot, b, pw);
-      } else {
-        uint32_t pw = pb;
-#pragma unroll
-        for (int b = 0; b < S; ++b)
-          if (S == 1 || si * S + (uint32_t)b < nblocks) decode_block(std::false_type{}, slot, b, pw);
-        pb += (pw - pb) & 0xFFFFu;
-      }
-    }
-  };
-
-  for (uint32_t s0 = 0; s0 < nsteps; s0 += R) {
-#pragma unroll
-    for (int slot = 0; slot < R; ++slot) step(slot, s0 + (uint32_t)slot);
-  }
-  if (pb - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
-}
-
-// ---------------------------------------------------------------------------
-// k = 1024, col_len = P * 1024 with P >= 4 (every bucket of a Llama-shaped
-// checkpoint).
+// k = 1024, col_len = P * 1024 (every bucket of a checkpoint written with the
+// compress CLI's default of 1024 substreams whose column range is a multiple
+// of 1024: every Llama linear has P >= 4).
 //
 // Element i of a substream lives in slab i: the 1024 columns
 // [c0 + 1024 (i % P), +1024) of the bucket's row i / P. Lane l of wave w,
@@ -751,8 +531,9 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, uint16_t *
 // instructions, so the in-order vmcnt waits stay static.
 //
 // The queue here stores chunk h in slot (~h) & 7 (slot-major, 4 KiB per
-// slot), and positions are kept negated (np = -p, p biased by two chunks as
-// in decode_k1024), so the window's slot addresses and its funnel shift come
+// slot), and positions are kept negated (np = -p, with p biased by two
+// chunks: queue chunk h holds stream chunk h - 2 and bit position p is kept
+// as p + 64), so the window's slot addresses and its funnel shift come
 // straight from np.
 //
 // ESC (kEsc: the bucket's tables hold ESC entries). An ESC entry's low half is
@@ -763,7 +544,10 @@ __device__ __forceinline__ void decode_k1024(const mps_fp8_tensor &T, uint16_t *
 // symbol from the 16 raw bits. ESC codes are rare (the symbols a key's
 // 127 most frequent leave out), so the wave almost never takes that branch.
 // ---------------------------------------------------------------------------
-template <bool kWrap, bool kEsc, int kShift>
+// kWrap: 0 when P % 4 == 0 (a group's four slabs lie in one row); 1 when P > 4
+// and P % 4 != 0 (they may straddle two rows); 2 when P < 4 (they span two to
+// four rows: slab i is row i / P, block i % P, taken per lane).
+template <int kWrap, bool kEsc, int kShift>
 __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *out, const uint32_t *__restrict__ lut,
                                              uint32_t *__restrict__ queue, uint32_t qlane, uint32_t lane,
                                              uint32_t kshift, uint32_t rows, uint32_t P,
@@ -926,17 +710,37 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
       const uint32_t so = uni(w_off + (w_blk << kshift));
       F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, vf_al, so, MPS_SLAB_FP8_CPOL);
       ret = so;
-    } else {
+    } else if constexpr (kWrap == 1) {
       const uint32_t b = w_blk + R;
       const bool wrap = b >= P;
       const bool ok = !wrap || w_row + 1u < rows;
       const uint32_t off = (wrap ? w_next : w_off) + ((wrap ? b - P : b) << kshift) + colw;
       F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, ok ? off : 0u, 0, MPS_SLAB_FP8_CPOL);
       ret = ok ? off << 1 : kSlabPast;
+    } else {
+      // P < 4: lane R's slab 4g + R is row w_row + d, block b - d P, where
+      // b = w_blk + R < 6 and d = b / P < 4. Slabs past the bucket's last row
+      // (a partial last group) load in bounds and store out of range.
+      const uint32_t b = w_blk + R;
+      const uint32_t d = P == 1u ? b : P == 2u ? (b >> 1) : (b >= 3u ? 1u : 0u);
+      const uint32_t o0 = row_offset(w_row), o1 = row_offset(w_row + 1u);
+      const uint32_t o2 = row_offset(w_row + 2u), o3 = row_offset(w_row + 3u);
+      const bool ok = w_row + d < rows;
+      const uint32_t off = (d == 0u ? o0 : d == 1u ? o1 : d == 2u ? o2 : o3) + ((b - d * P) << kshift) + colw;
+      F = __builtin_amdgcn_raw_buffer_load_b32(r_fp8, ok ? off : 0u, 0, MPS_SLAB_FP8_CPOL);
+      ret = ok ? off << 1 : kSlabPast;
     }
     // advance (branch-free; past the last group the walk stays on it)
     const bool more = w_g + 1u < gall;
     const uint32_t nb = w_blk + 4u;
+    if constexpr (kWrap == 2) {
+      // four slabs on: P = 1 and 2 move whole rows, P = 3 one or two rows
+      const uint32_t dr = P == 1u ? 4u : P == 2u ? 2u : (nb >= 6u ? 2u : 1u);
+      w_blk = uni(more ? nb - dr * P : w_blk);
+      w_row = uni(w_row + (more ? dr : 0u));
+      w_g = uni(w_g + (more ? 1u : 0u));
+      return ret;
+    }
     const bool wr = nb >= P;
     const uint32_t nrow = w_row + ((more && wr) ? 1u : 0u);
     const uint32_t noff = row_offset(nrow);
@@ -1292,39 +1096,27 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   decode_slab4<WRAP, ESC, 10>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)lane, 10u, (uint32_t)rows, P, \
                               rowoff_lo, rowoff_hi, base, first, pos, pos_end, status)
       if (P % 4 == 0) {
-        if (has_esc) MPS_SLAB(false, true);
-        else MPS_SLAB(false, false);
+        if (has_esc) MPS_SLAB(0, true);
+        else MPS_SLAB(0, false);
       } else {
-        if (has_esc) MPS_SLAB(true, true);
-        else MPS_SLAB(true, false);
+        if (has_esc) MPS_SLAB(1, true);
+        else MPS_SLAB(1, false);
       }
-#undef MPS_SLAB
       return;
     }
-#define MPS_K1024(GG)                                                                                     \
-  do {                                                                                                    \
-    if (has_esc)                                                                                          \
-      decode_k1024<GG, true>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P,      \
-                             rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);                    \
-    else                                                                                                  \
-      decode_k1024<GG, false>(T, out, lut, qregion, (uint32_t)lane, (uint32_t)col, (uint32_t)rows, P,     \
-                              rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);                   \
-  } while (0)
-    if (P % 8 == 0) MPS_K1024(8);
-    else if (P % 7 == 0) MPS_K1024(7);
-    else if (P % 4 == 0) MPS_K1024(4);
-    else if (P % 2 == 0) MPS_K1024(2);
-    else MPS_K1024(1);
-#undef MPS_K1024
+    // P < 4: the same path, with groups that span two to four rows
+    if (has_esc) MPS_SLAB(2, true);
+    else MPS_SLAB(2, false);
+#undef MPS_SLAB
   } else if (kSlabK && slab) {
     // k_eff 256 / 512 with P % 4 == 0: work-item tid decodes substream `col` of its range
     const uint32_t ks = k_eff == 512 ? 9u : 8u;
     const uint32_t P = (uint32_t)cl >> ks;
     if (has_esc)
-      decode_slab4<false, true, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
+      decode_slab4<0, true, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
                                    rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
     else
-      decode_slab4<false, false, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
+      decode_slab4<0, false, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
                                     rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
   } else if (fast) {
     decode_rows_fast(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows,

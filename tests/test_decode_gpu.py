@@ -87,6 +87,41 @@ def test_decode_k1024_esc(n, m, seed):
     assert _status() == 0
 
 
+@pytest.mark.parametrize("n,m,seed,esc", [
+    (1, 1024, 140, False),     # P = 1, one row: one partial group
+    (5, 1024, 141, False),     # P = 1: a group spans four rows, the last holds one
+    (3, 2048, 142, False),     # P = 2: six slabs, the last group half full
+    (66, 2048, 143, False),
+    (7, 3072, 144, False),     # P = 3: groups straddle rows at every block offset, tail of one
+    (127, 3072, 145, False),
+    (128, 1024, 146, False),   # the most rows a k = 1024 bucket takes
+    (9, 1024, 147, True),      # ESC codes with P = 1
+    (11, 3072, 148, True),     # ESC codes with P = 3, tail of one
+])
+def test_decode_k1024_small_p_slab(n, m, seed, esc):
+    """k = 1024 buckets with P = col_len / 1024 < 4 take the slab path with a
+    per-lane row walk (slab i is row i / P, block i % P): one scale key, so a
+    bucket holds every row (up to 128) and its last group is partial unless
+    4 | rows * P. Bit-exact through the op and through a plan, which splits the
+    larger buckets into row ranges; the status word stays clear."""
+    if esc:
+        bf, q, scales = _esc_inputs(n, m, seed)
+    else:
+        bf, q, sc_u16 = synth(n, m, seed=seed)
+        scales = sc_u16[:1].copy()
+    sc, stats = oracle.encode(bf, q, scales, 7, 1024, with_stats=True)
+    assert (stats["esc_keys"] >= 1) == esc
+    _status()
+    got = _gpu_decode(sc, q)
+    assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
+    assert _status() == 0
+    outs, info, status = _plan_decode([(bf, q, sc)])
+    assert np.array_equal(outs[0], bf), f"plan mismatches: {(outs[0] != bf).sum()}"
+    assert status == 0
+    if n >= 66:
+        assert info["work_items"] > sc["bucket_table_i32"].shape[0]  # row ranges from lane checkpoints
+
+
 @pytest.mark.parametrize("n,m,k,seed,esc", [
     (200, 4096, 256, 120, False),   # P = 16, per-row scales
     (100, 1536, 256, 121, False),   # P = 6: groups straddle rows
