@@ -6,7 +6,7 @@ placed next to this file so it travels with the source tree.
 Tuning builds: ``python -m mpserve_amd.build --define MPS_SLAB_PREFETCH=12 --out
 /tmp/lib_df12.so`` compiles the same sources with the decode kernel's
 compile-time knobs set otherwise (``MPS_SLAB_PREFETCH``, ``MPS_PRIO_LEAD``,
-``MPS_SLAB_RESERVE_BLOCKS``, ``MPS_SLAB_ALIGN``, ``MPS_LUT_SPREAD``, ``MPS_SLAB_OUT_CPOL``,
+``MPS_SLAB_RESERVE_BLOCKS``, ``MPS_SLAB_ALIGN``, ``MPS_SLAB_PAIR``, ``MPS_LUT_SPREAD``, ``MPS_SLAB_OUT_CPOL``,
 ``MPS_SLAB_FP8_CPOL``, ``MPS_SLAB_BS_CPOL``, and the plans' ``MPS_SPLIT_DIV``,
 ``MPS_TAIL_RATIO``; for AWQ ``MPS_AWQ_SLAB_PREFETCH``, ``MPS_AWQ_FEED_EVERY``,
 ``MPS_AWQ_PRIO``, ``MPS_AWQ_PRIO_LEAD``, ``MPS_AWQ_RUN_DIV``) into another file, for

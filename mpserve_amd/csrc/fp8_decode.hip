@@ -601,12 +601,15 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
 #ifndef MPS_SLAB_RESERVE_BLOCKS
 #define MPS_SLAB_RESERVE_BLOCKS 4
 #endif
+#ifndef MPS_SLAB_PAIR
+#define MPS_SLAB_PAIR 0
+#endif
   constexpr int RB = MPS_SLAB_RESERVE_BLOCKS;  // 16-byte blocks per bitstream request
   // Byte address of the bucket's bitstream modulo one request (16 * RB bytes):
   // requests after the first start on that boundary, so each one touches a
   // single cache-line half (RB = 4) or line (RB = 8).
-  const uint32_t phase =
-      ((uint32_t)reinterpret_cast<uintptr_t>(T.bitstream) + (uint32_t)(bucket_bit >> 3)) & (16u * RB - 1u);
+  const uint32_t line_phase = (uint32_t)reinterpret_cast<uintptr_t>(T.bitstream) + (uint32_t)(bucket_bit >> 3);
+  const uint32_t phase = line_phase & (16u * RB - 1u);
   // The initial queue: the four words read during set-up, or three when the
   // fourth would leave the next request off a 16-byte boundary.
   const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
@@ -669,9 +672,16 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
     }
     rcnt = land ? ninb : rcnt;
     ifl = ifl && !land;
-    // no requests past the substream's end (biased end + the window's reach)
-    const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
     const uint32_t off = (rqb >> 3) - 8u;
+    // MPS_SLAB_PAIR (a tuning knob, off): a request that ended in the middle of
+    // a 128-byte line is followed by one for the line's other half as soon as
+    // it lands (the reserve is then full, but the landing set is free), so the
+    // two halves are fetched a step apart and the second finds the line in L2.
+    // It cuts the launch's L2 fetches by 14% but not its time: the lines it
+    // saves are not what the launch waits for.
+    const bool pair = MPS_SLAB_PAIR && land && ((line_phase + off) & 64u) != 0u;
+    // no requests past the substream's end (biased end + the window's reach)
+    const bool req = !ifl && (rcnt <= 1u || pair) && (int32_t)(rqb - (pos_end + 192u)) < 0;
     // blocks up to the next request boundary (the first request may be short)
     const uint32_t nreq = MPS_SLAB_ALIGN ? (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4 : (uint32_t)RB;
     if (req) {
@@ -893,8 +903,8 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
 // from the launch's work counter (queue[0]), at the start of its set-up, so
 // that the atomic's round trip overlaps the set-up's loads; every thread
 // gets it in `ticket` (zero without kQueue).
-// kSlabK: fast-path buckets with k_eff 256 or 512 and P % 4 == 0 take the slab
-// path (else the scalar element walk). Only launches whose tensors have such
+// kSlabK: fast-path buckets with k_eff 256 or 512 take the slab path (else the
+// scalar element walk). Only launches whose tensors have such
 // k compile it in: the extra slab instances cost the k = 1024 launches 1.5%
 // (registers), though their own code is unchanged.
 template <bool kQueue, bool kSlabK>
@@ -927,8 +937,8 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   const int lane = multi ? (tid & (k_eff - 1)) : tid;  // the lane's substream (work-item within its range)
   // Substream of this work-item: the k = 1024 paths give wave w's 16-lane row
   // R, position v the column 64w + 4v + R (see decode_slab4); the others, the lane.
-  // A fast-path bucket with k_eff 256 or 512 and P % 4 == 0 takes the slab path too (kSlabK).
-  const bool slab = kSlabK && fast && (k_eff == 256 || k_eff == 512) && cl % (4 * k_eff) == 0;
+  // A fast-path bucket with k_eff 256 or 512 takes the slab path too (kSlabK).
+  const bool slab = kSlabK && fast && (k_eff == 256 || k_eff == 512);
   const int col = k1024 ? ((tid & ~63) | ((tid & 15) << 2) | ((tid >> 4) & 3))
                   : slab ? ((lane & ~63) | ((lane & 15) << 2) | ((lane >> 4) & 3)) : lane;
   const bool active = bucket_ok && rows > 0 && lane < k_eff;
@@ -1109,15 +1119,24 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     else MPS_SLAB(2, false);
 #undef MPS_SLAB
   } else if (kSlabK && slab) {
-    // k_eff 256 / 512 with P % 4 == 0: work-item tid decodes substream `col` of its range
+    // k_eff 256 / 512 (col_len % k_eff == 0 on the fast path): work-item tid
+    // decodes substream `col` of its range, over slabs of k_eff columns
     const uint32_t ks = k_eff == 512 ? 9u : 8u;
     const uint32_t P = (uint32_t)cl >> ks;
-    if (has_esc)
-      decode_slab4<0, true, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
-                                   rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
-    else
-      decode_slab4<0, false, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P,
-                                    rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
+#define MPS_SLABK(WRAP, ESC)                                                                                   \
+  decode_slab4<WRAP, ESC, 0>(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, ks, (uint32_t)rows, P, rowoff_lo, \
+                             rowoff_hi, base, first, pos, pos_end, status)
+    if (P % 4 == 0) {
+      if (has_esc) MPS_SLABK(0, true);
+      else MPS_SLABK(0, false);
+    } else if (P > 4) {
+      if (has_esc) MPS_SLABK(1, true);
+      else MPS_SLABK(1, false);
+    } else {
+      if (has_esc) MPS_SLABK(2, true);
+      else MPS_SLABK(2, false);
+    }
+#undef MPS_SLABK
   } else if (fast) {
     decode_rows_fast(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows,
                      (uint32_t)(cl / k_eff), rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);

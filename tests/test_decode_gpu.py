@@ -129,18 +129,27 @@ def test_decode_k1024_small_p_slab(n, m, seed, esc):
     (130, 2048, 512, 123, False),   # P = 4
     (40, 2048, 256, 124, True),     # ESC entries, P = 8
     (30, 1792, 256, 125, True),     # ESC entries, P = 7
+    (50, 768, 256, 126, False),     # P = 3: groups span two rows
+    (33, 1024, 512, 127, False),    # P = 2
+    (9, 512, 512, 128, False),      # P = 1: groups span four rows
+    (120, 1280, 256, 129, "one_key"),  # P = 5, one 120-row bucket: ranges side by side
+    (128, 768, 256, 130, "one_key"),   # P = 3, ranges side by side
+    (101, 512, 512, 131, "one_key"),   # P = 1, two ranges an item
+    (26, 512, 256, 132, True),      # ESC entries, P = 2
+    (13, 768, 512, 133, True),      # ESC entries, P = 1.5 -> k_eff 512 does not divide: not the slab path
 ])
 def test_decode_slab_k256_k512(n, m, k, seed, esc):
-    """Buckets with k = 256 or 512 substreams and P = col_len / k >= 4 take the slab
-    path (groups of four elements across 4 x 4 lane transposes), as the single
-    op and inside a plan (whole buckets and row ranges side by side)."""
-    if esc:
+    """Buckets with k = 256 or 512 substreams take the slab path (groups of four
+    elements across 4 x 4 lane transposes) for every P = col_len / k: groups in one
+    row (4 | P), straddling two rows (P > 4), or spanning two to four rows (P < 4);
+    as the single op and inside a plan (whole buckets and row ranges side by side)."""
+    if esc is True:
         bf, q, scales = _esc_inputs(n, m, seed)
         sc, stats = oracle.encode(bf, q, scales, 7, k, with_stats=True)
         assert stats["esc_keys"] >= 1 and stats["esc_elements"] > 0
     else:
         bf, q, scales = synth(n, m, seed=seed)
-        sc = oracle.encode(bf, q, scales, 7, k)
+        sc = oracle.encode(bf, q, scales[:1].copy() if esc == "one_key" else scales, 7, k)
     _status()
     got = _gpu_decode(sc, q)
     assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
