@@ -423,6 +423,28 @@ def test_plan_splits_buckets_into_row_ranges(case):
     assert status == 0
 
 
+def test_plan_small_buckets_of_k1024_tensors_on_the_k256_slab_path():
+    """In a plan that also holds a k = 256 tensor (so its kernel has the k = 256 /
+    512 slab instances), k = 1024 buckets of one short row have k_eff = 256 or
+    512 substreams (a row of 256 or 512 columns) and take that slab path with
+    P = 1; bit-exact, and so through the op, whose kernel walks them per element."""
+    a = synth(64, 1024, seed=150)
+    b = synth(5, 256, seed=151)     # one row a bucket: k_eff 256
+    c = synth(3, 512, seed=152)     # k_eff 512
+    items = [(a[0], a[1], oracle.encode(a[0], a[1], a[2][:1].copy(), 7, 256)),
+             (b[0], b[1], oracle.encode(b[0], b[1], b[2], 7, 1024)),
+             (c[0], c[1], oracle.encode(c[0], c[1], c[2], 7, 1024))]
+    assert (items[1][2]["bucket_row_offsets_i32"][1:] - items[1][2]["bucket_row_offsets_i32"][:-1] == 1).all()
+    outs, _, status = _plan_decode(items)
+    for (bf, _, _), got in zip(items, outs):
+        assert np.array_equal(got, bf), f"mismatches: {(got != bf).sum()}"
+    assert status == 0
+    for bf, q, sc in items[1:]:
+        _status()
+        assert np.array_equal(_gpu_decode(sc, q), bf)
+        assert _status() == 0
+
+
 def test_plan_split_with_bad_row_keeps_bucket_whole():
     """A row index out of range in a bucket the plan would split: the checkpoint
     walk stops, the bucket stays whole, and its decode reports the bad row."""
