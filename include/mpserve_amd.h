@@ -84,11 +84,14 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream);
  * new plan in that case. The pointed-to sidecars must stay alive while the
  * plan is used. Launches are persistent: one workgroup per CU takes work
  * items from a queue in the plan's memory, which each launch leaves as it
- * found it, so launches of one plan (mps_fp8_plan_decode and
- * mps_fp8_plan_decode_into alike) must not overlap: issue them on one stream,
- * or order their streams. Decodes are asynchronous on their stream and OR
- * their MPS_STATUS_* flags into the plan's status word
- * (mps_fp8_plan_read_status).
+ * found it. The plan holds 32 such queues and gives each stream that launches
+ * it (mps_fp8_plan_decode and mps_fp8_plan_decode_into alike) its own at the
+ * stream's first launch, so launches on different streams may overlap, and a
+ * launch captured into a graph replays with the queue of the stream it was
+ * captured on (a replay must then not overlap an eager launch on that same
+ * stream). A 33rd stream is refused with MPS_ERR_RUNTIME. Decodes are
+ * asynchronous on their stream and OR their MPS_STATUS_* flags into the
+ * plan's status word (mps_fp8_plan_read_status).
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:739); it serves its apply() and model loading paths
  * (scripts/mpserve_vllm_fp8_huffman.py:491-557). */
@@ -114,16 +117,27 @@ int mps_fp8_plan_destroy(mps_fp8_plan *plan);
 /* Allocation-free batched decode: decodes `count` tensors (at most 1024, with
  * at most 63,100 buckets in all) in one persistent launch, as a plan would,
  * but without creating one. It calls no hipMalloc, hipFree or other
- * allocating routine and does not synchronise: the descriptors (read from the
- * host array before the call returns) and one work record per bucket go into
- * a static device array of 4 MiB that each device holds from library load to
- * the end of the process. Buckets are not split into row ranges. Flags go to
- * the device status word (mps_fp8_read_status). Calls that overlap on one
- * device share that array and race: issue them on one stream, or order them.
- * Larger inputs are rejected with MPS_ERR_INVALID_ARGUMENT before any work.
+ * allocating routine and does not synchronise: the descriptors (copied from
+ * the host array on `stream`) and one work record per bucket go into a static
+ * device array of 4 MiB that each device holds from library load to the end
+ * of the process. Buckets are not split into row ranges. Flags go to the
+ * device status word (mps_fp8_read_status). Calls that overlap on one device
+ * share that array and race: issue them on one stream, or order them.
+ * Larger inputs, and a `stream` that is capturing a graph (the descriptor
+ * copy would replay from a host array that is gone), are rejected with
+ * MPS_ERR_INVALID_ARGUMENT before any copy or launch.
  * No counterpart in the reference; it serves callers that cannot allocate
- * device memory (code under graph capture, tight serving loops). */
+ * device memory in their decode loop (tight serving loops, harnesses that
+ * forbid allocation). Code under graph capture launches a plan made before
+ * the capture instead. */
 int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, int64_t max_len, void *stream);
+
+/* Capture id of `stream`: the id of the graph capture it is in, or 0 when it
+ * is not capturing (hipStreamGetCaptureInfo). No counterpart in the
+ * reference: the vLLM method uses it to tell a captured forward pass from an
+ * eager one, so that a packed block's decoded weight is reused only within
+ * one of them. */
+int mps_stream_capture_id(void *stream, uint64_t *id_out);
 
 /* Inputs of the GPU sidecar builder, all device pointers: BF16 bit patterns
  * and FP8 bytes of the same tensor (`numel` elements, shape dims[0..ndim)),

@@ -100,6 +100,7 @@ def lib():
     L.mps_fp8_plan_destroy.argtypes = [_p]
     L.mps_fp8_read_status.argtypes = [ctypes.c_int, _p, ctypes.POINTER(ctypes.c_uint32)]
     L.mps_fp8_decode_batch_noalloc.argtypes = [ctypes.POINTER(MpsFp8Tensor), _i64, _i64, _p]
+    L.mps_stream_capture_id.argtypes = [_p, ctypes.POINTER(ctypes.c_uint64)]
     if hasattr(L, "mps_fp8_encode"):
         L.mps_fp8_encode.argtypes = [ctypes.POINTER(MpsFp8EncodeIn), _p, ctypes.POINTER(_p)]
         L.mps_fp8_sidecar_sizes.argtypes = [_p, ctypes.POINTER(_i64)]
@@ -116,7 +117,7 @@ def lib():
     L.mps_awq_plan_destroy.argtypes = [_p]
     for name in ("mps_clock_rate_khz", "mps_fp8_decode", "mps_fp8_plan_create", "mps_fp8_plan_decode",
                  "mps_fp8_plan_decode_into", "mps_fp8_plan_info", "mps_fp8_plan_read_status",
-                 "mps_fp8_plan_destroy", "mps_fp8_read_status", "mps_fp8_decode_batch_noalloc",
+                 "mps_fp8_plan_destroy", "mps_fp8_read_status", "mps_fp8_decode_batch_noalloc", "mps_stream_capture_id",
                  "mps_awq_decode", "mps_awq_encode",
                  "mps_awq_plan_create", "mps_awq_plan_decode", "mps_awq_plan_decode_into", "mps_awq_plan_info", "mps_awq_plan_read_status",
                  "mps_awq_plan_destroy"):

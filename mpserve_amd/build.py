@@ -6,7 +6,7 @@ placed next to this file so it travels with the source tree.
 Tuning builds: ``python -m mpserve_amd.build --define MPS_SLAB_PREFETCH=12 --out
 /tmp/lib_df12.so`` compiles the same sources with the decode kernel's
 compile-time knobs set otherwise (``MPS_SLAB_PREFETCH``, ``MPS_PRIO_LEAD``,
-``MPS_SLAB_RESERVE_BLOCKS``, ``MPS_SLAB_ALIGN``, ``MPS_SLAB_PAIR``, ``MPS_LUT_SPREAD``, ``MPS_SLAB_OUT_CPOL``,
+``MPS_SLAB_RESERVE_BLOCKS``, ``MPS_SLAB_ALIGN``, ``MPS_SLAB_OUT_CPOL``,
 ``MPS_SLAB_FP8_CPOL``, ``MPS_SLAB_BS_CPOL``, and the plans' ``MPS_SPLIT_DIV``,
 ``MPS_TAIL_RATIO``; for AWQ ``MPS_AWQ_SLAB_PREFETCH``, ``MPS_AWQ_FEED_EVERY``,
 ``MPS_AWQ_PRIO``, ``MPS_AWQ_PRIO_LEAD``, ``MPS_AWQ_RUN_DIV``) into another file, for
@@ -43,17 +43,32 @@ def _hipcc() -> str:
 
 def build(verbose: bool = False, defines=(), out: str | None = None) -> str:
     """Compile every HIP source into libmpserve_amd.so (always recompiles), or,
-    with ``defines`` (``NAME=VALUE`` strings), into the tuning library ``out``."""
+    with ``defines`` (``NAME=VALUE`` strings), into the tuning library ``out``.
+    The sources compile in parallel, one object each (in a temporary
+    directory), and are then linked."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
     if defines and (out is None or os.path.abspath(out) == LIB):
         raise ValueError("a build with --define needs --out: the product library keeps the default knobs")
     target = os.path.abspath(out) if out else LIB
     srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    tmp = target + ".tmp"
-    cmd = [_hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-I", os.path.join(ROOT, "include"), "-I", CSRC,
-           *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    incs = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    with tempfile.TemporaryDirectory(prefix="mps_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.basename(s) + ".o") for s in srcs]
+        cmds = [[_hipcc(), *flags, *(f"-D{d}" for d in defines), *incs, "-c", s, "-o", o] for s, o in zip(srcs, objs)]
+        if verbose:
+            for c in cmds:
+                print(" ".join(c), flush=True)
+        with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+            for f in [ex.submit(subprocess.run, c, check=True) for c in cmds]:
+                f.result()
+        tmp = target + ".tmp"
+        link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+        if verbose:
+            print(" ".join(link), flush=True)
+        subprocess.run(link, check=True)
     os.replace(tmp, target)
     return target
 

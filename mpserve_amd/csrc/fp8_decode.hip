@@ -43,17 +43,6 @@ constexpr int kRowsLds = 256;             // row indices staged in LDS
 constexpr uint32_t kEscBit = 1u << 4;
 constexpr int kMaxDevices = 64;
 
-// Table layout knob (tuning builds only). With MPS_LUT_SPREAD, entry p of the
-// table of FP8 byte q sits at word 128 q + (p ^ (q & 0x7C)): each table's 4-entry
-// chunks are permuted by bits 2..6 of its byte, so that lanes with different
-// bytes and equal peeks read different banks. On gfx950 it measured 1.3% slower
-// with bank-conflict cycles almost unchanged (the peeks of a compressed stream
-// are already spread evenly over the banks), so the default is the plain layout.
-#ifndef MPS_LUT_SPREAD
-#define MPS_LUT_SPREAD 0
-#endif
-__device__ __forceinline__ uint32_t lut_spread(uint32_t q) { return MPS_LUT_SPREAD ? (q & 0x7Cu) : 0u; }
-
 // Integrity flags go to a per-device status word passed to every launch.
 __device__ __forceinline__ void flag(uint32_t *status, unsigned int f) { atomicOr(status, f); }
 
@@ -226,7 +215,7 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, uint16_t *_
   };
   auto decode_one = [&](uint32_t q, Idx idx) {
     const uint32_t peek = (uint32_t)(buf >> (64 - kL));
-    const uint32_t ent = lut[(q << kL) | (peek ^ lut_spread(q))];
+    const uint32_t ent = lut[(q << kL) | peek];
     const int len = (int)(ent & 7u);
     buf <<= len;
     cnt -= len;
@@ -438,7 +427,7 @@ __device__ __forceinline__ void decode_rows_fast(const mps_fp8_tensor &T, uint16
       for (int j = g; j < g + kG; ++j) {
         if ((uint32_t)j < nvalid) {
           const uint32_t so = walk(ws);
-          const uint32_t idx = (q[j] << kL) | ((win >> (32 - kL)) ^ lut_spread(q[j]));
+          const uint32_t idx = (q[j] << kL) | (win >> (32 - kL));
           uint32_t ent = lut[idx];
           const uint32_t len = ent & 7u;
           win <<= len;
@@ -601,9 +590,6 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
 #ifndef MPS_SLAB_RESERVE_BLOCKS
 #define MPS_SLAB_RESERVE_BLOCKS 4
 #endif
-#ifndef MPS_SLAB_PAIR
-#define MPS_SLAB_PAIR 0
-#endif
   constexpr int RB = MPS_SLAB_RESERVE_BLOCKS;  // 16-byte blocks per bitstream request
   // Byte address of the bucket's bitstream modulo one request (16 * RB bytes):
   // requests after the first start on that boundary, so each one touches a
@@ -673,15 +659,8 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
     rcnt = land ? ninb : rcnt;
     ifl = ifl && !land;
     const uint32_t off = (rqb >> 3) - 8u;
-    // MPS_SLAB_PAIR (a tuning knob, off): a request that ended in the middle of
-    // a 128-byte line is followed by one for the line's other half as soon as
-    // it lands (the reserve is then full, but the landing set is free), so the
-    // two halves are fetched a step apart and the second finds the line in L2.
-    // It cuts the launch's L2 fetches by 14% but not its time: the lines it
-    // saves are not what the launch waits for.
-    const bool pair = MPS_SLAB_PAIR && land && ((line_phase + off) & 64u) != 0u;
     // no requests past the substream's end (biased end + the window's reach)
-    const bool req = !ifl && (rcnt <= 1u || pair) && (int32_t)(rqb - (pos_end + 192u)) < 0;
+    const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
     // blocks up to the next request boundary (the first request may be short)
     const uint32_t nreq = MPS_SLAB_ALIGN ? (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4 : (uint32_t)RB;
     if (req) {
@@ -780,7 +759,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
     for (int j = 0; j < 4; ++j) {
       if (!kTail || (uint32_t)j < tail) {
         const uint32_t qb = (fq >> (8 * j)) & 0xFFu;
-        const uint32_t q9 = (qb << 9) | (lut_spread(qb) << 2);
+        const uint32_t q9 = qb << 9;
         const uint32_t x = __builtin_amdgcn_alignbit(win, win, s);
         e[j] = *reinterpret_cast<const uint32_t *>(lbytes + ((x & 0x1FCu) ^ q9));
         s -= e[j];
@@ -800,7 +779,7 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
           for (int j = 0; j < 4; ++j) {
             if (!kTail || (uint32_t)j < tail) {
               const uint32_t qb = (fq >> (8 * j)) & 0xFFu;
-              const uint32_t q9 = (qb << 9) | (lut_spread(qb) << 2);
+              const uint32_t q9 = qb << 9;
               const uint32_t w = window(p);
               uint32_t ent = *reinterpret_cast<const uint32_t *>(lbytes + (((w >> 23) & 0x1FCu) ^ q9));
               p -= ent & 7u;
@@ -1073,8 +1052,8 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     }
     const uint32_t qt = (uint32_t)((tid >> 4) + 64 * i);  // the table's FP8 byte
     uint32_t *tab = lut + qt * kTable;
-    *reinterpret_cast<uint4 *>(tab + (((uint32_t)part * 8u) ^ lut_spread(qt))) = make_uint4(e[0], e[1], e[2], e[3]);
-    *reinterpret_cast<uint4 *>(tab + (((uint32_t)part * 8u + 4u) ^ lut_spread(qt))) = make_uint4(e[4], e[5], e[6], e[7]);
+    *reinterpret_cast<uint4 *>(tab + (uint32_t)part * 8u) = make_uint4(e[0], e[1], e[2], e[3]);
+    *reinterpret_cast<uint4 *>(tab + (uint32_t)part * 8u + 4u) = make_uint4(e[4], e[5], e[6], e[7]);
   }
   // Block-wide ORs of "a row index is out of range" (bit 0) and "a table has an
   // ESC entry" (bit 1): one word per wave, written by its first lane. Wave 0's
@@ -1510,7 +1489,11 @@ using namespace mps;
 
 namespace {
 constexpr size_t kAlign = 256;
-constexpr size_t kQueueOff = 64;
+// Work queues of a plan: one per stream that launches it (two u32 words each,
+// 64 bytes apart), so that launches on different streams - a graph replay
+// and an eager decode, a prefetch on a side stream - never share one.
+constexpr int kPlanQueues = 32;
+constexpr size_t kQueueStride = 64;
 // A work item's set-up (tables into the LDS, the lanes' first loads, the
 // pipeline's fill and drain) costs about as long as decoding this many
 // elements; plans weigh items by their elements plus this.
@@ -1527,7 +1510,11 @@ inline bool slab_k(int64_t k) { return k == 256 || k == 512; }
 struct mps_fp8_plan {
   void *d_block = nullptr;
   uint32_t *d_status = nullptr;
-  uint32_t *d_queue = nullptr;  // the decode launch's work counter and exit count (zero between launches)
+  // kPlanQueues work queues (work counter and exit count, zero between
+  // launches); queue i serves streams[i], assigned at the stream's first launch.
+  uint32_t *d_queue = nullptr;
+  std::mutex mu;
+  std::vector<void *> streams;
   mps_fp8_tensor *d_tensors = nullptr;
   WorkItem *d_work = nullptr;
   uint16_t *first_out = nullptr;  // the first tensor's output at creation (decode_into moves all by one offset)
@@ -1561,6 +1548,16 @@ int mps_clock_rate_khz(int device, int64_t *khz_out) {
   int v = 0;
   MPS_HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeClockRate, device));
   *khz_out = v;
+  return MPS_OK;
+}
+
+int mps_stream_capture_id(void *stream, uint64_t *id_out) {
+  last_error().clear();
+  if (!id_out) return fail(MPS_ERR_INVALID_ARGUMENT, "id_out is NULL");
+  hipStreamCaptureStatus s = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  MPS_HIP_CHECK(hipStreamGetCaptureInfo(reinterpret_cast<hipStream_t>(stream), &s, &id));
+  *id_out = s == hipStreamCaptureStatusActive ? (uint64_t)id : 0u;
   return MPS_OK;
 }
 
@@ -1806,11 +1803,12 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
     max_items += ranges - 1;
   }
 
-  // The plan's device block: the status word at 0 and the queue at kQueueOff
-  // in the first kAlign bytes, then the descriptors, checkpoints, split jobs,
-  // their flags and the work records.
+  // The plan's device block: the status word at 0, the work queues from
+  // kAlign, then the descriptors, checkpoints, split jobs, their flags and the
+  // work records.
   if (max_items >= kMaxQueueItems) return fail(MPS_ERR_INVALID_ARGUMENT, "too many work items for one plan");
-  const size_t o_tensors = kAlign;
+  const size_t o_queues = kAlign;
+  const size_t o_tensors = o_queues + align_up(kQueueStride * kPlanQueues);
   const size_t o_ckpt = o_tensors + align_up(sizeof(mps_fp8_tensor) * (size_t)count);
   const size_t o_jobs = o_ckpt + align_up(sizeof(uint32_t) * (size_t)ck_words);
   const size_t o_failed = o_jobs + align_up(sizeof(SplitJob) * jobs.size());
@@ -1835,11 +1833,11 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
   };
   char *blk = static_cast<char *>(p->d_block);
   p->d_status = reinterpret_cast<uint32_t *>(blk);
-  p->d_queue = reinterpret_cast<uint32_t *>(blk + kQueueOff);
+  p->d_queue = reinterpret_cast<uint32_t *>(blk + o_queues);
   p->d_tensors = reinterpret_cast<mps_fp8_tensor *>(blk + o_tensors);
   p->d_work = reinterpret_cast<WorkItem *>(blk + o_work);
   uint32_t *d_ckpt = reinterpret_cast<uint32_t *>(blk + o_ckpt);
-  // Status word and queue (zero), descriptors, jobs and their flags (zero): one copy, on the caller's stream.
+  // Status word and queues (zero), descriptors, jobs and their flags (zero): one copy, on the caller's stream.
   std::vector<char> head(o_work, 0);
   if (count > 0) std::memcpy(head.data() + o_tensors, tensors, sizeof(mps_fp8_tensor) * (size_t)count);
   if (!jobs.empty()) std::memcpy(head.data() + o_jobs, jobs.data(), sizeof(SplitJob) * jobs.size());
@@ -1913,17 +1911,38 @@ int mps_fp8_plan_create(const mps_fp8_tensor *tensors, int64_t count, void *stre
 }
 
 namespace {
+// The work queue of `stream` in the plan: the one it was given at its first
+// launch, or the next free one. A launch leaves its queue as it found it, so
+// launches on one stream (in stream order) can share one; launches on
+// different streams may overlap and each has its own. A graph captured on a
+// stream replays with that stream's queue.
+int plan_queue(mps_fp8_plan *plan, void *stream, uint32_t **queue) {
+  std::lock_guard<std::mutex> lock(plan->mu);
+  size_t i = 0;
+  while (i < plan->streams.size() && plan->streams[i] != stream) ++i;
+  if (i == plan->streams.size()) {
+    if (i >= (size_t)kPlanQueues)
+      return fail(MPS_ERR_RUNTIME, "a decode plan serves at most %d streams", kPlanQueues);
+    plan->streams.push_back(stream);
+  }
+  *queue = plan->d_queue + i * (kQueueStride / sizeof(uint32_t));
+  return MPS_OK;
+}
+
 int plan_launch(mps_fp8_plan *plan, int64_t out_delta, uint32_t *status, void *stream) {
   if (plan->work_items == 0) return MPS_OK;
   unsigned grid = 0;
-  const int rc = persistent_grid(plan->work_items, &grid);
+  int rc = persistent_grid(plan->work_items, &grid);
+  if (rc != MPS_OK) return rc;
+  uint32_t *queue = nullptr;
+  rc = plan_queue(plan, stream, &queue);
   if (rc != MPS_OK) return rc;
   if (plan->slab_k)
     hipLaunchKernelGGL(fp8_decode_plan<true>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                       plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, plan->d_queue);
+                       plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, queue);
   else
     hipLaunchKernelGGL(fp8_decode_plan<false>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                       plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, plan->d_queue);
+                       plan->d_tensors, plan->d_work, plan->work_items, status, out_delta, queue);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }
@@ -1998,6 +2017,19 @@ int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, i
     return fail(MPS_ERR_INVALID_ARGUMENT,
                 "mps_fp8_decode_batch_noalloc: %lld buckets exceed its static scratch (at most %lld)",
                 (long long)total, (long long)kMaxBatchWork);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // The descriptors travel by a copy from the caller's host array. Captured
+  // into a graph, that copy would re-read the host address on every replay,
+  // long after the array is gone: a capturing stream is refused, before any
+  // copy or launch.
+  {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return fail(MPS_ERR_INVALID_ARGUMENT,
+                  "mps_fp8_decode_batch_noalloc cannot run on a capturing stream (its descriptors are copied "
+                  "from host memory); create a decode plan before the capture and launch that instead");
+  }
   if (total == 0) return MPS_OK;
   int dev = 0;
   MPS_HIP_CHECK(hipGetDevice(&dev));
@@ -2009,7 +2041,6 @@ int mps_fp8_decode_batch_noalloc(const mps_fp8_tensor *tensors, int64_t count, i
   if (rc != MPS_OK) return rc;
   auto *d_tensors = reinterpret_cast<mps_fp8_tensor *>(base);
   auto *d_work = reinterpret_cast<WorkItem *>(base + kBatchWorkOff);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // The descriptors are read from the caller's host array before this returns.
   MPS_HIP_CHECK(hipMemcpyAsync(d_tensors, tensors, sizeof(mps_fp8_tensor) * (size_t)count, hipMemcpyHostToDevice, st));
   hipLaunchKernelGGL(fp8_batch_records, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, d_tensors,

@@ -164,6 +164,26 @@ class _TensorPlan:
 _CACHES: list = []  # every per-sidecar plan cache, for clear_decode_plans()
 
 
+class _CacheEntry:
+    """One sidecar's slot in a _SidecarPlans: weak references to its tensors'
+    storages and their versions, its plan once built, and whether a graph
+    captured a launch of that plan."""
+
+    __slots__ = ("refs", "versions", "plan", "pinned")
+
+    def __init__(self, tensors: Sequence[torch.Tensor]):
+        self.refs = [weakref.ref(t.untyped_storage()) for t in tensors]
+        self.versions = [t._version for t in tensors]
+        self.plan = None
+        self.pinned = False
+
+    def valid(self, tensors: Sequence[torch.Tensor]) -> bool:
+        for r, v, t in zip(self.refs, self.versions, tensors):
+            if r() is not t.untyped_storage() or t._version != v:
+                return False
+        return True
+
+
 class _SidecarPlans:
     """Single-tensor decode plans behind huffman_decode_fp8, one per sidecar.
 
@@ -173,38 +193,38 @@ class _SidecarPlans:
     into row ranges that start from lane checkpoints, but computing those
     walks every substream once and synchronises. So the op decodes a sidecar's
     first call over whole buckets, builds its plan on the second call, and
-    launches the plan from then on.
+    launches the plan from then on, on any stream: a plan gives each stream
+    that launches it a work queue of its own.
 
     Invalidation rule. An entry is keyed by the device addresses of the FP8
-    tensor and the ten sidecar arrays, with n and m and the stream: a plan's
-    launches share its work queue and must not overlap, so each stream that
-    decodes a sidecar gets a plan of its own. For each of the eleven
+    tensor and the ten sidecar arrays, with n and m. For each of the eleven
     tensors it keeps a weak reference to the tensor's storage and the tensor's
     version counter (dtype views such as int64 -> uint64 share both with the
     tensor they view). It is used only while every storage is alive and no
     version has changed, so a sidecar that was freed (another may now sit at
-    the same addresses) or rewritten in place through torch gets a new plan. A writer that bypasses torch's version counters (another library
-    writing through the raw pointers) must call clear_decode_plans(). No plan
-    is built while the current stream captures a graph (building
-    synchronises); built plans launch there like any kernel. At most
+    the same addresses) or rewritten in place through torch gets a new plan.
+    A writer that bypasses torch's version counters (another library writing
+    through the raw pointers) must call clear_decode_plans(). At most
     ``capacity`` entries are kept, least recently used first out;
     MPSERVE_DECODE_PLANS=0 turns the cache off.
+
+    Graph capture. No plan is built while the current stream captures
+    (building synchronises and allocates); built plans launch there like any
+    kernel. A plan launched during a capture is pinned: a replay of that graph
+    may launch it at any later time, so when its entry is evicted or
+    invalidated the plan is kept alive until clear_decode_plans(). No plan is
+    freed while the stream captures (hipFree there would break the capture):
+    such plans are freed on the next call made outside a capture.
     """
 
     def __init__(self, capacity: int = 256, factory=None):
         self.capacity = capacity
         self.factory = factory if factory is not None else _TensorPlan  # (descriptor, stream) -> plan
-        self._entries: "collections.OrderedDict[tuple, list]" = collections.OrderedDict()
+        self._entries: "collections.OrderedDict[tuple, _CacheEntry]" = collections.OrderedDict()
+        self._kept: list = []      # plans of dropped entries that a captured graph may still launch
+        self._deferred: list = []  # plans dropped during a capture, to free outside it
         self._lock = threading.Lock()
         _CACHES.append(self)
-
-    @staticmethod
-    def _valid(entry, tensors: Sequence[torch.Tensor]) -> bool:
-        refs, versions = entry[0], entry[1]
-        for r, v, t in zip(refs, versions, tensors):
-            if r() is not t.untyped_storage() or t._version != v:
-                return False
-        return True
 
     def get(self, tensors: Sequence[torch.Tensor], n: int, m: int, desc, device: torch.device, stream: int,
             extra: tuple = ()) -> Optional[_TensorPlan]:
@@ -212,38 +232,65 @@ class _SidecarPlans:
         ``extra``: further key parts (an AWQ group size)."""
         if self.capacity <= 0 or os.environ.get("MPSERVE_DECODE_PLANS", "1") == "0":
             return None
-        key = (device.index, int(stream), n, m) + tuple(extra) + tuple(t.data_ptr() for t in tensors)
+        capturing = torch.cuda.is_current_stream_capturing()
+        key = (device.index, n, m) + tuple(extra) + tuple(t.data_ptr() for t in tensors)
         dropped = []
         try:
             with self._lock:
                 entry = self._entries.get(key)
-                if entry is not None and not self._valid(entry, tensors):
+                if entry is not None and not entry.valid(tensors):
                     dropped.append(self._entries.pop(key))
                     entry = None
                 if entry is None:
-                    self._entries[key] = [[weakref.ref(t.untyped_storage()) for t in tensors],
-                                          [t._version for t in tensors], None]
+                    self._entries[key] = _CacheEntry(tensors)
                     while len(self._entries) > self.capacity:
                         dropped.append(self._entries.popitem(last=False)[1])
                     return None
                 self._entries.move_to_end(key)
-                if entry[2] is None:
-                    if torch.cuda.is_current_stream_capturing():
+                if entry.plan is None:
+                    if capturing:
                         return None
-                    entry[2] = self.factory(desc, stream)
-                return entry[2]
+                    entry.plan = self.factory(desc, stream)
+                if capturing:
+                    entry.pinned = True
+                return entry.plan
         finally:
+            self._release(dropped, capturing)
+
+    def _release(self, dropped, capturing: bool) -> None:
+        """Free the plans of dropped entries, keeping those a captured graph may
+        launch and deferring every free while the stream captures."""
+        free = []
+        with self._lock:
             for e in dropped:
-                if e[2] is not None:
-                    e[2].close()
+                if e.plan is None:
+                    continue
+                if e.pinned:
+                    self._kept.append(e.plan)
+                elif capturing:
+                    self._deferred.append(e.plan)
+                else:
+                    free.append(e.plan)
+            if not capturing:
+                free += self._deferred
+                self._deferred = []
+        for p in free:
+            p.close()
 
     def clear(self) -> None:
+        """Drop every entry and free every plan, pinned ones included: call it
+        when no captured graph that launched them will replay again."""
+        capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
         with self._lock:
-            entries = list(self._entries.values())
+            plans = [e.plan for e in self._entries.values() if e.plan is not None] + self._kept + self._deferred
             self._entries.clear()
-        for e in entries:
-            if e[2] is not None:
-                e[2].close()
+            self._kept = []
+            self._deferred = []
+            if capturing:
+                self._deferred = plans
+                plans = []
+        for p in plans:
+            p.close()
 
     def __len__(self) -> int:
         return len(self._entries)
@@ -270,8 +317,9 @@ def huffman_decode_fp8(fp8_params_u8: torch.Tensor, bitstream_u64: torch.Tensor,
     Runs on the current stream of the FP8 tensor's device. ``out`` (keyword
     only, not in the reference) decodes into a caller-owned contiguous BF16
     buffer of n*m elements, e.g. a preallocated scratch weight. From its
-    second call on a sidecar the op launches a cached plan of that sidecar
-    (_SidecarPlans); the second call synchronises the stream once.
+    second call on a sidecar the op launches a cached plan of that sidecar on
+    whatever stream is current (_SidecarPlans); the second call synchronises
+    the stream once.
     """
     n = int(n)
     m = int(m)

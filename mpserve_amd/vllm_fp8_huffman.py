@@ -28,13 +28,20 @@ How it gets there is this build's own:
   decoded once at load time (the memory of a BF16 model, no decode per step).
 * A layer of a packed attention/MLP block (non-empty
   ``huff_attn_block_row_*``) multiplies by its row slice of its leader's
-  (the block's ``o_proj``) decoded weight, as the reference does (:559-655).
+  (the block's ``o_proj``) decoded weight, as the reference does (:559-655);
+  the leader itself, when it carries pack rows, multiplies by its own slice.
+  The leader's weight is decoded at most once per forward pass for the whole
+  block: the scratch pool records which layer's weight each buffer holds (and
+  in which graph capture and vLLM forward context it was written), and the
+  block's later layers reuse it (the reference caches it per forward context,
+  :559-577).
 
 Importing this module requires vLLM (as the reference's does); it registers
 the method as a side effect.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 import re
 import weakref
@@ -153,20 +160,45 @@ class FP8HuffmanConfig(QuantizationConfig):
 class ScratchPool:
     """BF16 weight buffers keyed by (device, elements, slot), shared by every
     layer of that size: slot 0 is the weight apply() multiplies by, slot 1 the
-    one prefetch() fills for the next layer."""
+    one prefetch() fills for the next layer.
+
+    It also records, per buffer, the token of the last decode enqueued into it
+    (the layer's state, the capture id of the stream, the vLLM forward
+    context), so that a packed block's layers can reuse their leader's decoded
+    weight while nothing else has been decoded into that buffer since."""
 
     def __init__(self) -> None:
         self._bufs: Dict[Tuple[int, int, int], torch.Tensor] = {}
+        self._owner: Dict[int, tuple] = {}
+
+    @staticmethod
+    def _key(device: torch.device, numel: int, slot: int) -> Tuple[int, int, int]:
+        return (device.index if device.index is not None else torch.cuda.current_device(), int(numel), int(slot))
 
     def get(self, device: torch.device, numel: int, slot: int) -> torch.Tensor:
-        key = (device.index if device.index is not None else torch.cuda.current_device(), int(numel), int(slot))
+        key = self._key(device, numel, slot)
         buf = self._bufs.get(key)
         if buf is None:
             buf = self._bufs[key] = torch.empty(int(numel), dtype=torch.bfloat16, device=device)
         return buf
 
+    def existing(self, device: torch.device, numel: int, slot: int) -> Optional[torch.Tensor]:
+        return self._bufs.get(self._key(device, numel, slot))
+
+    def mark(self, buf: torch.Tensor, token: tuple) -> None:
+        """A decode with ``token`` was just enqueued into ``buf``."""
+        self._owner[buf.data_ptr()] = token
+
+    def holds(self, buf: torch.Tensor, token: tuple) -> bool:
+        """Whether the last decode enqueued into ``buf`` carried ``token`` (objects
+        compared by identity, integers by value)."""
+        t = self._owner.get(buf.data_ptr())
+        return t is not None and len(t) == len(token) and all(
+            a is b or (type(a) is int and type(b) is int and a == b) for a, b in zip(t, token))
+
     def clear(self) -> None:
         self._bufs.clear()
+        self._owner.clear()
 
 
 SCRATCH = ScratchPool()
@@ -205,17 +237,17 @@ def _discard(param: torch.Tensor, loaded_weight, *args, **kwargs) -> None:
     """weight_loader of the checkpoint's FP8 weight and scales: the sidecar carries them."""
 
 
-@dataclass
+@dataclass(eq=False)
 class _LayerDecode:
     """What a layer needs at apply(): set up once, by process_weights_after_loading."""
     out_features: int
     in_features: int
     pack: Optional[Tuple[int, int]] = None           # (first row, rows) in the block leader's weight
+    leader: Optional[str] = None                     # the block leader's prefix, when packed
     plan: Optional[object] = None                    # DecodePlan into `weight`'s buffer
     weight: Optional[torch.Tensor] = None            # BF16 [N, K] the plan decodes into
     cached: bool = False                             # weight decoded once, kept
     pending: Optional[Tuple[torch.cuda.Event, torch.Tensor]] = None  # a prefetch's (event, weight)
-    last: Optional[Tuple[torch.cuda.Event, int]] = None  # after the plan's last launch: (event, stream handle)
     extra: Dict[str, object] = field(default_factory=dict)
 
 
@@ -229,6 +261,42 @@ def _as_2d(fp8: torch.Tensor, k: int) -> torch.Tensor:
     if fp8.dim() == 1 and k > 0 and fp8.numel() % k == 0:
         return fp8.view(-1, k)
     raise ValueError(f"fp8_huffman: huff_fp8_u8 of shape {tuple(fp8.shape)} does not hold rows of {k} bytes")
+
+
+def _capture_id(device: torch.device) -> int:
+    """Id of the graph capture the current stream is in (0: not capturing)."""
+    if not torch.cuda.is_current_stream_capturing():
+        return 0
+    from . import _native
+
+    v = ctypes.c_uint64(0)
+    h = torch.cuda.current_stream(device).cuda_stream
+    _native.check(_native.lib().mps_stream_capture_id(ctypes.c_void_p(h), ctypes.byref(v)))
+    return int(v.value)
+
+
+def _forward_context() -> object:
+    """vLLM's current forward context object, or None outside one (or without
+    vllm.forward_context): a new object per forward pass."""
+    try:
+        from vllm.forward_context import get_forward_context, is_forward_context_available
+    except Exception:
+        return None
+    try:
+        return get_forward_context() if is_forward_context_available() else None
+    except Exception:
+        return None
+
+
+def _leader_prefix(prefix: object) -> Optional[str]:
+    """The block leader of a layer: ``<block>.self_attn.o_proj`` for a layer of
+    an attention or MLP block, else None (reference :579-587)."""
+    if not isinstance(prefix, str) or not prefix:
+        return None
+    for part in (".self_attn.", ".mlp."):
+        if part in prefix:
+            return prefix.split(part, 1)[0] + ".self_attn.o_proj"
+    return None
 
 
 def _first_int(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -317,10 +385,15 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
         if isinstance(prefix, str) and prefix:
             _LAYERS_BY_PREFIX[prefix] = layer
         out_features, in_features = getattr(layer, "_fp8_huff_sizes", (0, 0))
-        st = _LayerDecode(out_features=out_features, in_features=in_features, pack=self._pack_rows(layer))
+        pack = self._pack_rows(layer)
+        # Pack rows count only inside an attention or MLP block, whose leader is
+        # its o_proj; elsewhere the reference decodes the layer's own sidecar (:609-629).
+        leader = _leader_prefix(prefix) if pack is not None else None
+        st = _LayerDecode(out_features=out_features, in_features=in_features,
+                          pack=pack if leader is not None else None, leader=leader)
         layer._fp8_huff = st
-        if st.pack is not None:
-            return  # decoded through its block leader
+        if leader is not None and leader != prefix:
+            return  # a member of a packed block: decoded through its leader
         sidecars = self._sidecars(layer)
         fp8s = [_as_2d(s["huff_fp8_u8"], in_features) for s in sidecars]
         if not fp8s[0].is_cuda:
@@ -352,26 +425,28 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
                                f"{getattr(layer, 'prefix', type(layer).__name__)!r}")
         return st
 
+    def _token(self, st: _LayerDecode) -> tuple:
+        return (st, _capture_id(st.weight.device), _forward_context())
+
     def decoded_weight(self, layer: torch.nn.Module, m_in: Optional[int] = None, slot: int = 0,
                        stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-        """The layer's BF16 [N, K] weight, its decode enqueued on ``stream``
-        (default: current) into scratch ``slot`` (or the layer's own buffer in
-        cache mode, decoded once)."""
+        """The layer's BF16 [N, K] weight (for a packed block's leader, the whole
+        block's), its decode enqueued on ``stream`` (default: current) into
+        scratch ``slot`` (or the layer's own buffer in cache mode, decoded once).
+
+        Launches of a layer's plan on different streams may overlap: the plan
+        gives each stream its own work queue, and a graph replays with the
+        queue of the stream it was captured on. What they write is the caller's
+        to order: two decodes into one slot on two streams, or a decode into the
+        slot a GEMM on another stream still reads, race."""
         st = self._state(layer)
-        if st.pack is not None:
-            raise RuntimeError("fp8_huffman: a packed layer's weight is its leader's (see apply)")
         if st.plan is None:
+            if st.leader is not None and st.leader != getattr(layer, "prefix", None):
+                raise RuntimeError("fp8_huffman: a packed layer's weight is its leader's (see apply)")
             raise RuntimeError("fp8_huffman: the layer's sidecar is not on a GPU")
         if st.cached:
             return st.weight
         s = stream if stream is not None else torch.cuda.current_stream(st.weight.device)
-        # A plan's launches share its work queue and must not overlap: a launch
-        # on another stream than the last one (a prefetch on a side stream after
-        # a decode on the current one, or back) first waits for that one. Under
-        # graph capture the captured order stands.
-        capturing = torch.cuda.is_current_stream_capturing()
-        if st.last is not None and st.last[1] != s.cuda_stream and not capturing:
-            s.wait_event(st.last[0])
         if slot == 0:
             st.plan.decode(s)
             out = st.weight
@@ -379,10 +454,7 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
             buf = SCRATCH.get(st.weight.device, st.weight.numel(), slot)
             st.plan.decode_into(buf, s)
             out = buf.view(st.weight.shape)
-        if not capturing:
-            ev = st.last[0] if st.last is not None else torch.cuda.Event()
-            ev.record(s)
-            st.last = (ev, s.cuda_stream)
+        SCRATCH.mark(out, self._token(st))
         return out
 
     def prefetch(self, layer: torch.nn.Module, m_in: Optional[int] = None, stream: Optional[torch.cuda.Stream] = None,
@@ -398,21 +470,50 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
         ev.record(stream if stream is not None else torch.cuda.current_stream(w.device))
         st.pending = (ev, w)
 
+    def _take_pending(self, st: _LayerDecode) -> Optional[torch.Tensor]:
+        """A prefetched weight, once the current stream waits for its decode."""
+        if st.pending is None:
+            return None
+        ev, w = st.pending
+        st.pending = None
+        torch.cuda.current_stream(w.device).wait_event(ev)
+        return w
+
+    def _block_weight(self, leader: torch.nn.Module) -> torch.Tensor:
+        """A packed block's decoded weight: its leader's, decoded at most once per
+        forward pass (the reference's forward-context cache, :559-577). It is
+        reused while the scratch buffer that holds it has had nothing else
+        decoded into it, in the same graph capture (or none) and the same vLLM
+        forward context."""
+        st = self._state(leader)
+        if st.plan is None:
+            raise RuntimeError(f"fp8_huffman: the layer-pack leader {getattr(leader, 'prefix', None)!r} "
+                               "has no decoded weight (its sidecar is not on a GPU)")
+        if st.cached:
+            return st.weight
+        w = self._take_pending(st)
+        if w is not None:
+            return w
+        token = self._token(st)
+        for slot in (0, 1):
+            buf = st.weight if slot == 0 else SCRATCH.existing(st.weight.device, st.weight.numel(), slot)
+            if buf is not None and SCRATCH.holds(buf, token):
+                return buf.view(st.weight.shape)
+        return self.decoded_weight(leader)
+
     def _leader_weight(self, layer: torch.nn.Module, st: _LayerDecode) -> torch.Tensor:
-        """A packed layer's rows of its block leader's (``<block>.self_attn.o_proj``) weight."""
+        """A packed layer's rows of its block leader's (``<block>.self_attn.o_proj``)
+        weight; the leader's own rows when the layer is the leader."""
         prefix = getattr(layer, "prefix", "") or ""
-        for part in (".self_attn.", ".mlp."):
-            if part in prefix:
-                leader_prefix = prefix.split(part, 1)[0] + ".self_attn.o_proj"
-                break
+        if st.leader == prefix:
+            leader, method = layer, self
         else:
-            raise RuntimeError(f"fp8_huffman: {prefix!r} is packed but not in an attention or MLP block")
-        leader = _LAYERS_BY_PREFIX.get(leader_prefix)
-        if leader is None:
-            raise RuntimeError(f"fp8_huffman: cannot find layer-pack leader {leader_prefix!r} for {prefix!r}")
-        method = getattr(leader, "quant_method", None)
-        method = method if isinstance(method, FP8HuffmanLinearMethod) else self
-        w_full = method._weight_for_apply(leader)
+            leader = _LAYERS_BY_PREFIX.get(st.leader)
+            if leader is None:
+                raise RuntimeError(f"fp8_huffman: cannot find layer-pack leader {st.leader!r} for {prefix!r}")
+            method = getattr(leader, "quant_method", None)
+            method = method if isinstance(method, FP8HuffmanLinearMethod) else self
+        w_full = method._block_weight(leader)
         start, rows = st.pack
         return w_full[start:start + rows]
 
@@ -420,12 +521,8 @@ class FP8HuffmanLinearMethod(LinearMethodBase):
         st = self._state(layer)
         if st.pack is not None:
             return self._leader_weight(layer, st)
-        if st.pending is not None:
-            ev, w = st.pending
-            st.pending = None
-            torch.cuda.current_stream(w.device).wait_event(ev)
-            return w
-        return self.decoded_weight(layer)
+        w = self._take_pending(st)
+        return w if w is not None else self.decoded_weight(layer)
 
     # ------------------------------------------------------------------ apply
     def apply(self, layer: torch.nn.Module, x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:

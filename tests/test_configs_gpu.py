@@ -1,12 +1,12 @@
 """Parity of the benchmark configurations at their full shapes, on the GPU.
 
-Configuration 2 (one Llama-3-8B layer) and the smaller tensors of
-configuration 3 (one Llama-3-70B layer with outliers, so ESC codes) compare
-the GPU sidecar builder with the CPU oracle byte for byte and the GPU decode
-with the input bit for bit. The 70B gate/up/down tensors (235 M elements
-each) are past what the single-threaded oracle builds in seconds; they are
-checked by the round trip GPU build -> GPU decode == input, the status word
-and the sidecar's structural invariants. Configuration 4 drives the vLLM
+Configuration 2 (one Llama-3-8B layer) and configuration 3 (one Llama-3-70B
+layer with outliers, so ESC codes; all seven tensors, the 235 M-element
+gate/up/down included, about a minute of oracle time each) compare the GPU
+sidecar builder with the CPU oracle byte for byte and the GPU decode with the
+input bit for bit. Each 70B tensor's ESC keys and ESC-coded elements also
+match the oracle's counts, the latter counted on the GPU from the sidecar's
+tables and the input. Configuration 4 drives the vLLM
 method's apply() at the 8B layer's merged shapes for T in {1, 16, 128, 1024};
 configuration 5 decodes all 225 weights of the 8B model in one plan launch.
 
@@ -29,8 +29,8 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 CFG2 = config_weights("layer8b")
 CFG3 = config_weights("layer70b")
-# 70B tensors the oracle builds within seconds (k/v 8 M, q/o 67 M elements)
-CFG3_ORACLE = ("layers.0.q_proj", "layers.0.k_proj", "layers.0.v_proj", "layers.0.o_proj")
+# every 70B tensor is compared with the oracle (k/v 8 M, q/o 67 M, gate/up/down 235 M elements)
+CFG3_ORACLE = tuple(c[0] for c in CFG3)
 
 
 def _status():
@@ -60,6 +60,34 @@ def _assert_same_as_oracle(side, w):
         assert g.dtype == NP_DTYPES[key] and g.shape == r.shape, (key, g.dtype, g.shape, r.shape)
         assert np.array_equal(g, r), f"{key}: {(g != r).sum()} differing entries"
     return stats
+
+
+def _esc_elements(side, w) -> int:
+    """Elements coded as ESC: those of a key with ESC entries whose symbol is not
+    one its table keeps (build_huffman.cu:485-535, :850-864), counted on the GPU
+    from the sidecar and the input alone."""
+    lens = side["decode_lens_u8"]
+    esc_gids = torch.nonzero(((lens & 0x88) != 0).any(dim=1)).flatten().tolist()
+    if not esc_gids:
+        return 0
+    n, m = w.fp8_u8.shape
+    ro = side["bucket_row_offsets_i32"].long()
+    bucket_of_pos = torch.repeat_interleave(torch.arange(ro.numel() - 1, device=DEV), ro[1:] - ro[:-1])
+    row_bucket = torch.empty(n, dtype=torch.long, device=DEV)
+    row_bucket[side["row_indices_i32"].long()] = bucket_of_pos
+    table = side["bucket_table_i32"]
+    syms = side["decode_syms_u16"].view(torch.int16).to(torch.int32) & 0xFFFF
+    nib = torch.stack([lens & 0xF, lens >> 4], dim=2).reshape(lens.shape[0], -1)  # entry p's nibble
+    count = 0
+    for r0 in range(0, n, 1024):  # row chunks keep the gathered ids small
+        r1 = min(n, r0 + 1024)
+        gid = table[row_bucket[r0:r1, None], w.fp8_u8[r0:r1].long()]
+        sym = w.bf16[r0:r1].view(torch.int16).to(torch.int32) & 0xFFFF
+        for g in esc_gids:
+            kept = torch.unique(syms[g][((nib[g] & 8) == 0) & ((nib[g] & 7) != 0)])
+            sel = gid == g
+            count += int((~torch.isin(sym[sel], kept)).sum().item())
+    return count
 
 
 def _assert_invariants(side, n, m):
@@ -125,8 +153,11 @@ def test_cfg3_layer70b(name, n, m, seed, sigma, outlier_p):
     assert int(per_key.max()) >= 0.99 * n
     assert side["bucket_table_i32"].shape[0] == int(((per_key + 127) // 128).sum())
     if name in CFG3_ORACLE:
+        print(f"[cfg3] {name}: oracle build of {n}x{m}", flush=True)
         ostats = _assert_same_as_oracle(side, w)
         assert ostats["esc_keys"] == stats["esc_keys"]
+        assert ostats["esc_collisions"] == stats["esc_collisions"] == 0
+        assert ostats["esc_elements"] == _esc_elements(side, w)
         assert (ostats["esc_elements"] > 0) == (stats["esc_keys"] > 0)
     _assert_invariants(side, n, m)
     _decode_op_and_plan(side, w)

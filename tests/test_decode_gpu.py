@@ -585,3 +585,76 @@ def test_cuda_clock_rate_khz():
 
     khz = MPServe_cuda.cuda_clock_rate_khz()
     assert isinstance(khz, int) and khz > 0
+
+
+def test_op_alternates_two_sidecars_on_two_streams():
+    """huffman_decode_fp8 on two sidecars, each called on two streams in turn with
+    no synchronisation between the calls: from the second sighting each sidecar's
+    cached plan launches on both streams, every stream with its own work queue.
+    Every output is bit-exact."""
+    import MPServe_cuda
+    from mpserve_amd.mpserve_cuda import _PLANS, read_status
+
+    MPServe_cuda.clear_decode_plans()
+    sides = []
+    for i, (n, m) in enumerate(((256, 8192), (384, 4096))):
+        bf, q, sc_u16 = synth(n, m, seed=260 + i)
+        sides.append((to_torch(oracle.encode(bf, q, sc_u16, 7, 1024), DEV), torch.from_numpy(q).to(DEV), bf))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for rnd in range(4):
+        for j in range(4):
+            sc_t, q_t, _ = sides[j % 2]
+            st = streams[(j // 2 + rnd) % 2]
+            with torch.cuda.stream(st):
+                o = torch.full(q_t.shape, float("nan"), dtype=torch.bfloat16, device=DEV)
+                MPServe_cuda.huffman_decode_fp8(*decode_args(sc_t, q_t), out=o)
+            outs.append((o, j % 2, rnd, st))
+    torch.cuda.synchronize()
+    assert len(_PLANS) == 2 and all(e.plan is not None for e in _PLANS._entries.values())
+    for o, which, rnd, _ in outs:
+        got = o.view(torch.uint16).cpu().numpy()
+        assert np.array_equal(got, sides[which][2]), f"round {rnd}, sidecar {which}"
+    assert read_status(torch.device(DEV)) == 0
+
+
+def test_one_plan_on_two_streams_at_once():
+    """Launches of one plan on two streams overlap (each takes its items from its
+    stream's queue) and both decode every item, round after round."""
+    from mpserve_amd.decode import DecodePlan
+
+    shapes = [(512, 4096, 1024)] * 4 + [(64, 1024, 256)] * 4
+    items, refs = [], []
+    for i, (n, m, k) in enumerate(shapes):
+        bf, q, sc_u16 = synth(n, m, seed=270 + i)
+        items.append((torch.from_numpy(q).to(DEV), to_torch(oracle.encode(bf, q, sc_u16, 7, k), DEV)))
+        refs.append(bf)
+    total = sum(q.numel() for q, _ in items)
+    flat = [torch.empty(total, dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+    outs, off = [], 0
+    for q, _ in items:
+        outs.append(flat[0][off:off + q.numel()])
+        off += q.numel()
+    plan = DecodePlan([(q, sc, o) for (q, sc), o in zip(items, outs)])
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rnd in range(3):
+        for f in flat:
+            f.fill_(float("nan"))
+        for st in streams:
+            st.wait_stream(torch.cuda.current_stream())
+        for f, st in zip(flat, streams):
+            plan.decode_into(f, st)
+        for st in streams:
+            torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        for s_i, f in enumerate(flat):
+            off = 0
+            for j, r in enumerate(refs):
+                got = f[off:off + r.size].view(torch.uint16).cpu().numpy().reshape(r.shape)
+                off += r.size
+                assert np.array_equal(got, r), f"round {rnd}, stream {s_i}, tensor {j}"
+    from mpserve_amd.mpserve_cuda import read_status
+
+    assert read_status(torch.device(DEV)) == 0

@@ -55,7 +55,7 @@ def test_in_place_write_and_free_invalidate(monkeypatch):
     entry = next(iter(c._entries.values()))
     import weakref
 
-    entry[0][4] = weakref.ref(torch.zeros(1).untyped_storage())  # dead once the temporary goes
+    entry.refs[4] = weakref.ref(torch.zeros(1).untyped_storage())  # dead once the temporary goes
     assert c.get(_args(ts), 4, 1, None, dev, 0) is None and p2.closed
 
 
@@ -76,9 +76,50 @@ def test_no_plan_built_while_capturing_and_lru_bound(monkeypatch):
     others = [_sidecar() for _ in range(2)]
     for o in others:
         c.get(_args(o), 4, 1, None, dev, 0)
-    assert len(c) == 2 and p.closed  # least recently used entry evicted, its plan destroyed
+    # least recently used entry evicted, but a captured graph may still launch its plan: kept open
+    assert len(c) == 2 and not p.closed
+    capturing["on"] = False
+    for o in others:
+        c.get(_args(o), 4, 1, None, dev, 0)
+    assert not p.closed  # still kept outside the capture
     c.clear()
-    assert len(c) == 0
+    assert len(c) == 0 and p.closed
+
+
+def test_no_plan_freed_during_capture(monkeypatch):
+    """A plan built and launched outside any capture, whose entry is evicted or
+    invalidated during a capture, is freed on the next call outside it."""
+    monkeypatch.setattr(mc, "_TensorPlan", _StandInPlan)
+    capturing = {"on": False}
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: capturing["on"])
+    c = mc._SidecarPlans(capacity=1)
+    dev = torch.device("cuda", 0)
+    ts, other = _sidecar(), _sidecar()
+    c.get(_args(ts), 4, 1, None, dev, 0)
+    p = c.get(_args(ts), 4, 1, None, dev, 0)
+    assert isinstance(p, _StandInPlan)
+    capturing["on"] = True
+    assert c.get(_args(other), 4, 1, None, dev, 0) is None  # evicts ts's entry during the capture
+    assert not p.closed
+    ts[2].fill_(3)  # and an invalidation during the capture
+    assert c.get(_args(ts), 4, 1, None, dev, 0) is None
+    assert not p.closed
+    capturing["on"] = False
+    c.get(_args(other), 4, 1, None, dev, 0)
+    assert p.closed
+
+
+def test_one_plan_serves_every_stream(monkeypatch):
+    """The cache is not keyed by stream: a plan gives each stream its own work queue."""
+    monkeypatch.setattr(mc, "_TensorPlan", _StandInPlan)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    c = mc._SidecarPlans(capacity=4)
+    dev = torch.device("cuda", 0)
+    ts = _sidecar()
+    assert c.get(_args(ts), 4, 1, None, dev, 11) is None
+    p = c.get(_args(ts), 4, 1, None, dev, 22)
+    assert isinstance(p, _StandInPlan)
+    assert c.get(_args(ts), 4, 1, None, dev, 33) is p and len(c) == 1
 
 
 def test_env_switch_turns_cache_off(monkeypatch):

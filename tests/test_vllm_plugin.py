@@ -135,6 +135,73 @@ def test_loaders_unsharded_and_sharded():
     assert vfh._LAYERS_BY_PREFIX["model.layers.0.self_attn.o_proj"] is layer
 
 
+def _pack(start, rows):
+    return {"huff_attn_block_row_start_i32": torch.tensor([start], dtype=torch.int32),
+            "huff_attn_block_row_len_i32": torch.tensor([rows], dtype=torch.int32)}
+
+
+def test_packed_leader_with_its_own_rows_does_not_recurse():
+    """A block leader (<block>.self_attn.o_proj) that carries pack rows itself
+    slices its own decoded weight (reference :628-655). Without a GPU its weight
+    cannot be decoded: that is reported, for the leader and for its members."""
+    bf, q, sc = synth(96, 64, seed=3)
+    leader, lm = make_layer("model.layers.5.self_attn.o_proj", [96], 64)
+    load(leader, stored_sidecar(bf, q, sc, 64))
+    load(leader, _pack(0, 32))
+    lm.process_weights_after_loading(leader)
+    st = leader._fp8_huff
+    assert st.pack == (0, 32) and st.leader == "model.layers.5.self_attn.o_proj"
+    with pytest.raises(RuntimeError, match="not on a GPU"):
+        lm._weight_for_apply(leader)
+    member, mm = make_layer("model.layers.5.mlp.gate_up_proj", [64], 64)
+    load(member, _pack(32, 64))
+    mm.process_weights_after_loading(member)
+    assert member._fp8_huff.plan is None and member._fp8_huff.leader == "model.layers.5.self_attn.o_proj"
+    with pytest.raises(RuntimeError, match="layer-pack leader"):
+        mm._weight_for_apply(member)
+    with pytest.raises(RuntimeError, match="leader's"):
+        mm.decoded_weight(member)
+    orphan, om = make_layer("model.layers.9.mlp.down_proj", [8], 64)
+    load(orphan, _pack(0, 8))
+    om.process_weights_after_loading(orphan)
+    with pytest.raises(RuntimeError, match="cannot find layer-pack leader"):
+        om._weight_for_apply(orphan)
+
+
+def test_pack_rows_outside_a_block_are_ignored():
+    """Pack rows of a layer that is in no attention or MLP block do not apply:
+    the reference then decodes the layer's own sidecar (:609-629)."""
+    bf, q, sc = synth(16, 64, seed=4)
+    layer, method = make_layer("model.embed_proj", [16], 64)
+    load(layer, stored_sidecar(bf, q, sc, 64))
+    load(layer, _pack(0, 8))
+    method.process_weights_after_loading(layer)
+    assert layer._fp8_huff.pack is None and layer._fp8_huff.leader is None
+    assert vfh._leader_prefix("model.layers.2.self_attn.qkv_proj") == "model.layers.2.self_attn.o_proj"
+    assert vfh._leader_prefix("model.layers.2.mlp.down_proj") == "model.layers.2.self_attn.o_proj"
+    assert vfh._leader_prefix("lm_head") is None and vfh._leader_prefix("") is None
+
+
+def test_scratch_tokens_separate_layers_captures_and_forward_passes():
+    """A buffer's token names the layer state, the capture id and the forward
+    context of the last decode enqueued into it; a packed block reuses its
+    leader's weight only under the same three."""
+    pool = vfh.ScratchPool()
+    buf = torch.empty(4, dtype=torch.bfloat16)
+    a, b = object(), object()
+    fwd1, fwd2 = object(), object()
+    assert not pool.holds(buf, (a, 0, None))
+    pool.mark(buf, (a, 0, fwd1))
+    assert pool.holds(buf, (a, 0, fwd1))
+    assert not pool.holds(buf, (b, 0, fwd1))      # another layer decoded since
+    assert not pool.holds(buf, (a, 7, fwd1))      # inside a capture: eager contents are not the graph's
+    assert not pool.holds(buf, (a, 0, fwd2))      # the next forward pass
+    pool.mark(buf, (a, 7, None))
+    assert pool.holds(buf, (a, 7, None)) and not pool.holds(buf, (a, 8, None))  # another capture
+    pool.clear()
+    assert not pool.holds(buf, (a, 7, None))
+
+
 def test_apply_rejects_cpu_and_bad_dtypes():
     layer, method = make_layer("p", [8], 8)
     with pytest.raises(ValueError, match="requires CUDA tensors"):
@@ -298,3 +365,56 @@ def test_packed_block_layers_use_the_leaders_rows():
         out = method.apply(layer, x)
         assert out.shape == (3, rows)
         assert torch.allclose(out.float(), torch.matmul(x, w[start:start + rows].t()).float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.gpu
+def test_packed_leader_with_its_own_rows_decodes_once_per_forward():
+    """o_proj leads a packed block and carries pack rows itself: it multiplies by
+    its own rows, qkv and gate by theirs, all of the leader's exact decoded
+    weight; the leader's plan launches once per forward pass of the block
+    (reference :559-587, :628-655), again after another layer of the same size
+    has been decoded into the shared scratch buffer."""
+    k = 1024
+    bf, q, sc = synth(512, k, seed=250)  # qkv rows 0..255, o_proj 256..383, gate 384..511
+    leader, lm = make_layer("model.layers.6.self_attn.o_proj", [128], k)
+    load(leader, _to(stored_sidecar(bf, q, sc), DEV))
+    load(leader, _to(_pack(256, 128), DEV))
+    lm.process_weights_after_loading(leader)
+    st = leader._fp8_huff
+    assert st.plan is not None and st.pack == (256, 128) and st.weight.shape == (512, k)
+    launches = {"n": 0}
+    real_decode = st.plan.decode
+
+    def counted(stream=None):
+        launches["n"] += 1
+        return real_decode(stream)
+
+    st.plan.decode = counted
+    w = torch.from_numpy(bf).view(torch.bfloat16).to(DEV)
+    members = []
+    for prefix, start, rows in (("model.layers.6.self_attn.qkv_proj", 0, 256), ("model.layers.6.mlp.gate_proj", 384, 128)):
+        layer, method = make_layer(prefix, [rows], k)
+        load(layer, _to(_pack(start, rows), DEV))
+        method.process_weights_after_loading(layer)
+        members.append((layer, method, start, rows))
+    order = [members[0], (leader, lm, 256, 128), members[1]]
+    # another layer of the same size shares the leader's scratch buffer
+    other_bf, other_q, other_sc = synth(512, k, seed=251)
+    other, om = make_layer("model.layers.7.self_attn.o_proj", [512], k)
+    load(other, _to(stored_sidecar(other_bf, other_q, other_sc), DEV))
+    om.process_weights_after_loading(other)
+    assert other._fp8_huff.weight.data_ptr() == st.weight.data_ptr()
+    x = torch.randn((5, k), device=DEV).to(torch.bfloat16)
+    for fwd in range(3):
+        launches["n"] = 0
+        for layer, method, start, rows in order:
+            got_w = method._weight_for_apply(layer)
+            assert torch.equal(got_w.view(torch.uint16), w[start:start + rows].view(torch.uint16)), (fwd, layer.prefix)
+            out = method.apply(layer, x)
+            assert out.shape == (5, rows)
+            ref = torch.matmul(x.float(), w[start:start + rows].float().t())
+            assert torch.allclose(out.float(), ref, rtol=2e-2, atol=2e-2), (fwd, layer.prefix)
+        assert launches["n"] == 1, f"forward {fwd}: the leader decoded {launches['n']} times"
+        om.apply(other, x)  # the next layer of this size overwrites the scratch buffer
+    torch.cuda.synchronize()
+    assert st.plan.read_status() == 0

@@ -90,3 +90,30 @@ def test_noalloc_rejects_inputs_beyond_its_scratch():
     arr = (_native.MpsFp8Tensor * 1)(big)
     with pytest.raises(ValueError, match="static scratch"):
         _native.check(_native.lib().mps_fp8_decode_batch_noalloc(arr, 1, 7, None))
+
+
+def test_noalloc_refuses_a_capturing_stream():
+    """Under graph capture the descriptor copy from the caller's host array would
+    replay from freed host memory: the call is refused on the host, before any
+    copy or launch, and the capture itself stays usable (not replayed here)."""
+    from mpserve_amd import _native
+    from mpserve_amd.decode import sidecar_decode_args
+    from mpserve_amd.mpserve_cuda import _descriptor, _stream_handle
+
+    q_t, sc_t, bf = _items([(64, 1024, 1024, False)], 740)[0]
+    out = torch.empty(q_t.shape, dtype=torch.bfloat16, device=DEV)
+    arr = (_native.MpsFp8Tensor * 1)(_descriptor(*sidecar_decode_args(q_t, sc_t)[:13], out))
+    x = torch.zeros(8, device=DEV)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    rc = None
+    with torch.cuda.graph(g):
+        x.add_(1)
+        rc = _native.lib().mps_fp8_decode_batch_noalloc(arr, 1, 7, ctypes.c_void_p(_stream_handle(torch.device(DEV))))
+        msg = _native.lib().mps_last_error().decode()
+    assert rc == _native.MPS_ERR_INVALID_ARGUMENT and "capturing" in msg
+    torch.cuda.synchronize()
+    # outside the capture the same call runs
+    _noalloc([(q_t, sc_t, bf)], [out])
+    torch.cuda.synchronize()
+    assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf)
