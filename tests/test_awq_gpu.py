@@ -560,7 +560,7 @@ def test_op_plan_cache_alternating_sidecars():
             assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16)), f"call {call}"
         assert read_status(torch.device(DEV)) == 0
     cache = awq_mod._plan_cache()
-    assert len(cache) == 2 and all(e[2] is not None for e in cache._entries.values())
+    assert len(cache) == 2 and all(e.plan is not None for e in cache._entries.values())
     sc, w, n, m, group = cases[0]
     buf = torch.zeros(n * m + 1, dtype=torch.bfloat16, device=DEV)
     out = _op_call(sc, w, n, m, group, out=buf[1:])  # 2-byte offset: the direct kernel
@@ -570,7 +570,7 @@ def test_op_plan_cache_alternating_sidecars():
     out = _op_call(sc, w, n, m, group)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16))
-    assert sum(e[2] is None for e in cache._entries.values()) == 1
+    assert sum(e.plan is None for e in cache._entries.values()) == 1
     assert read_status(torch.device(DEV)) == 0
     mc.clear_decode_plans()
     assert len(cache) == 0

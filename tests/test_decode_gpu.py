@@ -485,9 +485,9 @@ def test_op_plan_cache_alternating_sidecars():
             assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf), f"call {call}"
         assert _status() == 0
     entries = list(mc._PLANS._entries.values())
-    assert len(entries) == 2 and all(e[2] is not None for e in entries)
+    assert len(entries) == 2 and all(e.plan is not None for e in entries)
     # the few-bucket sidecar's plan splits its 2 buckets into row ranges
-    wi = ctypes_work_items(entries[0][2])
+    wi = ctypes_work_items(entries[0].plan)
     assert wi > 2
     stored, q_t, bf = cases[1]
     q_t.copy_(q_t.clone())  # same bytes, new version
@@ -495,7 +495,7 @@ def test_op_plan_cache_alternating_sidecars():
                                           *decode_args(stored, q_t)[2:])
     torch.cuda.synchronize()
     assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf)
-    assert sum(e[2] is None for e in mc._PLANS._entries.values()) == 1
+    assert sum(e.plan is None for e in mc._PLANS._entries.values()) == 1
     mc.clear_decode_plans()
     assert len(mc._PLANS) == 0
 
