@@ -43,8 +43,34 @@ constexpr int kRowsLds = 256;             // row indices staged in LDS
 constexpr uint32_t kEscBit = 1u << 4;
 constexpr int kMaxDevices = 64;
 
-// Integrity flags go to a per-device status word passed to every launch.
-__device__ __forceinline__ void flag(uint32_t *status, unsigned int f) { atomicOr(status, f); }
+// A load through a global (not generic) pointer: generic (flat) loads count in
+// two counters, and an outstanding one makes the compiler turn every later
+// memory wait into a full one.
+template <typename V>
+__device__ __forceinline__ V gload(const V *p) {
+  return *(const __attribute__((address_space(1))) V *)(p);
+}
+// The same, not merged with its neighbours (which would make an unaligned wide
+// load, and a generic one).
+template <typename V>
+__device__ __forceinline__ V gload_single(const V *p) {
+  return *(const volatile __attribute__((address_space(1))) V *)(p);
+}
+
+// A store through a global pointer, for the same reason.
+template <typename V>
+__device__ __forceinline__ void gstore(V *p, V v) {
+  *(__attribute__((address_space(1))) V *)(p) = v;
+}
+
+// Integrity flags go to a per-device status word passed to every launch. The
+// atomic addresses global memory, not a generic pointer: an outstanding
+// generic (flat) access makes the compiler turn every later memory wait into a
+// full one.
+__device__ __forceinline__ void flag(uint32_t *status, unsigned int f) {
+  __hip_atomic_fetch_or((__attribute__((address_space(1))) uint32_t *)(status), f, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Stream chunk c (32 bits, stream order) of a bitstream of u64 words stored
 // little-endian: word w's high half (its first 32 stream bits) is u32 2w+1.
@@ -53,7 +79,7 @@ __device__ __forceinline__ void flag(uint32_t *status, unsigned int f) { atomicO
 // runs past its last code selects a table entry whose low bits do not matter.
 __device__ __forceinline__ uint32_t chunk_at(const uint32_t *__restrict__ bs32, uint64_t nchunks, uint64_t c) {
   const uint64_t cc = c < nchunks ? c : nchunks - 1;
-  return bs32[cc ^ 1u];
+  return gload(bs32 + (cc ^ 1u));
 }
 
 __device__ uint32_t g_zero_chunks[2];
@@ -189,7 +215,7 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, uint16_t *_
   uint32_t qa[kDepth], qb[kDepth];
   next_block(ia);
 #pragma unroll
-  for (int j = 0; j < kDepth; ++j) qa[j] = fp8[ia[j]];
+  for (int j = 0; j < kDepth; ++j) qa[j] = gload(fp8 + ia[j]);
   uint32_t s0 = chunk_at(bs32, nchunks, tail), s1 = chunk_at(bs32, nchunks, tail + 1);
   bool stale = false;  // the staged pair no longer starts at `tail`
 
@@ -225,7 +251,7 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, uint16_t *_
       buf <<= 16;
       cnt -= 16;
     }
-    out[idx] = (uint16_t)sym;
+    gstore(out + idx, (uint16_t)sym);
     refill();
   };
   // One block: decode (qc, ic) while (qn_, in_) receive the next block's loads.
@@ -243,7 +269,7 @@ __device__ __forceinline__ void decode_lane(const mps_fp8_tensor &T, uint16_t *_
     stale = false;
     next_block(inx);
 #pragma unroll
-    for (int j = 0; j < kDepth; ++j) qnx[j] = fp8[inx[j]];
+    for (int j = 0; j < kDepth; ++j) qnx[j] = gload(fp8 + inx[j]);
     s0 = chunk_at(bs32, nchunks, tail);
     s1 = chunk_at(bs32, nchunks, tail + 1);
     if (i0 + kDepth <= count) {
@@ -596,13 +622,10 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   // single cache-line half (RB = 4) or line (RB = 8).
   const uint32_t line_phase = (uint32_t)reinterpret_cast<uintptr_t>(T.bitstream) + (uint32_t)(bucket_bit >> 3);
   const uint32_t phase = line_phase & (16u * RB - 1u);
-  // The initial queue: the four words read during set-up, or three when the
-  // fourth would leave the next request off a 16-byte boundary.
+  // The initial queue (written below): the four words read during set-up, or
+  // three when the fourth would leave the next request off a 16-byte boundary.
   const uint32_t rq0 = ((pos >> 5) & ~1u) + 2u;
   const uint32_t nfirst = (MPS_SLAB_ALIGN && ((phase + 4u * (rq0 - 2u)) & 15u)) ? 6u : 8u;
-#pragma unroll
-  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
-  if (nfirst == 8u) put_pair(rq0 + 6u, first[3].y, first[3].x);
   uint32_t wqb = (rq0 + nfirst) << 5;  // 32 x (first chunk not yet written)
   uint32_t rqb = wqb;                  // 32 x (first chunk not yet requested)
   uint32_t np = 0u - (pos + 64u);      // negated biased position
@@ -810,6 +833,11 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   uint32_t Fr[DF], SOr[DF];
 #pragma unroll
   for (int u = 0; u < DF; ++u) SOr[u] = load_group(Fr[u]);
+  // The initial queue, written once the first FP8 loads are in flight: the
+  // wait for the set-up's bitstream words overlaps them.
+#pragma unroll
+  for (int i = 0; i < 3; ++i) put_pair(rq0 + 2 * i, first[i].y, first[i].x);
+  if (nfirst == 8u) put_pair(rq0 + 6u, first[3].y, first[3].x);
   // Every wave of the workgroup decodes the same number of groups, but the
   // issue arbiter favours the oldest ready wave (waves 4r..4r+3 are the r-th
   // oldest on their SIMDs): left alone, the oldest waves finish first and the
@@ -878,6 +906,20 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
   return w;
 }
 
+// Item trace, in instrumented builds only (python -m mpserve_amd.build --define
+// MPS_TRACE_ITEMS=1 --out LIB; mpserve_amd.item_trace reads it). decode_bucket
+// then also notes the real-time clock after its set-up's last barrier.
+#ifndef MPS_TRACE_ITEMS
+#define MPS_TRACE_ITEMS 0
+#endif
+#if MPS_TRACE_ITEMS
+#define MPS_TR_PARAM , uint64_t &tr_setup, uint64_t &tr_levels
+#define MPS_TR_ARG , tr_setup, tr_levels
+#else
+#define MPS_TR_PARAM
+#define MPS_TR_ARG
+#endif
+
 // kQueue: the work item also takes the ticket of the workgroup's next one
 // from the launch's work counter (queue[0]), at the start of its set-up, so
 // that the atomic's round trip overlaps the set-up's loads; every thread
@@ -888,7 +930,8 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
 // (registers), though their own code is unchanged.
 template <bool kQueue, bool kSlabK>
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t *out, const WorkItem &w,
-                                              uint32_t *lds, uint32_t *status, uint32_t *queue, uint32_t &ticket) {
+                                              uint32_t *lds, uint32_t *status, uint32_t *queue,
+                                              uint32_t &ticket MPS_TR_PARAM) {
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
@@ -960,6 +1003,11 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   uint32_t pos = __builtin_amdgcn_raw_buffer_load_b32(r_sb, sb_off, 0, 0);
   uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(r_eb, sb_off, 0, 0);
 
+#if MPS_TRACE_ITEMS
+  const uint64_t tr_start = __builtin_amdgcn_s_memrealtime();
+  __asm__ volatile("" ::"v"(gids[0]), "v"(gids[3]), "v"(r_lo), "v"(r_hi), "v"(pos), "v"(pos_end));
+  const uint64_t tr_l1 = __builtin_amdgcn_s_memrealtime();
+#endif
   bool bad_table = false;
 #pragma unroll
   for (int i = 0; i < kSlices; ++i) {
@@ -974,23 +1022,17 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   bool bad_row = (has_lo && (r_lo < 0 || r_lo >= T.n)) | (has_hi && (r_hi < 0 || r_hi >= T.n));
   const uint32_t rowoff_lo = has_lo ? (uint32_t)r_lo * (uint32_t)T.m + (uint32_t)c0 : 0u;
   const uint32_t rowoff_hi = has_hi ? (uint32_t)r_hi * (uint32_t)T.m + (uint32_t)c0 : 0u;
-  // First four bitstream words of this lane (two 16-byte loads); the slab
-  // path queues all four, the others three.
-  uint2 first[4];
-  {
-    const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
-    const uint64_t base_byte = base >> 3;
-    const uint32_t win_bytes = rows_fast && base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
-    const __amdgpu_buffer_rsrc_t r_bs = make_rsrc(
-        reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
-    const uint32_t off0 = active ? ((pos >> 5) & ~1u) * 4u : kBsPast;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off0 + 16u * (uint32_t)i, 0, 0);
-      first[2 * i] = make_uint2(v[0], v[1]);
-      first[2 * i + 1] = make_uint2(v[2], v[3]);
-    }
-  }
+  // Offset of the lane's first bitstream words (loaded below, after the
+  // tables), computed here: the wait for `pos` then falls before the table
+  // loads are issued, not at the join of their two paths, where it would wait
+  // for the tables too.
+  uint32_t off0 = active ? ((pos >> 5) & ~1u) * 4u : kBsPast;
+  __asm__ volatile("" : "+v"(off0));
+  // Likewise the descriptor's bitstream fields (scalar loads), read before the
+  // table loads rather than where the words are loaded.
+  const uint8_t *bs_ptr = reinterpret_cast<const uint8_t *>(T.bitstream);
+  int64_t bs_words = T.bitstream_words;
+  __asm__ volatile("" : "+s"(bs_ptr), "+s"(bs_words));
   // The tables' contents (buffer loads when their byte offsets fit 31 bits).
   uint4 sv[kSlices];
   uint32_t nibs[kSlices];
@@ -1013,9 +1055,12 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     }
   }
   if (bad_table) flag(status, MPS_STATUS_BAD_TABLE);
+  // The two fallbacks below load through global pointers (gload), so that the
+  // waits after their join stay partial and the first bitstream words' loads
+  // below can still be in flight during the expansion.
   if (!rows_fast) {
     for (int i = tid; i < rows; i += kBlock) {
-      const int32_t r = w.row_idx[i];
+      const int32_t r = gload(w.row_idx + i);
       bad_row |= r < 0 || r >= T.n;
       s_rows[i] = r;
     }
@@ -1029,15 +1074,47 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
       const uint16_t *sp = T.decode_syms + (int64_t)g * kTable + part * 8;
       const uint8_t *lp = T.decode_lens + (int64_t)g * kPacked + part * 4;
       if (vec_ok) {
-        sv[i] = *reinterpret_cast<const uint4 *>(sp);
-        nibs[i] = *reinterpret_cast<const uint32_t *>(lp);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = gload(reinterpret_cast<const u32x4 *>(sp));
+        sv[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        nibs[i] = gload(reinterpret_cast<const uint32_t *>(lp));
       } else {
-        sv[i] = make_uint4((uint32_t)sp[0] | ((uint32_t)sp[1] << 16), (uint32_t)sp[2] | ((uint32_t)sp[3] << 16),
-                           (uint32_t)sp[4] | ((uint32_t)sp[5] << 16), (uint32_t)sp[6] | ((uint32_t)sp[7] << 16));
-        nibs[i] = (uint32_t)lp[0] | ((uint32_t)lp[1] << 8) | ((uint32_t)lp[2] << 16) | ((uint32_t)lp[3] << 24);
+        uint32_t h[8], b[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = gload_single(sp + j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = gload_single(lp + j);
+        sv[i] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        nibs[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
       }
     }
   }
+
+  // First four bitstream words of this lane (two 16-byte loads); the slab
+  // path queues all four, the others three. Issued after every other set-up
+  // load: a lane's words are scattered (64 lines a wave), and as the last loads
+  // in the in-order count the expansion below need not wait for them; the
+  // decode waits for them after it has issued its first FP8 loads.
+  uint2 first[4];
+  {
+    const uint64_t bs_bytes = bs_words > 0 ? (uint64_t)bs_words * 8u : 0u;
+    const uint64_t base_byte = base >> 3;
+    const uint32_t win_bytes = rows_fast && base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+    const __amdgpu_buffer_rsrc_t r_bs = make_rsrc(bs_ptr + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off0 + 16u * (uint32_t)i, 0, 0);
+      first[2 * i] = make_uint2(v[0], v[1]);
+      first[2 * i + 1] = make_uint2(v[2], v[3]);
+    }
+  }
+  // Keep the expansion below the two loads (it waits for the tables only).
+  __builtin_amdgcn_sched_barrier(0);
+#if MPS_TRACE_ITEMS
+  __asm__ volatile("" ::"v"(sv[0].x), "v"(sv[3].w), "v"(nibs[0]), "v"(nibs[3]));
+  const uint64_t tr_l2 = __builtin_amdgcn_s_memrealtime();
+  tr_levels = ((tr_l1 - tr_start) & 0xFFFFFFFFull) | ((tr_l2 - tr_start) << 32);
+#endif
   uint32_t esc_seen = 0;
 #pragma unroll
   for (int i = 0; i < kSlices; ++i) {
@@ -1072,6 +1149,9 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   const bool has_esc = (bflags & 2u) != 0;
   const bool any_bad_row = (bflags & 1u) != 0;
   __syncthreads();  // the flag words belong to the queue from here on
+#if MPS_TRACE_ITEMS
+  tr_setup = __builtin_amdgcn_s_memrealtime();
+#endif
 
   if (!bucket_ok || any_bad_row) {
     if (tid == 0) flag(status, !bucket_ok ? MPS_STATUS_BAD_BUCKET : MPS_STATUS_BAD_ROW);
@@ -1120,8 +1200,8 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     decode_rows_fast(T, out, lut, qregion, (uint32_t)tid, (uint32_t)lane, (uint32_t)k_eff, (uint32_t)rows,
                      (uint32_t)(cl / k_eff), rowoff_lo, rowoff_hi, base, first, pos, pos_end, status);
   } else {
-    const uint64_t pos0 = base + sb[lane];
-    const uint64_t pend = base + w.endbits[lane];
+    const uint64_t pos0 = base + gload(sb + lane);
+    const uint64_t pend = base + gload(w.endbits + lane);
     if (nm <= 0xFFFFFFFFull)
       decode_lane<uint32_t>(T, out, lut, s_rows, lane, k_eff, total, c0, cl, pos0, pend, status);
     else
@@ -1146,8 +1226,11 @@ template <bool kSlabK>
 __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   uint32_t ticket;
+#if MPS_TRACE_ITEMS
+  uint64_t tr_setup, tr_levels;
+#endif
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
-    decode_bucket<false, kSlabK>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket);
+    decode_bucket<false, kSlabK>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket MPS_TR_ARG);
     end_bucket();
   }
 }
@@ -1168,18 +1251,17 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
 // than kMaxQueueItems work items.
 constexpr int64_t kMaxQueueItems = (int64_t(1) << 30) - 65536;
 
-// Item trace, in instrumented builds only (python -m mpserve_amd.build --define
-// MPS_TRACE_ITEMS=1 --out LIB; mpserve_amd.item_trace reads it): workgroup g <
-// kTraceWgs records its first kTraceItems items, 4 words each: the real-time
-// clock (100 MHz) at the item's start and after its end barrier, the item's
-// path << 40 | rows << 20 | k_eff, and its col_len. Thread 0 writes them with
-// ordinary stores after the barrier.
-#ifndef MPS_TRACE_ITEMS
-#define MPS_TRACE_ITEMS 0
-#endif
+// The item trace (instrumented builds): workgroup g < kTraceWgs records its
+// first kTraceItems items, 8 words each: the real-time clock (100 MHz) at the
+// item's start and after its end barrier, the item's path << 40 | rows << 20 |
+// k_eff, its col_len, the clock after the set-up's last barrier, the clock
+// when waves 0 and 15 finished their decode (before the end drain), and (word
+// 7) wave 0's ticks from its set-up start to its level-1 loads' return (low
+// half) and to its level-2 loads' return (high half). Threads 0 and 960 write
+// them with ordinary stores after the barrier.
 #if MPS_TRACE_ITEMS
-constexpr int kTraceWgs = 256, kTraceItems = 128;
-__device__ uint64_t g_item_trace[kTraceWgs * kTraceItems * 4];
+constexpr int kTraceWgs = 256, kTraceItems = 128, kTraceWords = 8;
+__device__ uint64_t g_item_trace[kTraceWgs * kTraceItems * kTraceWords];
 #endif
 
 template <bool kSlabK>
@@ -1196,21 +1278,32 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
       uint32_t ticket;
 #if MPS_TRACE_ITEMS
       const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
+      uint64_t tr_setup = 0, tr_levels = 0;
 #endif
       const mps_fp8_tensor &T = tensors[w.tensor];
-      decode_bucket<true, kSlabK>(T, T.out + out_delta, w, lds, status, queue, ticket);
+      decode_bucket<true, kSlabK>(T, T.out + out_delta, w, lds, status, queue, ticket MPS_TR_ARG);
+#if MPS_TRACE_ITEMS
+      const uint64_t tr_wave = __builtin_amdgcn_s_memrealtime();
+#endif
       const int64_t next = (int64_t)gridDim.x + ticket;
       // The next record (scalar registers) is loaded before the drain of this
       // item's stores, which covers its round trip.
       const WorkItem wn = work[next < nwork ? next : 0];
       end_bucket();
 #if MPS_TRACE_ITEMS
-      if (threadIdx.x == 0 && blockIdx.x < kTraceWgs && tr_it < kTraceItems) {
-        uint64_t *tp = g_item_trace + ((size_t)blockIdx.x * kTraceItems + tr_it) * 4;
-        tp[0] = tr0;
-        tp[1] = __builtin_amdgcn_s_memrealtime();
-        tp[2] = ((uint64_t)(uint32_t)w.path << 40) | ((uint64_t)(uint32_t)w.rows << 20) | (uint64_t)(uint32_t)w.k_eff;
-        tp[3] = (uint64_t)(uint32_t)w.cl;
+      if (blockIdx.x < kTraceWgs && tr_it < kTraceItems) {
+        uint64_t *tp = g_item_trace + ((size_t)blockIdx.x * kTraceItems + tr_it) * kTraceWords;
+        if (threadIdx.x == 0) {
+          tp[0] = tr0;
+          tp[1] = __builtin_amdgcn_s_memrealtime();
+          tp[2] = ((uint64_t)(uint32_t)w.path << 40) | ((uint64_t)(uint32_t)w.rows << 20) | (uint64_t)(uint32_t)w.k_eff;
+          tp[3] = (uint64_t)(uint32_t)w.cl;
+          tp[4] = tr_setup;
+          tp[5] = tr_wave;
+          tp[7] = tr_levels;
+        } else if (threadIdx.x == 960) {
+          tp[6] = tr_wave;
+        }
       }
       ++tr_it;
 #endif

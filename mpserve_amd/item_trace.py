@@ -8,11 +8,14 @@ then run one of the synthetic workloads through it::
 
 FP8 workloads (model8b, layer8b, layer70b): every workgroup of the plan kernel
 records, for its first 128 items, the real-time clock (100 MHz) at the item's
-start and after its end barrier. The summary gives the launch's span, when the
-workgroups ended (the tail), and a least-squares fit of an item's duration to
+start, after its set-up's last barrier, when waves 0 and 15 finish their
+decode, and after its end barrier. The summary gives the launch's span, when
+the workgroups ended (the tail), a least-squares fit of an item's duration to
 ``a + b * (elements one work-item decodes)``, whose intercept is the per-item
-set-up. AWQ workload (awq8b, both layouts at ``--k``): one record per
-workgroup, its duration by record kind.
+overhead, and the mean of each phase: set-up (start to the set-up barrier),
+decode (to the last of the two waves' ends) and drain (to the end barrier).
+AWQ workload (awq8b, both layouts at ``--k``): one record per workgroup, its
+duration by record kind.
 
 The decoded outputs are checked bit-exact against the inputs (ESC collisions of
 the AWQ row builder aside), so a trace comes from a correct launch.
@@ -82,12 +85,12 @@ def fp8_trace(lib_path: str, workload: str, k: int) -> Dict:
         torch.cuda.synchronize()
         _native.check(lib.mps_fp8_plan_decode(plan, h))
         torch.cuda.synchronize()
-        words = 256 * 128 * 4
+        words = 256 * 128 * 8
         buf = (ctypes.c_uint64 * words)()
         _native.check(lib.mps_item_trace_read(buf, words))
     finally:
         lib.mps_fp8_plan_destroy(plan)
-    a = np.frombuffer(buf, dtype=np.uint64).reshape(256, 128, 4).astype(np.int64)
+    a = np.frombuffer(buf, dtype=np.uint64).reshape(256, 128, 8).astype(np.int64)
     valid = a[:, :, 1] > 0
     t0 = int(a[:, :, 0][valid].min())
     rec = a[valid]
@@ -107,6 +110,22 @@ def fp8_trace(lib_path: str, workload: str, k: int) -> Dict:
            "busy_mean_us": round(float(busy.mean()), 1),
            "idle_at_end_frac": round(float(1.0 - busy.mean() / ends.max()), 4),
            "fit_all": _fit(per_lane, dur)}
+    setup = (rec[:, 4] - rec[:, 0]) / 100.0
+    wave_end = np.maximum(rec[:, 5], rec[:, 6])
+    decode = (wave_end - rec[:, 4]) / 100.0
+    drain = (rec[:, 1] - wave_end) / 100.0
+    skew = np.abs(rec[:, 5] - rec[:, 6]) / 100.0
+    out["phases_us"] = {"setup_mean": round(float(setup.mean()), 2), "setup_median": round(float(np.median(setup)), 2),
+                        "decode_mean": round(float(decode.mean()), 2), "drain_mean": round(float(drain.mean()), 2),
+                        "drain_median": round(float(np.median(drain)), 2),
+                        "wave0_wave15_skew_mean": round(float(skew.mean()), 2)}
+    out["fit_decode_phase"] = _fit(per_lane, decode)
+    lv = rec[:, 7]
+    if (lv != 0).any():
+        l1, l2 = (lv & 0xFFFFFFFF) / 100.0, (lv >> 32) / 100.0
+        out["setup_levels_us"] = {"level1_mean": round(float(l1.mean()), 2),
+                                  "level2_mean": round(float((l2 - l1).mean()), 2),
+                                  "after_level2_mean": round(float((setup - l2).mean()), 2)}
     if multi.any():
         out["fit_side_by_side"] = _fit(per_lane[multi], dur[multi])
         out["items_side_by_side"] = int(multi.sum())
