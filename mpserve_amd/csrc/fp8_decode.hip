@@ -913,8 +913,8 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
 #define MPS_TRACE_ITEMS 0
 #endif
 #if MPS_TRACE_ITEMS
-#define MPS_TR_PARAM , uint64_t &tr_setup, uint64_t &tr_levels
-#define MPS_TR_ARG , tr_setup, tr_levels
+#define MPS_TR_PARAM , uint64_t (&tr)[4]
+#define MPS_TR_ARG , tr
 #else
 #define MPS_TR_PARAM
 #define MPS_TR_ARG
@@ -1022,14 +1022,12 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   bool bad_row = (has_lo && (r_lo < 0 || r_lo >= T.n)) | (has_hi && (r_hi < 0 || r_hi >= T.n));
   const uint32_t rowoff_lo = has_lo ? (uint32_t)r_lo * (uint32_t)T.m + (uint32_t)c0 : 0u;
   const uint32_t rowoff_hi = has_hi ? (uint32_t)r_hi * (uint32_t)T.m + (uint32_t)c0 : 0u;
-  // Offset of the lane's first bitstream words (loaded below, after the
-  // tables), computed here: the wait for `pos` then falls before the table
-  // loads are issued, not at the join of their two paths, where it would wait
-  // for the tables too.
+  // Offset of the lane's first bitstream words (loaded after the table
+  // expansion), computed here: the wait for `pos` then falls before the table
+  // loads are issued, not at the join of their two paths.
   uint32_t off0 = active ? ((pos >> 5) & ~1u) * 4u : kBsPast;
   __asm__ volatile("" : "+v"(off0));
-  // Likewise the descriptor's bitstream fields (scalar loads), read before the
-  // table loads rather than where the words are loaded.
+  // Likewise the descriptor's bitstream fields (scalar loads).
   const uint8_t *bs_ptr = reinterpret_cast<const uint8_t *>(T.bitstream);
   int64_t bs_words = T.bitstream_words;
   __asm__ volatile("" : "+s"(bs_ptr), "+s"(bs_words));
@@ -1090,11 +1088,46 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     }
   }
 
+#if MPS_TRACE_ITEMS
+  __asm__ volatile("" ::"v"(sv[0].x), "v"(sv[3].w), "v"(nibs[0]), "v"(nibs[3]));
+  const uint64_t tr_l2 = __builtin_amdgcn_s_memrealtime();
+  tr[1] = ((tr_l1 - tr_start) & 0xFFFFFFFFull) | ((tr_l2 - tr_start) << 32);
+  if ((tid & 63) == 0) s_wflag[32 + (tid >> 6)] = (uint32_t)(tr_l2 - tr_start);
+#endif
+  uint32_t esc_seen = 0;
+#pragma unroll
+  for (int i = 0; i < kSlices; ++i) {
+    esc_seen |= nibs[i] & 0x88888888u;
+    // Entry j = sym_j << 16 | (nib_j & 7) | (nib_j & 8 ? 16 : 0). The nibbles go
+    // to bytes (even entries in `fl`, odd ones in `fh`), where nib + (nib & 8)
+    // is the entry's low byte; one byte permute per entry then joins it with
+    // the symbol (the high or low half of sv: entries 2c and 2c + 1 share word c).
+    const uint32_t lo = nibs[i] & 0x0F0F0F0Fu, hi = (nibs[i] >> 4) & 0x0F0F0F0Fu;
+    const uint32_t fl = lo + (lo & 0x08080808u), fh = hi + (hi & 0x08080808u);
+    const uint32_t w4[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+    uint32_t e[8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      e[2 * c] = __builtin_amdgcn_perm(w4[c], fl, 0x05040C00u | (uint32_t)c);      // [fl byte c, 0, sym lo]
+      e[2 * c + 1] = __builtin_amdgcn_perm(w4[c], fh, 0x07060C00u | (uint32_t)c);  // [fh byte c, 0, sym hi]
+    }
+    const uint32_t qt = (uint32_t)((tid >> 4) + 64 * i);  // the table's FP8 byte
+    uint32_t *tab = lut + qt * kTable;
+    *reinterpret_cast<uint4 *>(tab + (uint32_t)part * 8u) = make_uint4(e[0], e[1], e[2], e[3]);
+    *reinterpret_cast<uint4 *>(tab + (uint32_t)part * 8u + 4u) = make_uint4(e[4], e[5], e[6], e[7]);
+  }
+#if MPS_TRACE_ITEMS
+  const uint64_t tr_exp = __builtin_amdgcn_s_memrealtime();
+#endif
   // First four bitstream words of this lane (two 16-byte loads); the slab
-  // path queues all four, the others three. Issued after every other set-up
-  // load: a lane's words are scattered (64 lines a wave), and as the last loads
-  // in the in-order count the expansion below need not wait for them; the
-  // decode waits for them after it has issued its first FP8 loads.
+  // path queues all four, the others three. A lane's words are scattered (64
+  // lines a wave), and the CU's memory path takes its waves' loads in order:
+  // issued with the table loads they held back the later waves' tables (and so
+  // the barrier below); issued at the decode's start, their round trip added
+  // to it. Issued here, once the wave's own tables are in LDS, they overlap
+  // the other waves' expansion and the two barriers; the decode waits for them
+  // after issuing its first FP8 loads.
+  __builtin_amdgcn_sched_barrier(0);
   uint2 first[4];
   {
     const uint64_t bs_bytes = bs_words > 0 ? (uint64_t)bs_words * 8u : 0u;
@@ -1108,30 +1141,6 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
       first[2 * i + 1] = make_uint2(v[2], v[3]);
     }
   }
-  // Keep the expansion below the two loads (it waits for the tables only).
-  __builtin_amdgcn_sched_barrier(0);
-#if MPS_TRACE_ITEMS
-  __asm__ volatile("" ::"v"(sv[0].x), "v"(sv[3].w), "v"(nibs[0]), "v"(nibs[3]));
-  const uint64_t tr_l2 = __builtin_amdgcn_s_memrealtime();
-  tr_levels = ((tr_l1 - tr_start) & 0xFFFFFFFFull) | ((tr_l2 - tr_start) << 32);
-#endif
-  uint32_t esc_seen = 0;
-#pragma unroll
-  for (int i = 0; i < kSlices; ++i) {
-    const uint32_t s8[8] = {sv[i].x & 0xFFFFu, sv[i].x >> 16, sv[i].y & 0xFFFFu, sv[i].y >> 16,
-                            sv[i].z & 0xFFFFu, sv[i].z >> 16, sv[i].w & 0xFFFFu, sv[i].w >> 16};
-    esc_seen |= nibs[i] & 0x88888888u;
-    uint32_t e[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t nib = (nibs[i] >> (4 * j)) & 0xFu;
-      e[j] = (s8[j] << 16) | (nib & 7u) | ((nib & 8u) ? kEscBit : 0u);
-    }
-    const uint32_t qt = (uint32_t)((tid >> 4) + 64 * i);  // the table's FP8 byte
-    uint32_t *tab = lut + qt * kTable;
-    *reinterpret_cast<uint4 *>(tab + (uint32_t)part * 8u) = make_uint4(e[0], e[1], e[2], e[3]);
-    *reinterpret_cast<uint4 *>(tab + (uint32_t)part * 8u + 4u) = make_uint4(e[4], e[5], e[6], e[7]);
-  }
   // Block-wide ORs of "a row index is out of range" (bit 0) and "a table has an
   // ESC entry" (bit 1): one word per wave, written by its first lane. Wave 0's
   // word also carries the ticket (bits 2..31).
@@ -1141,16 +1150,26 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     if ((tid & 63) == 0) s_wflag[tid >> 6] = wf | (tk << 2);
   }
   __syncthreads();
+#if MPS_TRACE_ITEMS
+  const uint64_t tr_b1 = __builtin_amdgcn_s_memrealtime();
+  uint32_t tr_l2max = 0;
+  for (int w = 0; w < kBlock / 64; ++w) tr_l2max = max(tr_l2max, s_wflag[32 + w]);
+  tr[2] = ((tr_exp - tr_start) & 0xFFFFFFFFull) | ((tr_b1 - tr_start) << 32);
+  tr[3] = tr_l2max;
+#endif
   uint32_t bflags = 0;
 #pragma unroll
-  for (int w = 0; w < kBlock / 64; ++w) bflags |= s_wflag[w];
+  for (int w = 0; w < kBlock / 64; w += 4) {
+    const uint4 f = *reinterpret_cast<const uint4 *>(s_wflag + w);
+    bflags |= f.x | f.y | f.z | f.w;
+  }
   bflags = uni(bflags);
   ticket = bflags >> 2;
   const bool has_esc = (bflags & 2u) != 0;
   const bool any_bad_row = (bflags & 1u) != 0;
   __syncthreads();  // the flag words belong to the queue from here on
 #if MPS_TRACE_ITEMS
-  tr_setup = __builtin_amdgcn_s_memrealtime();
+  tr[0] = __builtin_amdgcn_s_memrealtime();
 #endif
 
   if (!bucket_ok || any_bad_row) {
@@ -1227,7 +1246,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   uint32_t ticket;
 #if MPS_TRACE_ITEMS
-  uint64_t tr_setup, tr_levels;
+  uint64_t tr[4];
 #endif
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
     decode_bucket<false, kSlabK>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket MPS_TR_ARG);
@@ -1255,12 +1274,14 @@ constexpr int64_t kMaxQueueItems = (int64_t(1) << 30) - 65536;
 // first kTraceItems items, 8 words each: the real-time clock (100 MHz) at the
 // item's start and after its end barrier, the item's path << 40 | rows << 20 |
 // k_eff, its col_len, the clock after the set-up's last barrier, the clock
-// when waves 0 and 15 finished their decode (before the end drain), and (word
-// 7) wave 0's ticks from its set-up start to its level-1 loads' return (low
-// half) and to its level-2 loads' return (high half). Threads 0 and 960 write
-// them with ordinary stores after the barrier.
+// when waves 0 and 15 finished their decode (before the end drain), and wave
+// 0's ticks from its set-up start: to its level-1 loads' return (word 7 low
+// half), its tables' return (word 7 high half), the end of its table expansion
+// (word 8 low half), the set-up's first barrier (word 8 high half) and the
+// last wave's tables (word 9). Threads 0 and 960 write them with ordinary
+// stores after the barrier; words 10 and 11 are spare.
 #if MPS_TRACE_ITEMS
-constexpr int kTraceWgs = 256, kTraceItems = 128, kTraceWords = 8;
+constexpr int kTraceWgs = 256, kTraceItems = 128, kTraceWords = 12;
 __device__ uint64_t g_item_trace[kTraceWgs * kTraceItems * kTraceWords];
 #endif
 
@@ -1278,7 +1299,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
       uint32_t ticket;
 #if MPS_TRACE_ITEMS
       const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
-      uint64_t tr_setup = 0, tr_levels = 0;
+      uint64_t tr[4] = {0, 0, 0, 0};
 #endif
       const mps_fp8_tensor &T = tensors[w.tensor];
       decode_bucket<true, kSlabK>(T, T.out + out_delta, w, lds, status, queue, ticket MPS_TR_ARG);
@@ -1298,9 +1319,11 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
           tp[1] = __builtin_amdgcn_s_memrealtime();
           tp[2] = ((uint64_t)(uint32_t)w.path << 40) | ((uint64_t)(uint32_t)w.rows << 20) | (uint64_t)(uint32_t)w.k_eff;
           tp[3] = (uint64_t)(uint32_t)w.cl;
-          tp[4] = tr_setup;
+          tp[4] = tr[0];
           tp[5] = tr_wave;
-          tp[7] = tr_levels;
+          tp[7] = tr[1];
+          tp[8] = tr[2];
+          tp[9] = tr[3];
         } else if (threadIdx.x == 960) {
           tp[6] = tr_wave;
         }

@@ -85,12 +85,12 @@ def fp8_trace(lib_path: str, workload: str, k: int) -> Dict:
         torch.cuda.synchronize()
         _native.check(lib.mps_fp8_plan_decode(plan, h))
         torch.cuda.synchronize()
-        words = 256 * 128 * 8
+        words = 256 * 128 * 12
         buf = (ctypes.c_uint64 * words)()
         _native.check(lib.mps_item_trace_read(buf, words))
     finally:
         lib.mps_fp8_plan_destroy(plan)
-    a = np.frombuffer(buf, dtype=np.uint64).reshape(256, 128, 8).astype(np.int64)
+    a = np.frombuffer(buf, dtype=np.uint64).reshape(256, 128, 12).astype(np.int64)
     valid = a[:, :, 1] > 0
     t0 = int(a[:, :, 0][valid].min())
     rec = a[valid]
@@ -126,6 +126,13 @@ def fp8_trace(lib_path: str, workload: str, k: int) -> Dict:
         out["setup_levels_us"] = {"level1_mean": round(float(l1.mean()), 2),
                                   "level2_mean": round(float((l2 - l1).mean()), 2),
                                   "after_level2_mean": round(float((setup - l2).mean()), 2)}
+        w8, w9 = rec[:, 8], rec[:, 9]
+        if (w8 != 0).any():
+            exp_end, b1 = (w8 & 0xFFFFFFFF) / 100.0, (w8 >> 32) / 100.0
+            out["setup_levels_us"].update({
+                "last_wave_tables_mean": round(float((w9 / 100.0).mean()), 2),
+                "wave0_expansion_end_mean": round(float(exp_end.mean()), 2),
+                "first_barrier_mean": round(float(b1.mean()), 2)})
     if multi.any():
         out["fit_side_by_side"] = _fit(per_lane[multi], dur[multi])
         out["items_side_by_side"] = int(multi.sum())
