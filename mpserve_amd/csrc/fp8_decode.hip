@@ -935,7 +935,7 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
-  uint32_t *s_wflag = qregion + 5 * kBlock;                             // queue slot 5: one word per wave
+  uint32_t *s_wflag = qregion + 5 * kBlock;                             // queue slot 5: the waves' flag words
   // The work-item id through an opaque move: the per-lane constants of every
   // decode path derive from it, and hoisted out of the bucket loop they would
   // all stay live across the set-up, which then runs out of VGPRs.
@@ -1142,12 +1142,16 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     }
   }
   // Block-wide ORs of "a row index is out of range" (bit 0) and "a table has an
-  // ESC entry" (bit 1): one word per wave, written by its first lane. Wave 0's
-  // word also carries the ticket (bits 2..31).
+  // ESC entry" (bit 1): one word per wave; wave 0's also carries the ticket
+  // (bits 2..31). Every wave gets its own copy of the 16 words, in its own
+  // queue columns: wave w's lane i writes the word to column 64 i + w, and wave
+  // i reads columns 64 i .. 64 i + 15. Only wave i writes those columns later
+  // (its queue), after reading them, so no second barrier has to keep a fast
+  // wave's queue from overwriting words a slower wave has not read yet.
   {
     const uint32_t wf = (__builtin_amdgcn_ballot_w64(bad_row) ? 1u : 0u) |
-                        (__builtin_amdgcn_ballot_w64(esc_seen != 0) ? 2u : 0u);
-    if ((tid & 63) == 0) s_wflag[tid >> 6] = wf | (tk << 2);
+                        (__builtin_amdgcn_ballot_w64(esc_seen != 0) ? 2u : 0u) | (uni(tk) << 2);
+    if ((tid & 63) < kBlock / 64) s_wflag[((tid & 63) << 6) | (tid >> 6)] = wf;
   }
   __syncthreads();
 #if MPS_TRACE_ITEMS
@@ -1158,16 +1162,18 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
   tr[3] = tr_l2max;
 #endif
   uint32_t bflags = 0;
+  {
+    const uint32_t *mine = s_wflag + (uni((uint32_t)tid) & ~63u);  // this wave's copy
 #pragma unroll
-  for (int w = 0; w < kBlock / 64; w += 4) {
-    const uint4 f = *reinterpret_cast<const uint4 *>(s_wflag + w);
-    bflags |= f.x | f.y | f.z | f.w;
+    for (int w = 0; w < kBlock / 64; w += 4) {
+      const uint4 f = *reinterpret_cast<const uint4 *>(mine + w);
+      bflags |= f.x | f.y | f.z | f.w;
+    }
   }
   bflags = uni(bflags);
   ticket = bflags >> 2;
   const bool has_esc = (bflags & 2u) != 0;
   const bool any_bad_row = (bflags & 1u) != 0;
-  __syncthreads();  // the flag words belong to the queue from here on
 #if MPS_TRACE_ITEMS
   tr[0] = __builtin_amdgcn_s_memrealtime();
 #endif
