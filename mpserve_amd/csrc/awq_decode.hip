@@ -60,7 +60,17 @@ constexpr int kStage = 4;   // chunks staged a block: one 16-byte aligned quad
 constexpr int kQueue = 8;
 static_assert((kDepth * kAwqL + 31) / 32 <= kQueue - kStage, "a block's codes must fit the queue after an append");
 
-__device__ __forceinline__ void flag(uint32_t *status, unsigned int f) { atomicOr(status, f); }
+// A global-address-space atomic, not a generic one: an outstanding generic
+// (flat) access makes the compiler turn every later memory wait into a full one.
+__device__ __forceinline__ void flag(uint32_t *status, unsigned int f) {
+  __hip_atomic_fetch_or((__attribute__((address_space(1))) uint32_t *)(status), f, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT);
+}
+// A load through a global pointer, for the same reason.
+template <typename V>
+__device__ __forceinline__ V gload(const V *p) {
+  return *(const __attribute__((address_space(1))) V *)(p);
+}
 
 // Stream chunk c (32 bits, stream order) of u64 words stored little-endian:
 // word w's first 32 stream bits are u32 2w+1. Past the end the last chunk is
@@ -774,6 +784,14 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   const uint32_t pos_end = __builtin_amdgcn_raw_buffer_load_b32(
       r_end, live | (to_ck ? (((ck0 + 1u) << ks) + t) * 4u : (t + 1u) * 4u), 0, 0);
   const uint64_t bucket_bit = (uint64_t)T.bucket_bit_base[b];
+  // Offset of the lane's first bitstream words and the descriptor's bitstream
+  // fields, computed here, before the table loads (the words themselves are
+  // loaded after the table expansion).
+  uint32_t off0 = ((pos >> 5) & ~1u) * 4u;
+  __asm__ volatile("" : "+v"(off0));
+  const uint8_t *bs_ptr = reinterpret_cast<const uint8_t *>(T.bitstream);
+  int64_t bs_words = T.bitstream_words;
+  __asm__ volatile("" : "+s"(bs_ptr), "+s"(bs_words));
   // level 2
   const bool tab_ok = gq >= 0 && gq < T.num_tables;
   const bool tab_load = tables && tab_ok;
@@ -790,49 +808,59 @@ __device__ __forceinline__ void awq_slab_bucket(const mps_awq_tensor &T, const A
   }
   const auto ln = __builtin_amdgcn_raw_buffer_load_b128(
       r_lens, tab_load ? (uint32_t)gq * (uint32_t)kAwqPacked + (uint32_t)c * 16u : kSlabBsPast, 0, 0);
-  uint2 first[4];
-  {
-    const uint64_t bs_bytes = T.bitstream_words > 0 ? (uint64_t)T.bitstream_words * 8u : 0u;
-    const uint64_t base_byte = bucket_bit >> 3;
-    const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
-    const __amdgpu_buffer_rsrc_t r_bs = awq_rsrc(
-        reinterpret_cast<const uint8_t *>(T.bitstream) + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
-    const uint32_t off0 = ((pos >> 5) & ~1u) * 4u;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const auto x = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off0 + 16u * (uint32_t)i, 0, 0);
-      first[2 * i] = make_uint2(x[0], x[1]);
-      first[2 * i + 1] = make_uint2(x[2], x[3]);
-    }
-  }
   if (tables && tid == 0) {
     bool bad = false;
 #pragma unroll
     for (int qq = 0; qq < 16; ++qq) {
-      const int32_t id = T.bucket_table[b * 16 + qq];
+      const int32_t id = gload(T.bucket_table + b * 16 + qq);
       bad |= id < -1 || id >= T.num_tables;
     }
     if (bad) flag(status, MPS_STATUS_BAD_TABLE);
   }
   // expansion: entry p of value q = sym << 16 | (nibble 15 ? 27 : nibble); a
-  // missing table is all ESC entries, as the reference decodes it
+  // missing table is all ESC entries, as the reference decodes it. The
+  // nibbles go to bytes (even entries in `fl`, odd ones in `fh`); a byte b
+  // becomes b + 12 when it is 15 (the carry of b + 1 into bit 4, times 3/4
+  // of 16), and one byte permute per entry joins it with its symbol.
   uint32_t esc_seen = tab_ok ? 0u : 1u;
   if (tables) {
     const uint32_t nib32[4] = {ln[0], ln[1], ln[2], ln[3]};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t s8[8] = {sv[i].x & 0xFFFFu, sv[i].x >> 16, sv[i].y & 0xFFFFu, sv[i].y >> 16,
-                              sv[i].z & 0xFFFFu, sv[i].z >> 16, sv[i].w & 0xFFFFu, sv[i].w >> 16};
+      const uint32_t lo = nib32[i] & 0x0F0F0F0Fu, hi = (nib32[i] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t el = ((lo + 0x01010101u) & 0x10101010u) >> 2, eh = ((hi + 0x01010101u) & 0x10101010u) >> 2;
+      esc_seen |= el | eh;
+      const uint32_t fl = tab_ok ? lo + el + (el << 1) : 0x1B1B1B1Bu;
+      const uint32_t fh = tab_ok ? hi + eh + (eh << 1) : 0x1B1B1B1Bu;
+      const uint32_t w4[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};  // zero for a missing table
       uint32_t e[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t nib = (nib32[i] >> (4 * j)) & 15u;  // entry 8i + j: byte (8i + j) / 2, low nibble first
-        esc_seen |= nib == 15u ? 1u : 0u;
-        e[j] = tab_ok ? ((s8[j] << 16) | (nib == 15u ? kAwqEscLow : nib)) : kAwqEscLow;
+      for (int cc = 0; cc < 4; ++cc) {
+        e[2 * cc] = __builtin_amdgcn_perm(w4[cc], fl, 0x05040C00u | (uint32_t)cc);
+        e[2 * cc + 1] = __builtin_amdgcn_perm(w4[cc], fh, 0x07060C00u | (uint32_t)cc);
       }
       uint4 *dst = reinterpret_cast<uint4 *>(lut + (q << kAwqL) + 32 * c + 8 * i);
       dst[0] = make_uint4(e[0], e[1], e[2], e[3]);
       dst[1] = make_uint4(e[4], e[5], e[6], e[7]);
+    }
+  }
+  // The lane's first four bitstream words (two 16-byte loads), issued once the
+  // wave's own tables are in LDS: issued before, these scattered loads (64
+  // lines a wave) queued ahead of the other waves' table loads; here they
+  // overlap the other waves' expansion and the barriers, and the decode waits
+  // for them after issuing its first int4 loads.
+  __builtin_amdgcn_sched_barrier(0);
+  uint2 first[4];
+  {
+    const uint64_t bs_bytes = bs_words > 0 ? (uint64_t)bs_words * 8u : 0u;
+    const uint64_t base_byte = bucket_bit >> 3;
+    const uint32_t win_bytes = base_byte < bs_bytes ? (uint32_t)(bs_bytes - base_byte) : 0u;
+    const __amdgpu_buffer_rsrc_t r_bs = awq_rsrc(bs_ptr + (base_byte < bs_bytes ? base_byte : 0), win_bytes);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(r_bs, off0 + 16u * (uint32_t)i, 0, 0);
+      first[2 * i] = make_uint2(x[0], x[1]);
+      first[2 * i + 1] = make_uint2(x[2], x[3]);
     }
   }
   // group bases of this wave for slabs wl and wl + 64 (by-scale), or the
