@@ -931,7 +931,7 @@ __device__ __forceinline__ WorkItem bucket_item(const mps_fp8_tensor &T, int64_t
 template <bool kQueue, bool kSlabK>
 __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t *out, const WorkItem &w,
                                               uint32_t *lds, uint32_t *status, uint32_t *queue,
-                                              uint32_t &ticket MPS_TR_PARAM) {
+                                              uint32_t &ticket, int32_t wg_part, int32_t wg_parts MPS_TR_PARAM) {
   uint32_t *qregion = lds;
   uint32_t *lut = lds + kQWords;
   int32_t *s_rows = reinterpret_cast<int32_t *>(qregion) + 6 * kBlock;    // queue slot 6 (generic path)
@@ -1183,6 +1183,14 @@ __device__ __forceinline__ void decode_bucket(const mps_fp8_tensor &T, uint16_t 
     return;
   }
   if (!active) return;
+  // A bucket shared by `wg_parts` workgroups (the single-tensor kernel, few
+  // buckets for the CUs): every one expands the tables; on the k = 1024 paths
+  // workgroup `wg_part` then decodes the substreams of waves
+  // [16 wg_part / wg_parts, 16 (wg_part + 1) / wg_parts), on the others part 0 decodes all.
+  if (wg_parts > 1) {
+    const int32_t wv = (int32_t)(uni((uint32_t)tid) >> 6);
+    if (k1024 ? (wv * wg_parts / (kBlock / 64) != wg_part) : (wg_part != 0)) return;
+  }
   if (k1024) {
     const uint32_t P = (uint32_t)cl / 1024u;
     if (P >= 4) {
@@ -1248,14 +1256,27 @@ __device__ __forceinline__ void end_bucket() {
 // not also pay a workgroup launch. fp8_decode_one deals the buckets
 // round-robin; every workgroup runs the same uniform loop to its end.
 template <bool kSlabK>
-__global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status) {
+//
+// parts > 1 (k = 1024 tensors with fewer buckets than CUs): the grid is
+// buckets x parts, and workgroup g decodes part g % parts of bucket g / parts
+// (decode_bucket), so that a tensor of 8 buckets runs on 128 CUs instead of 8.
+// A bucket's substreams are sequential chains, which only lane checkpoints (a
+// plan's) cut into row ranges; fewer waves a CU run each chain faster.
+__global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint32_t *status, int32_t parts) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsWords];
   uint32_t ticket;
 #if MPS_TRACE_ITEMS
   uint64_t tr[4];
 #endif
+  if (parts > 1) {
+    const int64_t b = (int64_t)blockIdx.x / parts;
+    if (b < T.num_buckets)
+      decode_bucket<false, kSlabK>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket,
+                                   (int32_t)(blockIdx.x % parts), parts MPS_TR_ARG);
+    return;
+  }
   for (int64_t b = blockIdx.x; b < T.num_buckets; b += gridDim.x) {
-    decode_bucket<false, kSlabK>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket MPS_TR_ARG);
+    decode_bucket<false, kSlabK>(T, T.out, bucket_item(T, b), lds, status, nullptr, ticket, 0, 1 MPS_TR_ARG);
     end_bucket();
   }
 }
@@ -1308,7 +1329,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_plan(const mps_fp8_tensor *
       uint64_t tr[4] = {0, 0, 0, 0};
 #endif
       const mps_fp8_tensor &T = tensors[w.tensor];
-      decode_bucket<true, kSlabK>(T, T.out + out_delta, w, lds, status, queue, ticket MPS_TR_ARG);
+      decode_bucket<true, kSlabK>(T, T.out + out_delta, w, lds, status, queue, ticket, 0, 1 MPS_TR_ARG);
 #if MPS_TRACE_ITEMS
       const uint64_t tr_wave = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -1618,8 +1639,12 @@ constexpr int kPlanQueues = 32;
 constexpr size_t kQueueStride = 64;
 // A work item's set-up (tables into the LDS, the lanes' first loads, the
 // pipeline's fill and drain) costs about as long as decoding this many
-// elements; plans weigh items by their elements plus this.
-constexpr int64_t kItemSetup = 65536;
+// elements; plans weigh items by their elements plus this. (Tuning builds:
+// MPS_ITEM_SETUP.)
+#ifndef MPS_ITEM_SETUP
+#define MPS_ITEM_SETUP 65536
+#endif
+constexpr int64_t kItemSetup = MPS_ITEM_SETUP;
 size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 }  // namespace
 
@@ -1697,12 +1722,24 @@ int mps_fp8_decode(const mps_fp8_tensor *tensor, int64_t max_len, void *stream) 
   unsigned grid = 0;
   rc = persistent_grid(tensor->num_buckets, &grid);
   if (rc != MPS_OK) return rc;
+  // Few buckets for the CUs (k = 1024): each bucket shared by `parts`
+  // workgroups, the largest power of two up to 16 (one wave each) that keeps
+  // buckets x parts within the CUs.
+  int32_t parts = 1;
+  {
+    int dev2 = 0, cus = 0;
+    MPS_HIP_CHECK(hipGetDevice(&dev2));
+    MPS_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev2));
+    if (tensor->k == kBlock)
+      while (parts < kBlock / 64 && tensor->num_buckets * parts * 2 <= (int64_t)cus) parts *= 2;
+    if (parts > 1) grid = (unsigned)(tensor->num_buckets * parts);
+  }
   if (slab_k(tensor->k))
     hipLaunchKernelGGL(fp8_decode_one<true>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                       *tensor, status);
+                       *tensor, status, parts);
   else
     hipLaunchKernelGGL(fp8_decode_one<false>, dim3(grid), dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                       *tensor, status);
+                       *tensor, status, parts);
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;
 }

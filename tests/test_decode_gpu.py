@@ -658,3 +658,32 @@ def test_one_plan_on_two_streams_at_once():
     from mpserve_amd.mpserve_cuda import read_status
 
     assert read_status(torch.device(DEV)) == 0
+
+
+@pytest.mark.parametrize("n,m,scalar,outlier_p,seed", [
+    (256, 8192, True, 0.0, 280),     # 2 buckets: 16 workgroups each, one wave apiece
+    (1024, 8192, True, 0.0, 281),    # 8 buckets (a 70B k_proj's count)
+    (300, 14336, False, 0.0, 282),   # per-row scales, P = 14: groups straddle rows
+    (128, 2048, True, 0.0, 283),     # P = 2: groups span rows
+    (512, 8192, True, 1e-3, 284),    # ESC codes (one scale key with outliers)
+    (4096, 1024, False, 0.0, 285),   # many buckets: no sharing
+])
+def test_op_whole_buckets_shared_by_workgroups(monkeypatch, n, m, scalar, outlier_p, seed):
+    """With plans off, huffman_decode_fp8 launches whole buckets; a k = 1024
+    tensor with fewer buckets than CUs has each bucket shared by several
+    workgroups, each decoding some of its waves' substreams. Bit-exact,
+    status clear, every path of the slab decode."""
+    import MPServe_cuda
+
+    monkeypatch.setenv("MPSERVE_DECODE_PLANS", "0")
+    bf, q, sc_u16 = synth(n, m, seed=seed, outlier_p=outlier_p)
+    sc = oracle.encode(bf, q, sc_u16[:1].copy() if scalar else sc_u16, 7, 1024)
+    sc_t = to_torch(sc, DEV)
+    q_t = torch.from_numpy(q).to(DEV)
+    _status()
+    for _ in range(2):
+        out = torch.full((n, m), float("nan"), dtype=torch.bfloat16, device=DEV)
+        MPServe_cuda.huffman_decode_fp8(*decode_args(sc_t, q_t), out=out)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.view(torch.uint16).cpu().numpy(), bf)
+    assert _status() == 0
