@@ -1298,7 +1298,7 @@ __global__ __launch_bounds__(kBlock) void fp8_decode_one(mps_fp8_tensor T, uint3
 constexpr int64_t kMaxQueueItems = (int64_t(1) << 30) - 65536;
 
 // The item trace (instrumented builds): workgroup g < kTraceWgs records its
-// first kTraceItems items, 8 words each: the real-time clock (100 MHz) at the
+// first kTraceItems items, kTraceWords words each: the real-time clock (100 MHz) at the
 // item's start and after its end barrier, the item's path << 40 | rows << 20 |
 // k_eff, its col_len, the clock after the set-up's last barrier, the clock
 // when waves 0 and 15 finished their decode (before the end drain), and wave
