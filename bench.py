@@ -77,6 +77,8 @@ def parse_args(argv=None):
                         "awq8b: AWQ int4 decode of one 8B layer, both layouts")
     p.add_argument("--awq-k", type=int, default=1024,
                    help="substreams per bucket of the AWQ sidecars (the reference builders default to 256)")
+    p.add_argument("--awq-layout", choices=("by_scale", "row_buckets"), default="by_scale",
+                   help="--compare-libs --workload awq8b: the sidecar layout whose layer plan is timed")
     p.add_argument("--fp8-k", type=int, default=1024,
                    help="--compare-libs on an FP8 workload: substreams per bucket of its sidecars (the headline uses "
                         "1024; the reference's compress script defaults to 1024, its builder to 256)")
@@ -795,7 +797,8 @@ def compare_libs(args, dev) -> int:
     launches per library per round, the order reversed every other round. Box-to-box
     spread is several percent; within one process it is about 0.1%, which is what
     tuning the kernels' compile-time knobs needs. ``--workload awq8b`` compares the
-    AWQ by-scale layer's plan (group 128, k = --awq-k); otherwise an FP8 workload's."""
+    AWQ layer's plan (group 128, k = --awq-k, layout --awq-layout); otherwise an FP8
+    workload's."""
     import ctypes
     import statistics
 
@@ -814,8 +817,9 @@ def compare_libs(args, dev) -> int:
 
         workload, kind, tensor_t = "awq8b", "awq", _native.MpsAwqTensor
         for j, (name, n, m, _, _, _) in enumerate(config_weights("layer8b")):
-            w = make_awq_weight(n, m, 128, seed=300 + j, device=dev)
-            sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, args.awq_k, 1024, True)
+            by_scale = args.awq_layout == "by_scale"  # row buckets: one scale per row, as awq_result builds them
+            w = make_awq_weight(n, m, 128 if by_scale else None, seed=300 + j, device=dev)
+            sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, args.awq_k, 1024, by_scale)
             o = torch.empty((n, m), dtype=torch.bfloat16, device=dev)
             entries.append((name, w.int4_u8, sc, w.bf16))
             outs.append(o)
@@ -830,7 +834,7 @@ def compare_libs(args, dev) -> int:
         outs = [torch.empty(src.shape, dtype=torch.bfloat16, device=dev) for _, _, _, src in entries]
         descs = [_descriptor(*sidecar_decode_args(f, sc)[:13], o) for (_, f, sc, _), o in zip(entries, outs)]
     arr = (tensor_t * len(descs))(*descs)
-    libs = []
+    libs, first_out = [], None
     for path in args.compare_libs:
         L = ctypes.CDLL(os.path.abspath(path))
         vp = ctypes.c_void_p
@@ -853,9 +857,16 @@ def compare_libs(args, dev) -> int:
         read_status(plan, h, ctypes.byref(st))
         exact = None if args.no_verify else all(
             torch.equal(o.view(torch.uint16), src.view(torch.uint16)) for o, (_, _, _, src) in zip(outs, entries))
-        log(f"{path}: status {st.value}, bit-exact {exact}")
+        # Row-bucket AWQ sidecars with ESC collisions do not round-trip (in the
+        # reference's format as here): every build must then give the first one's output.
+        same = None
+        if not args.no_verify:
+            if first_out is None:
+                first_out = [o.clone() for o in outs]
+            same = all(torch.equal(o, f) for o, f in zip(outs, first_out))
+        log(f"{path}: status {st.value}, bit-exact {exact}, same output as the first library {same}")
         libs.append({"path": path, "plan": plan, "decode": decode, "destroy": destroy, "status": st.value,
-                     "bit_exact": exact, "ms": []})
+                     "bit_exact": exact, "same_as_first": same, "ms": []})
     for r in range(args.compare_rounds):
         for lib in (libs if r % 2 == 0 else libs[::-1]):
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
@@ -872,7 +883,7 @@ def compare_libs(args, dev) -> int:
         med = statistics.median(lib["ms"])
         rows.append({"lib": lib["path"], "median_ms": round(med, 4), "vs_first": round(med / base - 1, 4),
                      "rounds_ms": [round(x, 4) for x in lib["ms"]], "status": lib["status"],
-                     "bit_exact": lib["bit_exact"]})
+                     "bit_exact": lib["bit_exact"], "same_as_first": lib["same_as_first"]})
         lib["destroy"](lib["plan"])
     print(json.dumps({"metric": "plan launch ms per library build (one process, interleaved)",
                       "workload": WORKLOADS[workload], "device": torch.cuda.get_device_name(dev),

@@ -321,8 +321,10 @@ __device__ __forceinline__ void awq_bucket(const mps_awq_tensor &T, int64_t b, i
 
 template <int kSplit>
 __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T, uint32_t *status) {
-  __shared__ uint32_t lut[kLutEntries];
-  __shared__ uint32_t s_base[kRowSlots];
+  // Row offsets (the slab path's queue) first: the tables' base then rides in
+  // the LDS instructions' offset field, and the queue's address needs no add.
+  __shared__ __attribute__((aligned(16))) uint32_t lds[kRowSlots + kLutEntries];
+  uint32_t *s_base = lds, *lut = lds + kRowSlots;
   awq_bucket<kSplit>(T, blockIdx.x / kSplit, (int)(blockIdx.x % kSplit), lut, s_base, status);
 }
 
@@ -411,7 +413,10 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   constexpr int DF = MPS_AWQ_SLAB_PREFETCH;  // int4 prefetch distance (steps)
   constexpr int FE = MPS_AWQ_FEED_EVERY;     // steps per bitstream feed (16 bytes: 2 x 44 bits fit)
   static_assert(DF % FE == 0 && (FE == 1 || FE == 2), "a feed every one or two steps");
-  constexpr int RB = 4;  // 16-byte blocks per bitstream request
+#ifndef MPS_AWQ_RB
+#define MPS_AWQ_RB 4
+#endif
+  constexpr int RB = MPS_AWQ_RB;  // 16-byte blocks per bitstream request
   static_assert(kShift == 10 || (kShift == 0 && kLay != kLayRowsWrap), "k < 1024: no steps across rows");
   count = awq_uni(count);
   kshift = kShift ? (uint32_t)kShift : awq_uni(kshift);
@@ -430,6 +435,7 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
 
   const uint32_t lane4 = qlane << 2;
   const uint32_t R = (lane >> 4) & 3u;
+  const uint32_t R4 = R << 2;
   const uint32_t v4 = (lane & 15u) << 2;
   const char *qbytes = reinterpret_cast<const char *>(queue);
   const char *lbytes = reinterpret_cast<const char *>(lut);
@@ -472,6 +478,29 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     }
     return w;
   };
+#ifndef MPS_AWQ_WIN64
+#define MPS_AWQ_WIN64 1
+#endif
+  // 64 stream bits at -npv as {hi, lo}: three queue chunks, or memory for
+  // lanes whose queue lacks the third.
+  auto window64 = [&](uint32_t npv, uint32_t &hi, uint32_t &lo) {
+    const uint32_t t7 = npv << 7;
+    uint32_t c0 = *reinterpret_cast<const uint32_t *>(qbytes + ((t7 & 0x7000u) | lane4));
+    uint32_t c1 = *reinterpret_cast<const uint32_t *>(qbytes + (((t7 - 4096u) & 0x7000u) | lane4));
+    uint32_t c2 = *reinterpret_cast<const uint32_t *>(qbytes + (((t7 - 8192u) & 0x7000u) | lane4));
+    const bool dry = (int32_t)(wqb + npv) <= 63;
+    if (__builtin_amdgcn_ballot_w64(dry)) {
+      if (dry) {
+        const uint32_t h = (~npv) >> 5;
+        c0 = chunk_mem(h);
+        c1 = chunk_mem(h + 1u);
+        c2 = chunk_mem(h + 2u);
+        __asm__ volatile("" ::"v"(c0), "v"(c1), "v"(c2));  // wait for the loads here, not at a later join
+      }
+    }
+    hi = __builtin_amdgcn_alignbit(c0, c1, npv);
+    lo = __builtin_amdgcn_alignbit(c1, c2, npv);
+  };
   // Register reserve of up to RB 16-byte blocks after the queue's last chunk,
   // refilled by aligned 64-byte requests that land in inb.
   uint4 rv[RB], inb[RB];
@@ -479,15 +508,25 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   for (int i = 0; i < RB; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
   uint32_t rcnt = 0, ninb = 0;
   bool ifl = false;
+  // A feed writes chunks h .. h + 3 (h = wqb / 32, even) as two slot pairs,
+  // ((~h) >> 1) & 3 and the one below; the next feed's h is 4 more, so both
+  // pair indices flip bit 1: their byte addresses are kept and XORed with 0x4000.
+  char *const qw = reinterpret_cast<char *>(queue);
+  uint32_t fa = ((((~(wqb >> 5)) << 10) & 0x1800u) | qlane) << 2;
+  uint32_t fb = ((((~((wqb >> 5) + 2u)) << 10) & 0x1800u) | qlane) << 2;
   auto feed = [&]() {
     const bool f = rcnt != 0u && (int32_t)(wqb + np) < 128;
     if (f) {
-      const uint32_t h = wqb >> 5;
-      put_pair(h, rv[0].y, rv[0].x);
-      put_pair(h + 2u, rv[0].w, rv[0].z);
+      *reinterpret_cast<uint32_t *>(qw + fa) = rv[0].x;          // chunk h + 1
+      *reinterpret_cast<uint32_t *>(qw + fa + 4096u) = rv[0].y;  // chunk h
+      *reinterpret_cast<uint32_t *>(qw + fb) = rv[0].z;          // chunk h + 3
+      *reinterpret_cast<uint32_t *>(qw + fb + 4096u) = rv[0].w;  // chunk h + 2
 #pragma unroll
       for (int i = 0; i + 1 < RB; ++i) rv[i] = rv[i + 1];
     }
+    const uint32_t flip = f ? 0x4000u : 0u;
+    fa ^= flip;
+    fb ^= flip;
     wqb += f ? 128u : 0u;
     rcnt -= f ? 1u : 0u;
   };
@@ -540,11 +579,12 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   auto load_step = [&](uint32_t &F) -> uint32_t {
     uint32_t ret;
     if constexpr (kLay == kLayGroups) {
-      const uint32_t sl = 4u * w_g + R;  // this lane's slab
-      const bool hi = w_g >= 16u;        // slabs 4g .. 4g+3 are all below 64 or all above
+      // this lane's slab is 4 w_g + R: its base sits in lane (4 w_g + R) & 63 of
+      // base_lo (slabs below 64) or base_hi (the four slabs are all below or all above)
+      const bool hi = w_g >= 16u;
       const uint32_t src = hi ? base_hi : base_lo;
-      const uint32_t base = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((sl & 63u) << 2), (int)src);
-      const bool ok = sl < count;
+      const uint32_t base = (uint32_t)__builtin_amdgcn_ds_bpermute((int)(((w_g << 4) + R4) & 0xFCu), (int)src);
+      const bool ok = (int32_t)R < (int32_t)awq_uni(count - 4u * w_g);
       const uint32_t off = base + v4;
       F = __builtin_amdgcn_raw_buffer_load_b32(r_q, ok ? off : kSlabInPast, 0, 0);
       ret = ok ? off << 1 : kSlabOutPast;
@@ -588,6 +628,38 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     const uint32_t fq = __builtin_amdgcn_perm(p2[1], p2[0], selB);  // byte j = element j's int4 byte
     const uint32_t np0 = np;
     uint32_t e[4];
+#if MPS_AWQ_WIN64
+    {
+      // 64 stream bits at -np: the first two codes come from the high word; the
+      // second window starts where they end, cut from the same two words.
+      uint32_t hi, lo;
+      window64(np, hi, lo);
+      uint32_t s = 19u;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (!kTail || (uint32_t)j < tail) {
+          e[j] = lookup(fq >> (8 * j), __builtin_amdgcn_alignbit(hi, hi, s));
+          s -= e[j];
+        } else {
+          e[j] = 0u;
+        }
+      }
+      // the window 19 - s bits on: ({hi, lo} >> (32 - (19 - s)))[31:0] (the
+      // shift is taken mod 32, so the entries' high bits in s do not matter)
+      const uint32_t win = __builtin_amdgcn_alignbit(hi, lo, s + 13u);
+      uint32_t s2 = 19u;
+#pragma unroll
+      for (int j = 2; j < 4; ++j) {
+        if (!kTail || (uint32_t)j < tail) {
+          e[j] = lookup(fq >> (8 * j), __builtin_amdgcn_alignbit(win, win, s2));
+          s2 -= e[j];
+        } else {
+          e[j] = 0u;
+        }
+      }
+      np += (uint32_t)((int32_t)(s << 16) >> 16) + (uint32_t)((int32_t)(s2 << 16) >> 16) - 38u;
+    }
+#else
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t win = window(np);
@@ -604,26 +676,27 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
       }
       np += (uint32_t)((int32_t)(s << 16) >> 16) - 19u;  // minus the bits consumed
     }
+#endif
     if constexpr (kEsc) {
-      const bool esc = ((e[0] | e[1] | e[2] | e[3]) & kAwqEscBit) != 0u;
-      if (__builtin_amdgcn_ballot_w64(esc)) {
-        if (esc) {
-          uint32_t p = np0;
+      // A wave with an ESC code in the step decodes the step again one code at
+      // a time, every lane: the slow decode gives the fast one's result where
+      // there is no ESC, so no lane needs to be masked off.
+      if (__builtin_amdgcn_ballot_w64(((e[0] | e[1] | e[2] | e[3]) & kAwqEscBit) != 0u)) {
+        uint32_t p = np0;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if (!kTail || (uint32_t)j < tail) {
-              const uint32_t w = window(p);
-              uint32_t ent = lookup(fq >> (8 * j), w >> 19);
-              p -= ent & 15u;
-              if (ent & kAwqEscBit) {
-                ent = window(p) & 0xFFFF0000u;  // the symbol: the 16 raw bits after the code
-                p -= 16u;
-              }
-              e[j] = ent;
+        for (int j = 0; j < 4; ++j) {
+          if (!kTail || (uint32_t)j < tail) {
+            const uint32_t w = window(p);
+            uint32_t ent = lookup(fq >> (8 * j), w >> 19);
+            p -= ent & 15u;
+            if (ent & kAwqEscBit) {
+              ent = window(p) & 0xFFFF0000u;  // the symbol: the 16 raw bits after the code
+              p -= 16u;
             }
+            e[j] = ent;
           }
-          np = p;
         }
+        np = p;
       }
     }
     const auto t0 = __builtin_amdgcn_permlane32_swap(e[0], e[2], false, false);
@@ -1248,8 +1321,8 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tenso
                                                              const AwqWork *__restrict__ work,
                                                              const uint32_t *__restrict__ ckpt, uint32_t *status,
                                                              int64_t out_delta) {
-  __shared__ uint32_t lut[kLutEntries];
-  __shared__ uint32_t s_base[kRowSlots];
+  __shared__ __attribute__((aligned(16))) uint32_t lds[kRowSlots + kLutEntries];  // as in awq_decode_kernel
+  uint32_t *s_base = lds, *lut = lds + kRowSlots;
 #if MPS_TRACE_ITEMS
   const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
 #endif
