@@ -210,7 +210,12 @@ int mps_awq_decode(const mps_awq_tensor *tensor, int64_t max_len, void *stream);
  * descriptors into one device allocation the plan owns (with its own status
  * word, mps_awq_plan_read_status); the pointed-to tensors must stay alive
  * while the plan is used, and a tensor whose bucket metadata is rewritten
- * needs a new plan. Decodes are asynchronous on `stream`.
+ * needs a new plan. Decodes are asynchronous on `stream`. A launch runs one
+ * workgroup per CU that takes the plan's work records from a queue in the
+ * plan's memory; the plan holds 32 such queues and gives each stream that
+ * launches it its own (a 33rd stream is refused with MPS_ERR_RUNTIME), so
+ * launches on different streams may overlap. A graph replays with the queue
+ * of the stream it was captured on.
  * No counterpart in the reference, which launches once per tensor
  * (kernel/decode_huffman.cu:857, :998). */
 typedef struct mps_awq_plan mps_awq_plan;

@@ -405,8 +405,10 @@ class AwqDecodePlan:
 
     ``items``: (int4_u8 [n, m] uint8, sidecar dict as the AWQ builders return it,
     out contiguous bfloat16 of n*m elements), all on one device. The reference
-    launches once per tensor (decode_huffman.cu:857, :998); a plan launches one
-    workgroup per bucket of every tensor, largest buckets first. The plan keeps
+    launches once per tensor (decode_huffman.cu:857, :998); a plan's launch runs
+    one workgroup per CU, which take the plan's work records (buckets, runs of
+    buckets, row ranges) from a queue, largest first. Launches on different
+    streams may overlap: each stream gets a queue of its own. The plan keeps
     references to every tensor it points at.
     """
 

@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 #include <new>
 #include <type_traits>
 #include <utility>
@@ -530,7 +531,10 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     wqb += f ? 128u : 0u;
     rcnt -= f ? 1u : 0u;
   };
-  auto reserve = [&]() {
+  // The first request (is_first) runs up to the next 16 RB-byte boundary of the
+  // bitstream; every later one is RB whole blocks from that boundary on.
+  auto reserve = [&](auto is_first) {
+    constexpr bool kFirst = decltype(is_first)::value;
     const bool land = ifl && rcnt == 0u;
     if (land) {
 #pragma unroll
@@ -540,12 +544,12 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     ifl = ifl && !land;
     const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
     const uint32_t off = (rqb >> 3) - 8u;
-    const uint32_t nreq = (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4;
+    const uint32_t nreq = kFirst ? (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4 : (uint32_t)RB;
     if (req) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-            r_bs, (uint32_t)i < nreq ? off + 16u * (uint32_t)i : kSlabBsPast, 0, 0);
+            r_bs, (!kFirst || (uint32_t)i < nreq) ? off + 16u * (uint32_t)i : kSlabBsPast, 0, 0);
         inb[i] = make_uint4(v[0], v[1], v[2], v[3]);
       }
       ninb = nreq;
@@ -553,9 +557,9 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     ifl = ifl || req;
     rqb += req ? nreq << 7 : 0u;
   };
-  // every second step: a 16-byte feed covers the 2 x 44 bits two steps can take
+  // after every second step: a 16-byte feed covers the 2 x 44 bits two steps can take
   auto bitstream_step = [&]() {
-    reserve();
+    reserve(std::false_type{});
     feed();
   };
 
@@ -713,6 +717,7 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   uint32_t Fr[DF], SOr[DF];
 #pragma unroll
   for (int u = 0; u < DF; ++u) SOr[u] = load_step(Fr[u]);
+  reserve(std::true_type{});  // the first request (nothing to feed yet)
   // Wave priorities, as in the FP8 slab decode: the issue arbiter favours the
   // oldest ready wave, so a wave lowers its priority by one level per quarter
   // of its steps, counted from a head start that grows with its age.
@@ -743,10 +748,10 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     }
 #pragma unroll
     for (int u = 0; u < DF; ++u) {
-      if (u % FE == 0) bitstream_step();
       const uint32_t F = Fr[u], so = SOr[u];
       SOr[u] = load_step(Fr[u]);  // the step DF ahead
       step(std::false_type{}, F, so);
+      if (u % FE == FE - 1) bitstream_step();
     }
   }
   if (MPS_AWQ_PRIO) __builtin_amdgcn_s_setprio(0);
@@ -754,9 +759,9 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
 #pragma unroll
   for (int u = 0; u < DF; ++u) {
     if (g + (uint32_t)u < gall) {
-      if (u % FE == 0) bitstream_step();
       if (g + (uint32_t)u < nfull) step(std::false_type{}, Fr[u], SOr[u]);
       else step(std::true_type{}, Fr[u], SOr[u]);
+      if (u % FE == FE - 1) bitstream_step();
     }
   }
   if (0u - np - 64u != pos_end) flag(status, MPS_STATUS_DESYNC);
@@ -1316,29 +1321,69 @@ constexpr int kAwqTraceRecs = 8192;
 __device__ uint64_t g_awq_trace[kAwqTraceRecs * 4];
 #endif
 
+// The plan kernel is persistent (one workgroup per CU) and takes its records
+// from a queue, as the FP8 plan kernel does: workgroup g starts with record g;
+// thread 0 takes a ticket t from queue[0] as its wave finishes a record, and
+// the workgroup's next record is gridDim.x + t. The records are sorted largest
+// first, so the CUs that drew small records take more of them, and no record
+// pays a workgroup launch. The last workgroup to leave (queue[1] counts them)
+// puts both words back to zero: launches of one queue must not overlap.
+__device__ __forceinline__ uint32_t queue_add(uint32_t *q, uint32_t v) {
+  return __hip_atomic_fetch_add((__attribute__((address_space(1))) uint32_t *)(q), v, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int kRanges>
 __global__ __launch_bounds__(kAwqBlock) void awq_decode_plan(const mps_awq_tensor *__restrict__ tensors,
-                                                             const AwqWork *__restrict__ work,
+                                                             const AwqWork *__restrict__ work, int64_t nwork,
                                                              const uint32_t *__restrict__ ckpt, uint32_t *status,
-                                                             int64_t out_delta) {
+                                                             int64_t out_delta, uint32_t *queue) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kRowSlots + kLutEntries];  // as in awq_decode_kernel
   uint32_t *s_base = lds, *lut = lds + kRowSlots;
+  if ((int64_t)blockIdx.x < nwork) {
+    int64_t r = blockIdx.x;
+    for (;;) {
 #if MPS_TRACE_ITEMS
-  const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
+      const uint64_t tr0 = __builtin_amdgcn_s_memrealtime();
 #endif
-  const AwqWork wk = work[blockIdx.x];
-  awq_plan_record<kRanges>(tensors, wk, ckpt, status, out_delta, lut, s_base);
+      const AwqWork wk = work[r];
+      awq_plan_record<kRanges>(tensors, wk, ckpt, status, out_delta, lut, s_base);
+      // The ticket is taken once wave 0 is through with the record, so the
+      // next record goes to a workgroup that is about to be free (taken at the
+      // record's start, a long record's successor would wait behind it); its
+      // round trip overlaps the other waves' last steps. Every wave is then
+      // done with the LDS (the record's queue, where the ticket goes), thread 0
+      // hands out the ticket, and every wave has read it before the next
+      // record's set-up writes the LDS.
+      uint32_t t = 0;
+      if (threadIdx.x == 0) t = queue_add(queue, 1u);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (threadIdx.x == 0) lds[0] = t;
+      __syncthreads();
+      const int64_t next = (int64_t)gridDim.x + (int64_t)lds[0];
+      __syncthreads();
 #if MPS_TRACE_ITEMS
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0 && blockIdx.x < kAwqTraceRecs) {
-    uint64_t *tp = g_awq_trace + (size_t)blockIdx.x * 4;
-    tp[0] = tr0;
-    tp[1] = __builtin_amdgcn_s_memrealtime();
-    tp[2] = ((uint64_t)(uint32_t)wk.kind << 32) | (uint32_t)wk.nsub;
-    tp[3] = (uint64_t)wk.elems;
+      if (threadIdx.x == 0 && r < kAwqTraceRecs) {
+        uint64_t *tp = g_awq_trace + (size_t)r * 4;
+        tp[0] = tr0;
+        tp[1] = __builtin_amdgcn_s_memrealtime();
+        tp[2] = ((uint64_t)(uint32_t)wk.kind << 32) | (uint32_t)wk.nsub;
+        tp[3] = (uint64_t)wk.elems;
+      }
+#endif
+      if (next >= nwork) break;
+      r = next;
+    }
   }
-#endif
+  if (threadIdx.x == 0) {
+    if (queue_add(queue + 1, 1u) == gridDim.x - 1) {
+      __hip_atomic_exchange((__attribute__((address_space(1))) uint32_t *)(queue), 0u, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_exchange((__attribute__((address_space(1))) uint32_t *)(queue + 1), 0u, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 int check_awq(const mps_awq_tensor *t) {
@@ -1369,9 +1414,19 @@ using namespace mps;
 
 // A plan owns one device allocation: its status word, the tensor descriptors,
 // the work records, and the split jobs and lane checkpoints of its row ranges.
+// Work queues of a plan: one per stream that launches it (two u32 words each,
+// 64 bytes apart), so that launches on different streams never share one.
+constexpr int kAwqPlanQueues = 32;
+constexpr size_t kAwqQueueStride = 64;
+
 struct mps_awq_plan {
   int device = 0;
   int64_t count = 0, nwork = 0;
+  // kAwqPlanQueues work queues (zero between launches); queue i serves
+  // streams[i], assigned at the stream's first launch
+  uint32_t *d_queue = nullptr;
+  std::mutex mu;
+  std::vector<void *> streams;
   uint16_t *first_out = nullptr;  // the first tensor's output at creation (decode_into moves from it)
   void *d_block = nullptr;
   uint32_t *d_status = nullptr;
@@ -1665,9 +1720,10 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   plan->count = count;
   plan->nwork = (int64_t)items.size();
   plan->first_out = count > 0 ? tensors[0].out : nullptr;
-  // status word (zero) | descriptors | work records | split jobs | checkpoints | job failure flags
+  // status word (zero) | work queues (zero) | descriptors | work records | split jobs | checkpoints | job failure flags
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  const size_t o_tensors = 256;
+  const size_t o_queues = 256;
+  const size_t o_tensors = o_queues + up(kAwqQueueStride * kAwqPlanQueues);
   const size_t o_work = o_tensors + up(sizeof(mps_awq_tensor) * (size_t)count);
   const size_t o_jobs = o_work + up(sizeof(AwqWork) * items.size());
   const size_t o_ckpt = o_jobs + up(sizeof(AwqSplitJob) * jobs.size());
@@ -1680,6 +1736,7 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
   if (e == hipSuccess) {
     char *blk = static_cast<char *>(plan->d_block);
     plan->d_status = reinterpret_cast<uint32_t *>(blk);
+    plan->d_queue = reinterpret_cast<uint32_t *>(blk + o_queues);
     plan->d_tensors = reinterpret_cast<mps_awq_tensor *>(blk + o_tensors);
     plan->d_work = reinterpret_cast<AwqWork *>(blk + o_work);
     plan->d_ckpt = reinterpret_cast<uint32_t *>(blk + o_ckpt);
@@ -1715,9 +1772,27 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
 
 static int awq_plan_launch(mps_awq_plan *plan, int64_t out_delta, uint32_t *status, void *stream) {
   if (plan->nwork == 0) return MPS_OK;
+  // The stream's work queue: the one it was given at its first launch, or the
+  // next free one. A launch leaves its queue as it found it, so launches on
+  // one stream share one; a graph captured on a stream replays with its queue.
+  uint32_t *queue = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(plan->mu);
+    size_t i = 0;
+    while (i < plan->streams.size() && plan->streams[i] != stream) ++i;
+    if (i == plan->streams.size()) {
+      if (i >= (size_t)kAwqPlanQueues)
+        return fail(MPS_ERR_RUNTIME, "an AWQ decode plan serves at most %d streams", kAwqPlanQueues);
+      plan->streams.push_back(stream);
+    }
+    queue = plan->d_queue + i * (kAwqQueueStride / sizeof(uint32_t));
+  }
+  int cus = 0;
+  MPS_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, plan->device));
+  const unsigned grid = (unsigned)std::min<int64_t>(plan->nwork, std::max(cus, 1));
   auto launch = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, dim3((unsigned)plan->nwork), dim3(kAwqBlock), 0, reinterpret_cast<hipStream_t>(stream),
-                       plan->d_tensors, plan->d_work, plan->d_ckpt, status, out_delta);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kAwqBlock), 0, reinterpret_cast<hipStream_t>(stream), plan->d_tensors,
+                       plan->d_work, plan->nwork, plan->d_ckpt, status, out_delta, queue);
   };
   switch (plan->ranges_mode) {
     case 0: launch(awq_decode_plan<0>); break;

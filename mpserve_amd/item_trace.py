@@ -193,9 +193,18 @@ def awq_trace(lib_path: str, k: int) -> Dict:
             d = dur[kind == kv]
             by_kind[kinds.get(int(kv), str(kv))] = {"records": int(d.size), "mean_us": round(float(d.mean()), 1),
                                                     "max_us": round(float(d.max()), 1)}
+        span = float((a[:, 1].max() - t0) / 100.0)
+        ends = np.sort((a[:, 1] - t0) / 100.0)
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
         result["layouts"][layout] = {"records_traced": int(len(a)),
-                                     "span_us": round(float((a[:, 1].max() - t0) / 100.0), 1),
+                                     "span_us": round(span, 1),
                                      "record_us_mean": round(float(statistics.mean(dur.tolist())), 1),
+                                     # records' time over the CUs' (one workgroup per CU)
+                                     "busy_fraction": round(float(dur.sum()) / (span * cus), 3),
+                                     "last_start_us": round(float((a[:, 0].max() - t0) / 100.0), 1),
+                                     # when the last CUs' records end: the CUs-th latest end and the median of those
+                                     "ends_us": {"cus_th_latest": round(float(ends[-min(cus, len(ends))]), 1),
+                                                 "median_of_last_cus": round(float(np.median(ends[-cus:])), 1)},
                                      "by_kind": by_kind}
     return result
 

@@ -3,6 +3,8 @@ bit for bit against the input (and the oracle's decode), through MPServe_cuda.
 
 Integer work: the bar is equality.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -574,3 +576,68 @@ def test_op_plan_cache_alternating_sidecars():
     assert read_status(torch.device(DEV)) == 0
     mc.clear_decode_plans()
     assert len(cache) == 0
+
+
+def test_plan_queue_every_record_on_every_launch_replay_and_two_streams():
+    """An AWQ plan's workgroups take their records from a work queue in the plan's
+    memory, which each launch's last workgroup resets. Every launch, every replay of
+    a graph that captured one, and two launches of the plan on two streams at once
+    (each stream with its own queue) decode every record."""
+    from mpserve_amd import _native
+
+    print("[awq] plan queue: launches, graph replays, two streams", flush=True)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    shapes = [(4096, 4096, 1024), (4096, 4096, 1024), (1024, 4096, 256), (4096, 4096, 256)]
+    srcs, descs, sizes = [], [], []
+    for j, (n, m, k) in enumerate(shapes):
+        w = make_awq_weight(n, m, 128, seed=720 + j, device=DEV)
+        sc = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, k, 1024, True)
+        srcs.append(w)
+        descs.append(sc)
+        sizes.append(n * m)
+    total = sum(sizes)
+    flat = [torch.empty(total, dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+    outs, off = [], 0
+    for (n, m, _), sz in zip(shapes, sizes):
+        outs.append(flat[0][off:off + sz].view(n, m))
+        off += sz
+    plan = awq.AwqDecodePlan([(w.int4_u8, sc, o) for w, sc, o in zip(srcs, descs, outs)])
+    assert plan.info()["work_items"] > 2 * cus
+
+    def check(buf, tag):
+        torch.cuda.synchronize()
+        o = 0
+        for j, (w, sz) in enumerate(zip(srcs, sizes)):
+            assert torch.equal(buf[o:o + sz].view(torch.uint16), w.bf16.view(torch.uint16).reshape(-1)), \
+                f"{tag}: tensor {j}"
+            o += sz
+
+    plan.read_status()
+    for rep in range(3):
+        flat[0].fill_(float("nan"))
+        plan.decode()
+        check(flat[0], f"launch {rep}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.decode()
+    for rep in range(3):
+        flat[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        check(flat[0], f"replay {rep}")
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rnd in range(3):
+        for f in flat:
+            f.fill_(float("nan"))
+        for st in streams:
+            st.wait_stream(torch.cuda.current_stream())
+        for f, st in zip(flat, streams):
+            _native.check(_native.lib().mps_awq_plan_decode_into(plan._plan, ctypes.c_void_p(f.data_ptr()),
+                                                                 ctypes.c_void_p(st.cuda_stream)))
+        for st in streams:
+            torch.cuda.current_stream().wait_stream(st)
+        for s_i, f in enumerate(flat):
+            check(f, f"round {rnd}, stream {s_i}")
+    assert plan.read_status() == 0
+    assert read_status(torch.device(DEV)) == 0
+    plan.close()
