@@ -362,7 +362,8 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
 //          r and ends at row r + 1 of ckpt ([ranges + 1][k]).
 struct AwqWork {
   int32_t tensor, bucket, nsub, kind;
-  int32_t range, range_rows, ranges, pad;
+  int32_t range, range_rows, ranges;
+  int32_t tiny;  // kind 0: 1 when every bucket codes at most one element a lane (awq_tiny_lane)
   int64_t ckpt;
   int64_t elems;  // (the plan's ordering key)
 };
@@ -1194,9 +1195,52 @@ __global__ __launch_bounds__(kAwqBlock) void awq_checkpoints(const mps_awq_tenso
 // out_delta: elements every tensor's output moves by (a plan decoding into a
 // buffer laid out like, but other than, the one it was created with).
 // kRanges: bit 0, the plan has row ranges (kind 2 records); bit 1, row ranges
-// side by side (kind 3). Plans without them launch the instantiation that
-// leaves that path out: the range path's code in the same kernel measured 4.6%
-// slower on a by-scale layer.
+// side by side (kind 3); bit 2, tiny buckets (awq_tiny_lane). Plans without
+// them launch the instantiation that leaves that path out: the range path's
+// code in the same kernel measured 4.6% slower on a by-scale layer, the tiny
+// path's 4.4% slower on a row-bucket layer.
+// A bucket with no more elements than substreams codes one element a lane
+// (k_eff = its element count), so staging its 16 tables in LDS (128 KiB) costs
+// far more than its decode: each lane looks its one code up in the global
+// tables instead (decode_huffman.cu:417-468 for one element: the peek, the
+// length nibble, ESC with its 16 raw bits), and checks that the code ends
+// where the next lane's begins.
+__device__ __forceinline__ void awq_tiny_lane(const mps_awq_tensor &T, int64_t b, int32_t ra, int32_t c0, int32_t cl,
+                                              int32_t k, int lane, uint32_t *status) {
+  const uint32_t *__restrict__ sb = T.bucket_thread_startbit + b * ((int64_t)k + 1);
+  const uint64_t pos0 = (uint64_t)T.bucket_bit_base[b] + gload(sb + lane);
+  const uint64_t pos_end = (uint64_t)T.bucket_bit_base[b] + gload(sb + lane + 1);
+  const bool empty = T.bitstream_words <= 0;
+  const uint32_t *__restrict__ bs32 = empty ? g_awq_zero_chunks : reinterpret_cast<const uint32_t *>(T.bitstream);
+  const uint64_t nchunks = empty ? 2u : (uint64_t)T.bitstream_words * 2u;
+  const uint64_t cb = pos0 >> 5;
+  // 64 bits from the code's first chunk: the code and an ESC payload (27 bits) fit after any skip < 32
+  const uint64_t buf = (((uint64_t)chunk_at(bs32, nchunks, cb) << 32) | chunk_at(bs32, nchunks, cb + 1))
+                       << (pos0 & 31u);
+  const int32_t rr = lane / cl, cc = lane - rr * cl;
+  const int64_t row = gload(T.row_indices + ra + rr);
+  const int64_t col = T.group_col_start ? (int64_t)gload(T.group_col_start + ra + rr) : (int64_t)c0;
+  const bool ok = row >= 0 && row < T.n && col >= 0 && col + cl <= T.m;
+  if (!ok) flag(status, MPS_STATUS_BAD_ROW);
+  const uint32_t idx = ok ? (uint32_t)(row * T.m + col) + (uint32_t)cc : 0u;
+  const uint32_t q = ok ? (uint32_t)gload(T.int4 + idx) & 15u : 0u;
+  const int32_t gid = gload(T.bucket_table + b * 16 + q);
+  const uint32_t peek = (uint32_t)(buf >> (64 - kAwqL));
+  uint32_t nib = 15u, sym = 0u;
+  if (gid >= 0 && gid < T.num_tables) {  // a missing table decodes as ESC, as the reference's kernel does
+    const uint32_t ln = gload(T.decode_lens + (size_t)gid * kAwqPacked + (peek >> 1));
+    nib = (peek & 1u) ? (ln >> 4) & 15u : ln & 15u;
+    sym = gload(T.decode_syms + (size_t)gid * kAwqTable + peek);
+  }
+  uint32_t len = nib;
+  if (nib == 15u) {  // ESC: the code is L bits, then 16 raw bits (decode_huffman.cu:454-460)
+    sym = (uint32_t)((buf << kAwqL) >> 48);
+    len = kAwqL + 16u;
+  }
+  if (ok) *(__attribute__((address_space(1))) uint16_t *)(T.out + idx) = (uint16_t)sym;
+  if (pos0 + len != pos_end) flag(status, MPS_STATUS_DESYNC);
+}
+
 template <int kRanges>
 __device__ __forceinline__ void awq_plan_record(const mps_awq_tensor *__restrict__ tensors, const AwqWork &wk,
                                                 const uint32_t *__restrict__ ckpt, uint32_t *status,
@@ -1240,6 +1284,31 @@ __device__ __forceinline__ void awq_plan_record(const mps_awq_tensor *__restrict
   const int tid = threadIdx.x;
   const int sub = tid / per, lane = tid - sub * per;
   const int64_t b = (int64_t)w.y + (sub < nsub ? sub : 0);
+  if ((kRanges & 4) != 0 && wk.tiny) {
+    // Tiny buckets (the plan checked that each has no more elements than k):
+    // no tables in LDS, no barrier. Compiled only into the plans that have
+    // such records: the path costs the others registers.
+    if (tid == 0) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int32_t g = gload(T.bucket_table + (int64_t)w.y * 16 + q);
+        if (g < -1 || g >= T.num_tables) flag(status, MPS_STATUS_BAD_TABLE);
+      }
+    }
+    if (sub >= nsub) return;
+    const int32_t ra = T.bucket_row_offsets[b], rb = T.bucket_row_offsets[b + 1];
+    const bool by_scale = T.group_col_start != nullptr;
+    const int32_t c0 = by_scale ? 0 : T.bucket_col_start[b];
+    const int32_t cl = by_scale ? (int32_t)T.group_size : T.bucket_col_len[b];
+    if (rb <= ra) return;
+    if (cl <= 0 || ra < 0 || (int64_t)rb > T.num_row_indices || (!by_scale && (c0 < 0 || (int64_t)c0 + cl > T.m))) {
+      if (lane == 0) flag(status, MPS_STATUS_BAD_BUCKET);
+      return;
+    }
+    const int64_t total = (int64_t)(rb - ra) * cl;
+    if (lane < total && lane < (int)T.k) awq_tiny_lane(T, b, ra, c0, cl, (int32_t)T.k, lane, status);
+    return;
+  }
 
   // Tables of the record's first bucket, filled by all work-items (as awq_bucket<1>).
   {
@@ -1434,7 +1503,9 @@ struct mps_awq_plan {
   AwqWork *d_work = nullptr;
   uint32_t *d_ckpt = nullptr;  // lane checkpoints of the row buckets split into ranges
   int64_t splits = 0;          // row buckets split into ranges
-  int ranges_mode = 0;         // bit 0: some work record is a row range (kind 2); bit 1: ranges side by side (kind 3)
+  // bit 0: some work record is a row range (kind 2); bit 1: ranges side by side
+  // (kind 3); bit 2: tiny buckets (kind 0 with `tiny`)
+  int ranges_mode = 0;
 };
 
 extern "C" {
@@ -1622,15 +1693,20 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
         continue;
       }
       int64_t nsub = 1, elems = elems_of(b);
+      // Tiny: every bucket of the record codes at most one element a lane (k =
+      // 1024 only: with k 256 / 512 such buckets run in same-scale runs that
+      // share one table set-up, and the tiny path measured 2.9% slower there)
+      bool tiny = T.k == kAwqBlock && elems_of(b) <= T.k;
       if (rows_of(b) <= row_cap) {
         while (nsub < maxsub && b + nsub < B && rows_of(b + nsub) <= row_cap && !multi_ok(b + nsub) &&
                same_tables(b, b + nsub)) {
           elems += elems_of(b + nsub);
           total += elems_of(b + nsub);
+          tiny = tiny && elems_of(b + nsub) <= T.k;
           ++nsub;
         }
       }
-      base.push_back(AwqWork{(int32_t)i, (int32_t)b, (int32_t)nsub, 0, 0, 0, 1, 0, 0, elems});
+      base.push_back(AwqWork{(int32_t)i, (int32_t)b, (int32_t)nsub, 0, 0, 0, 1, tiny ? 1 : 0, 0, elems});
       rows_of_rec.push_back(0);
       p_of_rec.push_back(0);
       c0_of_rec.push_back(0);
@@ -1764,7 +1840,8 @@ int mps_awq_plan_create(const mps_awq_tensor *tensors, int64_t count, void *stre
     return hip_fail(e, "mps_awq_plan_create");
   }
   plan->splits = (int64_t)jobs.size();
-  plan->ranges_mode = (std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.kind == 2; }) ? 1 : 0) |
+  plan->ranges_mode = (std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.tiny != 0; }) ? 4 : 0) |
+                      (std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.kind == 2; }) ? 1 : 0) |
                       (std::any_of(items.begin(), items.end(), [](const AwqWork &w) { return w.kind == 3; }) ? 2 : 0);
   *plan_out = plan;
   return MPS_OK;
@@ -1798,7 +1875,11 @@ static int awq_plan_launch(mps_awq_plan *plan, int64_t out_delta, uint32_t *stat
     case 0: launch(awq_decode_plan<0>); break;
     case 1: launch(awq_decode_plan<1>); break;
     case 2: launch(awq_decode_plan<2>); break;
-    default: launch(awq_decode_plan<3>); break;
+    case 3: launch(awq_decode_plan<3>); break;
+    case 4: launch(awq_decode_plan<4>); break;
+    case 5: launch(awq_decode_plan<5>); break;
+    case 6: launch(awq_decode_plan<6>); break;
+    default: launch(awq_decode_plan<7>); break;
   }
   MPS_HIP_CHECK(hipGetLastError());
   return MPS_OK;

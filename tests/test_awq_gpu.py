@@ -641,3 +641,57 @@ def test_plan_queue_every_record_on_every_launch_replay_and_two_streams():
     assert plan.read_status() == 0
     assert read_status(torch.device(DEV)) == 0
     plan.close()
+
+
+@pytest.mark.parametrize("n,m,k,cap,by_scale,seed", [
+    (256, 1024, 1024, 3, True, 730),    # every bucket <= 3 groups: at most 384 elements for 1024 lanes
+    (512, 512, 1024, 2, True, 731),     # buckets of 1-2 groups; many tensors' worth of tiny records
+    (8, 96, 1024, 1024, False, 732),    # a row-bucket tensor of 768 elements
+])
+def test_plan_tiny_buckets_look_codes_up_in_the_global_tables(n, m, k, cap, by_scale, seed):
+    """Buckets with no more elements than lanes (k = 1024) code one element a lane:
+    the plan decodes them without staging their tables in LDS. Bit-exact to the
+    input, status clear; a group row out of range in one tiny bucket is flagged,
+    nothing is written outside the output, and every other element decodes."""
+    from mpserve_amd._native import MPS_STATUS_BAD_ROW
+
+    print(f"[awq] tiny buckets n={n} m={m} k={k} cap={cap} by_scale={by_scale}", flush=True)
+    w = make_awq_weight(n, m, 128 if by_scale else None, seed=seed, device=DEV)
+    sc, st = awq.build_awq_sidecar(w.bf16, w.int4_u8, w.scale_u16, 11, k, cap, by_scale, with_stats=True)
+    assert st["esc_collisions"] == 0
+    offs = (sc["bucket_group_offsets_i32"] if by_scale else sc["bucket_row_offsets_i32"]).cpu().numpy().astype(np.int64)
+    cols = 128 if by_scale else sc["bucket_col_len_i32"].cpu().numpy().astype(np.int64)
+    elems = np.diff(offs) * cols
+    assert (elems <= k).mean() > 0.5, "the case should be mostly tiny buckets"
+    out = torch.empty((n, m), dtype=torch.bfloat16, device=DEV)
+    plan = awq.AwqDecodePlan([(w.int4_u8, sc, out)])
+    plan.read_status()
+    for _ in range(2):
+        out.fill_(float("nan"))
+        plan.decode()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.uint16), w.bf16.view(torch.uint16))
+    assert plan.read_status() == 0
+    plan.close()
+    if not by_scale:
+        return
+    # a group row out of range in the first tiny bucket with two or more groups
+    b = int(next(i for i in range(len(elems)) if elems[i] <= k and offs[i + 1] - offs[i] >= 2))
+    bad = dict(sc)
+    rows = sc["group_rows_i32"].clone()
+    rows[int(offs[b]) + 1] = n + 77
+    bad["group_rows_i32"] = rows
+    guard = 4096
+    buf = torch.zeros(n * m + 2 * guard, dtype=torch.bfloat16, device=DEV)
+    out = buf[guard:guard + n * m].view(n, m)
+    plan = awq.AwqDecodePlan([(w.int4_u8, bad, out)])
+    plan.read_status()
+    plan.decode()
+    torch.cuda.synchronize()
+    assert plan.read_status() & MPS_STATUS_BAD_ROW
+    assert bool((buf[:guard] == 0).all()) and bool((buf[guard + n * m:] == 0).all())
+    keep = torch.ones((n, m), dtype=torch.bool, device=DEV)
+    r, c = int(sc["group_rows_i32"][int(offs[b]) + 1]), int(sc["group_col_start_i32"][int(offs[b]) + 1])
+    keep[r, c:c + 128] = False
+    assert torch.equal(out.view(torch.int16)[keep], w.bf16.view(torch.int16)[keep])
+    plan.close()
