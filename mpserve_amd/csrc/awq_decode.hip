@@ -351,9 +351,11 @@ __global__ __launch_bounds__(kAwqBlock) void awq_decode_kernel(mps_awq_tensor T,
 // 4 flags it and the running shift steps over the raw bits; a step holding an
 // ESC code is decoded again code by code, reading the raw symbol.
 // ---------------------------------------------------------------------------
-// A plan's work record: one record per workgroup.
-//  kind 0: buckets bucket .. bucket + nsub - 1 on the per-lane path (one scale, shared tables);
-//  kind 1: one slab-path bucket;
+// A plan's work record (a workgroup decodes one at a time, taking them from
+// the plan's queue: awq_decode_plan).
+//  kind 0: buckets bucket .. bucket + nsub - 1 on the per-lane path (one scale, shared tables;
+//          with `tiny`, buckets of one code a lane that look their codes up in the global tables);
+//  kind 1: slab-path buckets bucket .. bucket + nsub - 1 with identical table ids (a by-scale run);
 //  kind 2: rows [range * range_rows, +range_rows) of a slab-path row bucket split into
 //          `ranges` ranges, starting from the lane checkpoints at ckpt + (range - 1) * 1024
 //          and ending at ckpt + range * 1024 (the bucket's own start and end bits at its ends);
