@@ -93,12 +93,13 @@ class _AwqSidecar(ctypes.Structure):
 
 
 def build(force: bool = False) -> str:
-    """Compile liboracle.so with the committed Makefile."""
+    """Compile liboracle.so with the committed Makefile (``force``: always, even
+    when the library is newer than its sources)."""
     if force or not os.path.exists(_LIB_PATH) or any(
         os.path.getmtime(_LIB_PATH) < os.path.getmtime(os.path.join(_HERE, src))
         for src in ("fp8_huffman_oracle.c", "awq_huffman_oracle.c")
     ):
-        subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+        subprocess.run(["make", "-s", "-C", _HERE] + (["-B"] if force else []) + ["liboracle.so"], check=True)
     return _LIB_PATH
 
 
