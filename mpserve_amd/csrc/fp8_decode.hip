@@ -650,11 +650,12 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   };
 
   // Register reserve: up to RB 16-byte blocks that follow the queue's last
-  // chunk. Every fourth group, a lane whose reserve is down to one block
-  // requests the next RB * 16 bytes (loads from the same lines, so a 128-byte
-  // line is fetched about twice instead of once per 16 bytes); they land in
-  // the reserve four or more groups later, once it is empty. Every fourth
-  // group the reserve's front block moves into the queue if four slots are free.
+  // chunk. Every eighth group (MPS_SLAB_REQ_EVERY below), a lane whose reserve
+  // is down to one block requests the next RB * 16 bytes (loads from the same
+  // lines, so a 128-byte line is fetched about twice instead of once per 16
+  // bytes); they land in the reserve four or more groups later, once it is
+  // empty. Every fourth group the reserve's front block moves into the queue
+  // if four slots are free.
   uint4 rv[RB], inb[RB];
 #pragma unroll
   for (int i = 0; i < RB; ++i) rv[i] = inb[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -673,17 +674,33 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
     rcnt -= f ? 1u : 0u;
   };
   uint32_t ninb = 0;  // blocks of the request in flight
-  auto reserve = [&]() {
-    const bool land = ifl && rcnt == 0u;
-    if (land) {
+#ifndef MPS_SLAB_REQ_EVERY
+#define MPS_SLAB_REQ_EVERY 2
+#endif
+#ifndef MPS_SLAB_REQ_AT
+#define MPS_SLAB_REQ_AT 1
+#endif
+  // Requests are considered every MPS_SLAB_REQ_EVERY-th bitstream step, by
+  // lanes whose reserve is down to MPS_SLAB_REQ_AT blocks; landing and feeding
+  // run every step. Lanes reach the request point on different steps, so a
+  // request's four loads carry few active lanes; asking every other step
+  // gathers about twice as many into each load and halves their number.
+  static_assert(MPS_SLAB_REQ_EVERY >= 1 && (MPS_SLAB_REQ_EVERY & (MPS_SLAB_REQ_EVERY - 1)) == 0,
+                "a power of two");
+  uint32_t bstep = 0;  // bitstream steps taken (uniform)
+  auto land = [&]() {
+    const bool l = ifl && rcnt == 0u;
+    if (l) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) rv[i] = inb[i];
     }
-    rcnt = land ? ninb : rcnt;
-    ifl = ifl && !land;
+    rcnt = l ? ninb : rcnt;
+    ifl = ifl && !l;
+  };
+  auto reserve = [&]() {
     const uint32_t off = (rqb >> 3) - 8u;
     // no requests past the substream's end (biased end + the window's reach)
-    const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
+    const bool req = !ifl && rcnt <= (uint32_t)MPS_SLAB_REQ_AT && (int32_t)(rqb - (pos_end + 192u)) < 0;
     // blocks up to the next request boundary (the first request may be short)
     const uint32_t nreq = MPS_SLAB_ALIGN ? (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4 : (uint32_t)RB;
     if (req) {
@@ -700,7 +717,9 @@ __device__ __forceinline__ void decode_slab4(const mps_fp8_tensor &T, uint16_t *
   };
   // Once per four groups: one 16-byte feed covers the 4 x 28 bits they can consume.
   auto bitstream_step = [&]() {
-    reserve();
+    land();
+    if ((bstep & (MPS_SLAB_REQ_EVERY - 1)) == 0u) reserve();
+    bstep = uni(bstep + 1u);
     feed();
   };
 
