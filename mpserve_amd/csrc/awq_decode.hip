@@ -536,15 +536,17 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
   };
   // The first request (is_first) runs up to the next 16 RB-byte boundary of the
   // bitstream; every later one is RB whole blocks from that boundary on.
-  auto reserve = [&](auto is_first) {
-    constexpr bool kFirst = decltype(is_first)::value;
-    const bool land = ifl && rcnt == 0u;
-    if (land) {
+  auto land = [&]() {
+    const bool l = ifl && rcnt == 0u;
+    if (l) {
 #pragma unroll
       for (int i = 0; i < RB; ++i) rv[i] = inb[i];
     }
-    rcnt = land ? ninb : rcnt;
-    ifl = ifl && !land;
+    rcnt = l ? ninb : rcnt;
+    ifl = ifl && !l;
+  };
+  auto reserve = [&](auto is_first) {
+    constexpr bool kFirst = decltype(is_first)::value;
     const bool req = !ifl && rcnt <= 1u && (int32_t)(rqb - (pos_end + 192u)) < 0;
     const uint32_t off = (rqb >> 3) - 8u;
     const uint32_t nreq = kFirst ? (16u * RB - ((phase + off) & (16u * RB - 1u))) >> 4 : (uint32_t)RB;
@@ -560,9 +562,19 @@ __device__ __forceinline__ void awq_slab_decode(const mps_awq_tensor &T, const u
     ifl = ifl || req;
     rqb += req ? nreq << 7 : 0u;
   };
-  // after every second step: a 16-byte feed covers the 2 x 44 bits two steps can take
+  // after every second step: a 16-byte feed covers the 2 x 44 bits two steps can take.
+  // Requests are considered at every MPS_AWQ_REQ_EVERY-th of these: lanes reach
+  // the request point on different steps, so a request's loads carry few
+  // active lanes, and asking less often gathers more of them into each load.
+#ifndef MPS_AWQ_REQ_EVERY
+#define MPS_AWQ_REQ_EVERY 2
+#endif
+  static_assert(MPS_AWQ_REQ_EVERY >= 1 && (MPS_AWQ_REQ_EVERY & (MPS_AWQ_REQ_EVERY - 1)) == 0, "a power of two");
+  uint32_t bstep = 0;  // bitstream steps taken (uniform)
   auto bitstream_step = [&]() {
-    reserve(std::false_type{});
+    land();
+    if ((bstep & (MPS_AWQ_REQ_EVERY - 1)) == 0u) reserve(std::false_type{});
+    bstep = awq_uni(bstep + 1u);
     feed();
   };
 
