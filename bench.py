@@ -687,7 +687,11 @@ def vram_pretouch(dev, gib: int) -> None:
     if gib <= 0:
         return
     t0 = time.perf_counter()
-    buf = torch.empty(gib << 28, dtype=torch.int32, device=dev)
+    try:
+        buf = torch.empty(gib << 28, dtype=torch.int32, device=dev)
+    except torch.cuda.OutOfMemoryError:
+        log(f"VRAM pre-touch: {gib} GiB not available, skipped")
+        return
     buf.fill_(0)
     torch.cuda.synchronize()
     del buf
