@@ -675,28 +675,29 @@ def headline(entries, dev, args, build_s: float):
     return res, plan
 
 
-def vram_pretouch(dev, gib: int) -> None:
+def vram_pretouch(dev, gib: int) -> int:
     """Allocate, fill and free ``gib`` GiB of device memory, and return it to
     the driver. On a freshly assigned box, a process whose model sits on memory
     no earlier allocation used decodes at one level for its whole life (5.75 ms
     for the model); after this the same process measures 5.30-5.50 ms, as every
     later process on the box does without it. It runs before the inputs exist,
-    outside every timed region."""
+    outside every timed region. Returns the GiB it touched (0: skipped)."""
     import torch
 
     if gib <= 0:
-        return
+        return 0
     t0 = time.perf_counter()
     try:
         buf = torch.empty(gib << 28, dtype=torch.int32, device=dev)
     except torch.cuda.OutOfMemoryError:
         log(f"VRAM pre-touch: {gib} GiB not available, skipped")
-        return
+        return 0
     buf.fill_(0)
     torch.cuda.synchronize()
     del buf
     torch.cuda.empty_cache()
     log(f"VRAM pre-touch: {gib} GiB allocated, filled and freed ({time.perf_counter() - t0:.2f} s)")
+    return gib
 
 
 def copy_calibration(dev, mib: int) -> None:
@@ -930,7 +931,7 @@ def main(argv=None) -> int:
         return 2
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    vram_pretouch(dev, args.vram_pretouch_gib)
+    args.vram_pretouch_gib = vram_pretouch(dev, args.vram_pretouch_gib)
     if args.compare_libs:
         return compare_libs(args, dev)
     if args.workload == "all":
