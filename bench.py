@@ -67,8 +67,9 @@ def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
-    # A process's first launches run 5-8% slower than the rest; after them the
-    # launch time holds to about 0.1% at a level the buffers' placement sets.
+    # A new plan's first launch takes about twice the steady time and the next
+    # three up to 10% longer; from the fifth on the launch time holds to about
+    # 0.1% at a level the buffers' placement sets.
     p.add_argument("--warmup", type=int, default=300)
     p.add_argument("--workload", choices=("all", "model8b", "layer8b", "layer70b", "gemm8b", "awq8b"), default="all",
                    help="all: the headline (config 5) with configs 2, 3, 4 and the AWQ layer as sub-results; "
